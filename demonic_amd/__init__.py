@@ -1,0 +1,276 @@
+"""demonic_amd -- MI355X (gfx950) bf16 GEMV backend for demoniC's `@` operator.
+
+Python mirror of the C ABI in include/dmc_hip.h.  The functions keep the names
+and argument meaning of the reference's Metal backend (compiler/src/gpu.rs:
+400-474): `matmul_bf16_gpu` is dmc_matmul_bf16_gpu, `..._batched`,
+`..._batched_deferred` and `flush` likewise, plus the MI355X additions
+(transposed-RHS form, device regions, device-pointer GEMVs, events).
+
+Host-pointer calls take NumPy arrays: activations float32, weights uint16
+holding bf16 bit patterns, all C-contiguous.  Nothing here computes on the
+CPU; if libdmc_hip.so is missing, every call raises BackendMissing.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from ._lib import BackendMissing, HipError
+
+__all__ = [
+    "BackendMissing", "HipError", "available", "gemv_selected", "MIN_MACS",
+    "matmul_bf16_gpu", "matmul_bf16_gpu_t", "matmul_bf16_gpu_batched",
+    "matmul_bf16_gpu_batched_deferred", "flush", "DeviceBuffer", "gemv_cs", "gemv_rd",
+    "synchronize", "Event", "plan", "register_weight", "release_weights",
+    "resident_count", "resident_bytes", "device_info",
+]
+
+MIN_MACS = 1 << 17  # DMC_HIP_MIN_MACS in include/dmc_hip.h
+
+
+def _arr(a: np.ndarray, dtype, name: str) -> np.ndarray:
+    if not isinstance(a, np.ndarray):
+        raise TypeError(f"{name} must be a numpy array")
+    if a.dtype != dtype:
+        raise TypeError(f"{name} must be {np.dtype(dtype).name}, got {a.dtype}")
+    if not a.flags.c_contiguous:
+        raise ValueError(f"{name} must be C-contiguous")
+    return a
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data if a.size else 0
+
+
+def available() -> bool:
+    """True when a gfx950 device is usable (cf. blas_gemm_available, jit.rs:29359)."""
+    return bool(_lib.load().dmc_hip_available())
+
+
+def gemv_selected(hip_on: bool, deterministic_depth: int, m: int, k: int, n: int) -> bool:
+    """Route predicate, shaped like blas_gemm_selected (jit.rs:29346-29351)."""
+    return bool(_lib.load().dmc_hip_gemv_selected(int(hip_on), deterministic_depth, m, k, n))
+
+
+# Deferred outputs must stay alive until materialized; hold them here.
+_pending_refs: list[np.ndarray] = []
+
+
+def _dims2(x: np.ndarray) -> tuple[int, int]:
+    if x.ndim == 1:
+        return 1, x.shape[0]
+    if x.ndim == 2:
+        return x.shape
+    raise ValueError("activation must be rank 1 or 2")
+
+
+def matmul_bf16_gpu(x: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """out[m,n] = x[m,k] @ bf16(w[k,n]) -- dmc_matmul_bf16_gpu (gpu.rs:391-408)."""
+    x = _arr(x, np.float32, "x")
+    w = _arr(w, np.uint16, "w")
+    m, k = _dims2(x)
+    if w.ndim != 2 or w.shape[0] != k:
+        raise ValueError(f"shape mismatch: x {x.shape} @ w {w.shape}")
+    n = w.shape[1]
+    out = np.empty((m, n), np.float32)
+    _lib.load().dmc_matmul_bf16_gpu(_ptr(x), _ptr(w), _ptr(out), m, k, n)
+    _pending_refs.clear()
+    return out
+
+
+def matmul_bf16_gpu_t(x: np.ndarray, w_nk: np.ndarray) -> np.ndarray:
+    """out[m,n] = sum_k x[m,k] * bf16(w_nk[n,k]) -- `x @ W'` without the transpose."""
+    x = _arr(x, np.float32, "x")
+    w_nk = _arr(w_nk, np.uint16, "w_nk")
+    m, k = _dims2(x)
+    if w_nk.ndim != 2 or w_nk.shape[1] != k:
+        raise ValueError(f"shape mismatch: x {x.shape} @ w_nk' {w_nk.shape}")
+    n = w_nk.shape[0]
+    out = np.empty((m, n), np.float32)
+    _lib.load().dmc_matmul_bf16_gpu_t(_ptr(x), _ptr(w_nk), _ptr(out), m, k, n)
+    _pending_refs.clear()
+    return out
+
+
+def _check_batched(x, w, out, m, k, n, batch, ls, rs):
+    x = _arr(x, np.float32, "x")
+    w = _arr(w, np.uint16, "w")
+    out = _arr(out, np.float32, "out")
+    if min(m, k, n, batch, ls, rs) < 0:
+        raise ValueError("negative size or stride")
+    if batch and m and n:
+        if x.size < (batch - 1) * ls + m * k:
+            raise ValueError("x too small for batch/ls")
+        if w.size < (batch - 1) * rs + k * n:
+            raise ValueError("w too small for batch/rs")
+        if out.size < batch * m * n:
+            raise ValueError("out too small")
+    return x, w, out
+
+
+def matmul_bf16_gpu_batched(x, w, m, k, n, batch, ls, rs, out=None) -> np.ndarray:
+    """dmc_matmul_bf16_gpu_batched (gpu.rs:410-437): slice z reads x[z*ls:], w[z*rs:]."""
+    if out is None:
+        out = np.empty(batch * m * n, np.float32)
+    x, w, out = _check_batched(x, w, out, m, k, n, batch, ls, rs)
+    _lib.load().dmc_matmul_bf16_gpu_batched(_ptr(x), _ptr(w), _ptr(out), m, k, n, batch, ls, rs)
+    _pending_refs.clear()
+    return out
+
+
+def matmul_bf16_gpu_batched_deferred(x, w, out, m, k, n, batch, ls, rs) -> None:
+    """dmc_matmul_bf16_gpu_batched_deferred (gpu.rs:439-466): `out` is written by
+    the next synchronous call or flush(); it is kept alive until then."""
+    x, w, out = _check_batched(x, w, out, m, k, n, batch, ls, rs)
+    _lib.load().dmc_matmul_bf16_gpu_batched_deferred(
+        _ptr(x), _ptr(w), _ptr(out), m, k, n, batch, ls, rs)
+    _pending_refs.append(out)
+
+
+def flush() -> None:
+    """dmc_matmul_bf16_gpu_flush (gpu.rs:468-474)."""
+    _lib.load().dmc_matmul_bf16_gpu_flush()
+    _pending_refs.clear()
+
+
+# ---- device regions and device-pointer GEMVs -------------------------------------
+
+class DeviceBuffer:
+    """A hipMalloc-backed HBM region (dmc_hip_region_alloc)."""
+
+    def __init__(self, nbytes: int):
+        lib = _lib.load()
+        self.nbytes = int(nbytes)
+        self.addr = lib.dmc_hip_region_alloc(self.nbytes)
+        if not self.addr:
+            _lib.check(-3)
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        buf = cls(max(a.nbytes, 1))
+        buf.upload(a)
+        return buf
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        if offset + a.nbytes > self.nbytes:
+            raise ValueError("upload beyond region")
+        _lib.check(_lib.load().dmc_hip_upload(self.addr + offset, _ptr(a), a.nbytes))
+
+    def download(self, dtype, shape, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download beyond region")
+        _lib.check(_lib.load().dmc_hip_download(_ptr(out), self.addr + offset, out.nbytes))
+        return out
+
+    def copy_from(self, src: "DeviceBuffer", nbytes: int | None = None) -> None:
+        n = src.nbytes if nbytes is None else nbytes
+        if n > self.nbytes or n > src.nbytes:
+            raise ValueError("copy beyond region")
+        _lib.check(_lib.load().dmc_hip_copy_device(self.addr, src.addr, n))
+
+    def free(self) -> None:
+        if self.addr:
+            _lib.check(_lib.load().dmc_hip_region_free(self.addr))
+            self.addr = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
+
+
+def _addr(b) -> int:
+    return b.addr if isinstance(b, DeviceBuffer) else int(b)
+
+
+def gemv_cs(x, w, y, m: int, k: int, n: int, batch: int = 1, ls: int = 0, rs: int = 0) -> None:
+    """Enqueue y[z] = x[z] @ bf16(w[z]) on device regions (w [k,n] per slice)."""
+    _lib.check(_lib.load().dmc_hip_gemv_cs(_addr(x), _addr(w), _addr(y), m, k, n, batch, ls, rs))
+
+
+def gemv_rd(x, w, y, m: int, k: int, n: int) -> None:
+    """Enqueue y = x @ bf16(w)' on device regions (w [n,k], the row-dot layout)."""
+    _lib.check(_lib.load().dmc_hip_gemv_rd(_addr(x), _addr(w), _addr(y), m, k, n))
+
+
+def synchronize() -> None:
+    _lib.check(_lib.load().dmc_hip_synchronize())
+
+
+class Event:
+    """A HIP event recorded on the library stream."""
+
+    def __init__(self):
+        self.ev = _lib.load().dmc_hip_event_create()
+        if not self.ev:
+            _lib.check(-4)
+
+    def record(self) -> None:
+        _lib.check(_lib.load().dmc_hip_event_record(self.ev))
+
+    def synchronize(self) -> None:
+        _lib.check(_lib.load().dmc_hip_event_synchronize(self.ev))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = _lib.load().dmc_hip_event_elapsed_ms(self.ev, end.ev)
+        if ms < 0:
+            raise HipError(-4, "hipEventElapsedTime failed")
+        return ms
+
+    def __del__(self):
+        try:
+            if self.ev and _lib._lib is not None:
+                _lib._lib.dmc_hip_event_destroy(self.ev)
+        except Exception:
+            pass
+
+
+@dataclass
+class Plan:
+    vec: int
+    rows_or_rw: int
+    mt: int
+    grid_x: int
+    slices: int
+    workspace_bytes: int
+
+
+def plan(layout: str, m: int, k: int, n: int, batch: int = 1, rs: int = 0,
+         x_addr: int = 0, w_addr: int = 0) -> Plan:
+    """Launch plan for layout 'rd' or 'cs' (pure host computation)."""
+    out = (ctypes.c_int64 * 6)()
+    _lib.check(_lib.load().dmc_hip_plan(int(layout == "rd"), x_addr, w_addr, m, k, n, batch, rs, out))
+    return Plan(*[int(v) for v in out])
+
+
+def register_weight(w: np.ndarray) -> int:
+    """Make a host weight resident now; returns its device address."""
+    w = np.ascontiguousarray(w)
+    d = _lib.load().dmc_hip_register_weight(_ptr(w), w.nbytes)
+    if not d:
+        _lib.check(-3)
+    return d
+
+
+def release_weights() -> None:
+    _lib.check(_lib.load().dmc_hip_release_weights())
+
+
+def resident_count() -> int:
+    return int(_lib.load().dmc_hip_resident_count())
+
+
+def resident_bytes() -> int:
+    return int(_lib.load().dmc_hip_resident_bytes())
+
+
+def device_info() -> dict:
+    lib = _lib.load()
+    return {"arch": (lib.dmc_hip_device_arch() or b"").decode(), "cus": int(lib.dmc_hip_device_cus())}

@@ -1,0 +1,683 @@
+// dmc_hip_runtime.cpp -- host runtime and C ABI of libdmc_hip (include/dmc_hip.h).
+//
+// Plays the role of the reference's GpuCtx + gpu_run (compiler/src/gpu.rs:186-660)
+// on a discrete MI355X instead of unified Apple memory:
+//   * one HIP stream (default priority) carries every copy and launch, so all
+//     device-side ordering is stream order;
+//   * weights become resident in HBM on first sight, keyed by content (the
+//     decode loop hands the same bytes over at fresh arena addresses every step,
+//     gpu.rs:195-199), or ahead of time through dmc_hip_register_weight;
+//   * activations and outputs cross PCIe through pinned staging buffers; while
+//     deferred calls are pending each call takes its own slice of the staging
+//     buffers, and the next synchronous call or flush copies the pending
+//     outputs to their destinations (the deferred protocol of gpu.rs:439-474,
+//     with the overlap guard of gpu.rs:491-499);
+//   * no CPU arithmetic anywhere: a device failure is reported (int entries)
+//     or fatal (the void drop-in entries), never silently recomputed.
+#include "../../include/dmc_hip.h"
+#include "gemv_launch.h"
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+namespace {
+
+thread_local std::string t_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+[[noreturn]] void fatal(const char *where) {
+    fprintf(stderr, "dmc_hip: fatal: %s: %s\n", where, t_err.c_str());
+    fflush(stderr);
+    abort();
+}
+
+bool env_flag(const char *name) {
+    const char *v = getenv(name);
+    return v && *v && strcmp(v, "0") != 0;
+}
+
+// ---- content key for resident weights --------------------------------------
+//
+// Byte length plus 512 evenly spread 8-byte samples (and the last word and the
+// trailing bytes), each mixed with its index through the splitmix64 finalizer
+// into two independent 64-bit lanes.  ~500 scattered host reads per call, the
+// same order of cost as the reference's 256-sample fingerprint (gpu.rs:334-358).
+struct Key {
+    uint64_t a, b;
+    int64_t bytes;
+    bool operator==(const Key &o) const { return a == o.a && b == o.b && bytes == o.bytes; }
+};
+struct KeyHash {
+    size_t operator()(const Key &k) const { return (size_t)(k.a ^ (k.b << 1)); }
+};
+
+inline uint64_t mix64(uint64_t z) {
+    z ^= z >> 30;
+    z *= 0xbf58476d1ce4e5b9ULL;
+    z ^= z >> 27;
+    z *= 0x94d049bb133111ebULL;
+    z ^= z >> 31;
+    return z;
+}
+
+Key content_key(const void *ptr, int64_t bytes) {
+    const unsigned char *p = static_cast<const unsigned char *>(ptr);
+    uint64_t a = mix64((uint64_t)bytes ^ 0x6a09e667f3bcc908ULL);
+    uint64_t b = mix64((uint64_t)bytes + 0xbb67ae8584caa73bULL);
+    const uint64_t words = (uint64_t)bytes / 8;
+    auto fold = [&](uint64_t idx, uint64_t v) {
+        a = mix64(a ^ v ^ (idx * 0x9e3779b97f4a7c15ULL));
+        b = (b ^ v) * 0x100000001b3ULL + idx + 1;
+    };
+    if (words > 0) {
+        const uint64_t S = words < 512 ? words : 512;
+        for (uint64_t i = 0; i < S; ++i) {
+            const uint64_t idx = i * words / S;
+            uint64_t v;
+            memcpy(&v, p + idx * 8, 8);
+            fold(idx, v);
+        }
+        uint64_t v;
+        memcpy(&v, p + (words - 1) * 8, 8);
+        fold(words - 1, v);
+    }
+    uint64_t tail = 0;
+    for (int64_t i = (int64_t)words * 8; i < bytes; ++i) tail = (tail << 8) | p[i];
+    fold(words, tail);
+    return Key{a, mix64(b), bytes};
+}
+
+// ---- context ----------------------------------------------------------------
+
+struct Buf {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+
+struct Pending {
+    const void *src;  // pinned staging
+    void *dst;        // caller's out
+    size_t bytes;
+};
+
+struct Stats {
+    uint64_t calls = 0, stage_ns = 0, key_ns = 0, upload_ns = 0, enqueue_ns = 0, wait_ns = 0,
+             readback_ns = 0, uploads = 0;
+};
+
+struct Ctx {
+    bool tried = false, ok = false;
+    int device = 0;
+    int cus = 0;
+    std::string arch;
+    hipStream_t stream = nullptr;
+    std::unordered_map<Key, void *, KeyHash> weights;
+    int64_t resident_bytes = 0;
+    Buf dx, dy, ws;         // device scratch (reuse is stream-ordered)
+    Buf hx, hy;             // pinned staging
+    size_t hx_off = 0, hy_off = 0;
+    std::vector<Pending> pending;
+    void *dummy = nullptr;  // non-null device address for zero-byte weights
+    bool timing = false;
+    Stats st;
+};
+
+std::mutex g_mu;
+Ctx &ctx() {
+    static Ctx *c = new Ctx;  // never destroyed: no HIP calls during exit
+    return *c;
+}
+
+const int kMaxResident = 2048;  // gpu.rs:266
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(e == hipErrorOutOfMemory ? DMC_HIP_ENOMEM : DMC_HIP_EDEVICE, "%s: %s (%d)", what,
+                hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(expr, what)                                   \
+    do {                                                      \
+        hipError_t e_ = (expr);                               \
+        if (e_ != hipSuccess) return hip_fail(e_, what);      \
+    } while (0)
+
+// Caller holds g_mu.  Returns DMC_HIP_OK when the device is usable.
+int ensure_init() {
+    Ctx &c = ctx();
+    if (c.tried) {
+        if (!c.ok) return DMC_HIP_ENODEV;
+        HIP_TRY(hipSetDevice(c.device), "hipSetDevice");
+        return DMC_HIP_OK;
+    }
+    c.tried = true;
+    if (env_flag("DMC_HIP_DISABLE")) return fail(DMC_HIP_ENODEV, "disabled by DMC_HIP_DISABLE");
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0)
+        return fail(DMC_HIP_ENODEV, "no HIP device");
+    const char *dv = getenv("DMC_HIP_DEVICE");
+    c.device = (dv && *dv) ? atoi(dv) : 0;
+    if (c.device < 0 || c.device >= count) return fail(DMC_HIP_ENODEV, "DMC_HIP_DEVICE out of range");
+    if (hipSetDevice(c.device) != hipSuccess) return fail(DMC_HIP_ENODEV, "hipSetDevice failed");
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, c.device) != hipSuccess)
+        return fail(DMC_HIP_ENODEV, "hipGetDeviceProperties failed");
+    c.arch = prop.gcnArchName;
+    const size_t colon = c.arch.find(':');
+    if (colon != std::string::npos) c.arch.resize(colon);
+    if (c.arch != "gfx950")
+        return fail(DMC_HIP_ENODEV, "device %d is %s; this library is built for gfx950 only",
+                    c.device, c.arch.c_str());
+    c.cus = prop.multiProcessorCount;
+    if (hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking) != hipSuccess)
+        return fail(DMC_HIP_ENODEV, "hipStreamCreate failed");
+    if (hipMalloc(&c.dummy, 256) != hipSuccess) return fail(DMC_HIP_ENODEV, "hipMalloc failed");
+    c.timing = env_flag("DMC_HIP_TIME");
+    c.ok = true;
+    return DMC_HIP_OK;
+}
+
+// Grow a device scratch buffer; in-flight work may still read the old one, so
+// drain the stream before freeing it.
+int ensure_dev(Buf &b, size_t need) {
+    if (need <= b.cap) return DMC_HIP_OK;
+    Ctx &c = ctx();
+    size_t cap = b.cap ? b.cap : (size_t)1 << 20;
+    while (cap < need) cap *= 2;
+    if (b.p) {
+        HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+        HIP_TRY(hipFree(b.p), "hipFree");
+        b.p = nullptr;
+        b.cap = 0;
+    }
+    HIP_TRY(hipMalloc(&b.p, cap), "hipMalloc(scratch)");
+    b.cap = cap;
+    return DMC_HIP_OK;
+}
+
+int flush_locked();
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Reserve `need` bytes of pinned staging at a 256-byte aligned bump offset.
+// The caller has already materialized pending work if the reservation does
+// not fit behind it (see run_host), so a full buffer here has nothing pending
+// in it and may restart at 0 or be replaced.
+int stage(Buf &b, size_t &off, size_t need, char **out) {
+    size_t at = align256(off);
+    if (at + need > b.cap) {
+        Ctx &c = ctx();
+        at = 0;
+        if (need > b.cap) {
+            HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+            if (b.p) HIP_TRY(hipHostFree(b.p), "hipHostFree");
+            b.p = nullptr;
+            b.cap = 0;
+            size_t cap = (size_t)1 << 20;
+            while (cap < need) cap *= 2;
+            HIP_TRY(hipHostMalloc(&b.p, cap, hipHostMallocDefault), "hipHostMalloc(staging)");
+            b.cap = cap;
+        }
+    }
+    *out = static_cast<char *>(b.p) + at;
+    off = at + need;
+    return DMC_HIP_OK;
+}
+
+int release_weights_locked() {
+    Ctx &c = ctx();
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    for (auto &kv : c.weights) HIP_TRY(hipFree(kv.second), "hipFree(weight)");
+    c.weights.clear();
+    c.resident_bytes = 0;
+    return DMC_HIP_OK;
+}
+
+// Device copy of the host weight [host, host+bytes), uploading on a miss.
+int resident(const void *host, int64_t bytes, void **dev) {
+    Ctx &c = ctx();
+    if (bytes <= 0) {
+        *dev = c.dummy;
+        return DMC_HIP_OK;
+    }
+    auto t0 = std::chrono::steady_clock::now();
+    const Key key = content_key(host, bytes);
+    auto t1 = std::chrono::steady_clock::now();
+    c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
+    auto it = c.weights.find(key);
+    if (it != c.weights.end()) {
+        *dev = it->second;
+        return DMC_HIP_OK;
+    }
+    if ((int)c.weights.size() >= kMaxResident) {
+        int rc = release_weights_locked();
+        if (rc) return rc;
+    }
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, (size_t)bytes);
+    if (e == hipErrorOutOfMemory) {  // make room once: drop every resident weight
+        (void)hipGetLastError();
+        int rc = release_weights_locked();
+        if (rc) return rc;
+        e = hipMalloc(&d, (size_t)bytes);
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(weight)");
+    e = hipMemcpyAsync(d, host, (size_t)bytes, hipMemcpyHostToDevice, c.stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
+    if (e != hipSuccess) {
+        (void)hipFree(d);
+        return hip_fail(e, "weight upload");
+    }
+    c.weights.emplace(key, d);
+    c.resident_bytes += bytes;
+    c.st.uploads++;
+    c.st.upload_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
+                          std::chrono::steady_clock::now() - t1)
+                          .count();
+    if (env_flag("DMC_HIP_DEBUG"))
+        fprintf(stderr, "[hip] upload #%zu %lld MB\n", c.weights.size(), (long long)(bytes >> 20));
+    *dev = d;
+    return DMC_HIP_OK;
+}
+
+int flush_locked() {
+    Ctx &c = ctx();
+    if (!c.tried || !c.ok) return DMC_HIP_OK;
+    if (!c.pending.empty()) {
+        HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+        for (const Pending &p : c.pending) memcpy(p.dst, p.src, p.bytes);
+        c.pending.clear();
+    }
+    c.hx_off = 0;
+    c.hy_off = 0;
+    return DMC_HIP_OK;
+}
+
+bool overlaps_pending(const void *p, size_t bytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(p);
+    for (const Pending &q : ctx().pending) {
+        const uintptr_t d0 = reinterpret_cast<uintptr_t>(q.dst);
+        if (a0 < d0 + q.bytes && d0 < a0 + bytes) return true;
+    }
+    return false;
+}
+
+int64_t ns_since(std::chrono::steady_clock::time_point t) {
+    return std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t)
+        .count();
+}
+
+void stats_line(int64_t k, int64_t n) {
+    Ctx &c = ctx();
+    Stats &s = c.st;
+    if (!c.timing) return;
+    // The lm-head GEMV (the only n >= 100k call) closes a decode step, the
+    // delimiter of the reference's DMC_GPU_TIME line (gpu.rs:681-683).
+    if (n < 100000 && s.calls % 1024 != 0) return;
+    fprintf(stderr,
+            "[hip] calls=%llu stage=%lluus key=%lluus upload=%lluus(%llu) enqueue=%lluus "
+            "wait=%lluus readback=%lluus (last k=%lld n=%lld)\n",
+            (unsigned long long)s.calls, (unsigned long long)(s.stage_ns / 1000),
+            (unsigned long long)(s.key_ns / 1000), (unsigned long long)(s.upload_ns / 1000),
+            (unsigned long long)s.uploads, (unsigned long long)(s.enqueue_ns / 1000),
+            (unsigned long long)(s.wait_ns / 1000), (unsigned long long)(s.readback_ns / 1000),
+            (long long)k, (long long)n);
+    s = Stats{};
+}
+
+bool valid_dims(int64_t m, int64_t k, int64_t n) {
+    return m >= 0 && k >= 0 && n >= 0 && m <= INT32_MAX && k <= INT32_MAX && n <= INT32_MAX;
+}
+
+// Shared host-pointer path of every drop-in entry.
+int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, int64_t k,
+             int64_t n, int64_t batch, int64_t ls, int64_t rs, bool defer) {
+    if (m < 0 || k < 0 || n < 0 || batch < 0 || ls < 0 || rs < 0)
+        return fail(DMC_HIP_EINVAL, "negative size or stride (m=%lld k=%lld n=%lld batch=%lld)",
+                    (long long)m, (long long)k, (long long)n, (long long)batch);
+    if (m == 0 || n == 0 || batch == 0) return DMC_HIP_OK;
+    if (!valid_dims(m, k, n)) return fail(DMC_HIP_EINVAL, "dimension beyond int32");
+    if (!out || (k > 0 && (!l || !r))) return fail(DMC_HIP_EINVAL, "null pointer");
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    const size_t x_bytes = (size_t)((batch - 1) * ls + m * k) * 4;
+    const size_t w_bytes = (size_t)((batch - 1) * rs + k * n) * 2;
+    const size_t y_bytes = (size_t)(batch * m * n) * 4;
+    if (!c.pending.empty() &&
+        (overlaps_pending(l, x_bytes) || overlaps_pending(r, w_bytes) || overlaps_pending(out, y_bytes))) {
+        rc = flush_locked();
+        if (rc) return rc;
+    }
+    // Deferred calls each keep their own staging slices until materialized.
+    // If this call's slices do not fit behind them, materialize them first.
+    if (!c.pending.empty() &&
+        (align256(c.hx_off) + x_bytes > c.hx.cap || align256(c.hy_off) + y_bytes > c.hy.cap)) {
+        rc = flush_locked();
+        if (rc) return rc;
+    }
+    auto t0 = std::chrono::steady_clock::now();
+    char *hx = nullptr, *hy = nullptr;
+    if ((rc = stage(c.hx, c.hx_off, x_bytes, &hx))) return rc;
+    if ((rc = stage(c.hy, c.hy_off, y_bytes, &hy))) return rc;
+    if (x_bytes) memcpy(hx, l, x_bytes);
+    if ((rc = ensure_dev(c.dx, x_bytes ? x_bytes : 4))) return rc;
+    if ((rc = ensure_dev(c.dy, y_bytes))) return rc;
+    if (x_bytes)
+        HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
+    c.st.stage_ns += ns_since(t0);
+
+    void *dw = nullptr;
+    if ((rc = resident(r, (int64_t)w_bytes, &dw))) return rc;
+
+    auto t1 = std::chrono::steady_clock::now();
+    hipError_t e;
+    if (rd) {
+        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
+                         static_cast<float *>(c.dy.p), n, m, k, n};
+        e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+    } else {
+        dmc::CsProblem p{static_cast<const uint16_t *>(dw), static_cast<const float *>(c.dx.p),
+                         static_cast<float *>(c.dy.p), m, k, n, batch, ls, rs};
+        const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
+        if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
+        e = dmc::launch_cs(p, pl, c.ws.p, c.stream);
+    }
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    HIP_TRY(hipMemcpyAsync(hy, c.dy.p, y_bytes, hipMemcpyDeviceToHost, c.stream), "y readback");
+    c.st.enqueue_ns += ns_since(t1);
+    c.st.calls++;
+    if (defer) {
+        c.pending.push_back(Pending{hy, out, y_bytes});
+        return DMC_HIP_OK;
+    }
+    auto t2 = std::chrono::steady_clock::now();
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    c.st.wait_ns += ns_since(t2);
+    auto t3 = std::chrono::steady_clock::now();
+    for (const Pending &p : c.pending) memcpy(p.dst, p.src, p.bytes);
+    c.pending.clear();
+    memcpy(out, hy, y_bytes);
+    c.hx_off = 0;
+    c.hy_off = 0;
+    c.st.readback_ns += ns_since(t3);
+    stats_line(k, n);
+    return DMC_HIP_OK;
+}
+
+void run_host_or_die(const char *entry, bool rd, int64_t l, int64_t r, int64_t out, int64_t m,
+                     int64_t k, int64_t n, int64_t batch, int64_t ls, int64_t rs, bool defer) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = run_host(rd, reinterpret_cast<const float *>(l), reinterpret_cast<const uint16_t *>(r),
+                      reinterpret_cast<float *>(out), m, k, n, batch, ls, rs, defer);
+    if (rc) fatal(entry);
+}
+
+}  // namespace
+
+// ---- drop-in surface ----------------------------------------------------------
+
+extern "C" {
+
+void dmc_matmul_bf16_gpu(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    run_host_or_die("dmc_matmul_bf16_gpu", false, l, r, out, m, k, n, 1, 0, 0, false);
+}
+
+void dmc_matmul_bf16_gpu_batched(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n,
+                                 int64_t batch, int64_t ls, int64_t rs) {
+    run_host_or_die("dmc_matmul_bf16_gpu_batched", false, l, r, out, m, k, n, batch, ls, rs, false);
+}
+
+void dmc_matmul_bf16_gpu_batched_deferred(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k,
+                                          int64_t n, int64_t batch, int64_t ls, int64_t rs) {
+    run_host_or_die("dmc_matmul_bf16_gpu_batched_deferred", false, l, r, out, m, k, n, batch, ls, rs,
+                    true);
+}
+
+void dmc_matmul_bf16_gpu_flush(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (flush_locked()) fatal("dmc_matmul_bf16_gpu_flush");
+}
+
+void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    run_host_or_die("dmc_matmul_bf16_gpu_t", true, l, r, out, m, k, n, 1, 0, 0, false);
+}
+
+// ---- additions ----------------------------------------------------------------
+
+int32_t dmc_hip_available(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ensure_init() == DMC_HIP_OK ? 1 : 0;
+}
+
+int32_t dmc_hip_gemv_selected(int32_t hip_on, int32_t deterministic_depth, int64_t m, int64_t k,
+                              int64_t n) {
+    if (!hip_on || deterministic_depth != 0) return 0;
+    if (m <= 0 || k <= 0 || n <= 0) return 0;
+    const __int128 macs = (__int128)m * k * n;
+    return macs >= (__int128)DMC_HIP_MIN_MACS ? 1 : 0;
+}
+
+const char *dmc_hip_last_error(void) { return t_err.c_str(); }
+
+int64_t dmc_hip_region_alloc(int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes <= 0) return fail(DMC_HIP_EINVAL, "region size must be positive"), 0;
+    if (ensure_init()) return 0;
+    void *d = nullptr;
+    hipError_t e = hipMalloc(&d, (size_t)bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(region)"), 0;
+    return reinterpret_cast<int64_t>(d);
+}
+
+int32_t dmc_hip_region_free(int64_t dptr) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!dptr) return DMC_HIP_OK;
+    HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    HIP_TRY(hipFree(reinterpret_cast<void *>(dptr)), "hipFree(region)");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_upload(int64_t dst_dev, int64_t src_host, int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes < 0 || (bytes > 0 && (!dst_dev || !src_host))) return fail(DMC_HIP_EINVAL, "bad upload");
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return DMC_HIP_OK;
+    Ctx &c = ctx();
+    HIP_TRY(hipMemcpyAsync(reinterpret_cast<void *>(dst_dev), reinterpret_cast<const void *>(src_host),
+                           (size_t)bytes, hipMemcpyHostToDevice, c.stream),
+            "upload");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_download(int64_t dst_host, int64_t src_dev, int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes < 0 || (bytes > 0 && (!dst_host || !src_dev))) return fail(DMC_HIP_EINVAL, "bad download");
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return DMC_HIP_OK;
+    Ctx &c = ctx();
+    HIP_TRY(hipMemcpyAsync(reinterpret_cast<void *>(dst_host), reinterpret_cast<const void *>(src_dev),
+                           (size_t)bytes, hipMemcpyDeviceToHost, c.stream),
+            "download");
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_copy_device(int64_t dst_dev, int64_t src_dev, int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes < 0 || (bytes > 0 && (!dst_dev || !src_dev))) return fail(DMC_HIP_EINVAL, "bad copy");
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!bytes) return DMC_HIP_OK;
+    HIP_TRY(hipMemcpyAsync(reinterpret_cast<void *>(dst_dev), reinterpret_cast<const void *>(src_dev),
+                           (size_t)bytes, hipMemcpyDeviceToDevice, ctx().stream),
+            "device copy");
+    return DMC_HIP_OK;
+}
+
+int64_t dmc_hip_register_weight(int64_t host_ptr, int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes <= 0 || !host_ptr) return fail(DMC_HIP_EINVAL, "bad weight range"), 0;
+    if (ensure_init()) return 0;
+    void *d = nullptr;
+    if (resident(reinterpret_cast<const void *>(host_ptr), bytes, &d)) return 0;
+    return reinterpret_cast<int64_t>(d);
+}
+
+int32_t dmc_hip_release_weights(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    Ctx &c = ctx();
+    if (!c.tried || !c.ok) return DMC_HIP_OK;
+    int rc = flush_locked();
+    if (rc) return rc;
+    return release_weights_locked();
+}
+
+int64_t dmc_hip_resident_count(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return (int64_t)ctx().weights.size();
+}
+
+int64_t dmc_hip_resident_bytes(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ctx().resident_bytes;
+}
+
+int32_t dmc_hip_gemv_cs(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n,
+                        int64_t batch, int64_t ls, int64_t rs) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!valid_dims(m, k, n) || batch < 0 || ls < 0 || rs < 0)
+        return fail(DMC_HIP_EINVAL, "bad GEMV shape");
+    if (m == 0 || n == 0 || batch == 0) return DMC_HIP_OK;
+    if (!y_dev || (k > 0 && (!x_dev || !w_dev))) return fail(DMC_HIP_EINVAL, "null pointer");
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_dev), reinterpret_cast<const float *>(x_dev),
+                     reinterpret_cast<float *>(y_dev), m, k, n, batch, ls, rs};
+    const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
+    if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
+    hipError_t e = dmc::launch_cs(p, pl, c.ws.p, c.stream);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!valid_dims(m, k, n)) return fail(DMC_HIP_EINVAL, "bad GEMV shape");
+    if (m == 0 || n == 0) return DMC_HIP_OK;
+    if (!y_dev || (k > 0 && (!x_dev || !w_dev))) return fail(DMC_HIP_EINVAL, "null pointer");
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_dev), k, reinterpret_cast<const float *>(x_dev),
+                     k, reinterpret_cast<float *>(y_dev), n, m, k, n};
+    hipError_t e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_synchronize(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_init();
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k, int64_t n,
+                     int64_t batch, int64_t rs, int64_t *out6) {
+    if (!out6 || !valid_dims(m, k, n) || batch < 0 || rs < 0) return fail(DMC_HIP_EINVAL, "bad plan query");
+    int cus;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        cus = ctx().ok ? ctx().cus : 256;
+    }
+    if (layout_rd) {
+        dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_addr), k, reinterpret_cast<const float *>(x_addr),
+                         k, nullptr, n, m, k, n};
+        const dmc::RdPlan pl = dmc::plan_rd(p, cus);
+        const int64_t v[6] = {pl.vec, pl.rows, pl.mt, pl.grid_x, 1, 0};
+        memcpy(out6, v, sizeof v);
+    } else {
+        dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_addr), reinterpret_cast<const float *>(x_addr),
+                         nullptr, m, k, n, batch, 0, rs};
+        const dmc::CsPlan pl = dmc::plan_cs(p, cus);
+        const int64_t v[6] = {pl.vec, pl.rw, pl.mt, pl.grid_x, pl.slices, (int64_t)pl.workspace_bytes};
+        memcpy(out6, v, sizeof v);
+    }
+    return DMC_HIP_OK;
+}
+
+int64_t dmc_hip_event_create(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (ensure_init()) return 0;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreate"), 0;
+    return reinterpret_cast<int64_t>(ev);
+}
+
+int32_t dmc_hip_event_record(int64_t ev) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_init();
+    if (rc) return rc;
+    if (!ev) return fail(DMC_HIP_EINVAL, "null event");
+    HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(ev), ctx().stream), "hipEventRecord");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_event_synchronize(int64_t ev) {
+    if (!ev) return fail(DMC_HIP_EINVAL, "null event");
+    HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(ev)), "hipEventSynchronize");
+    return DMC_HIP_OK;
+}
+
+float dmc_hip_event_elapsed_ms(int64_t start, int64_t stop) {
+    if (!start || !stop) return -1.0f;
+    float ms = -1.0f;
+    if (hipEventElapsedTime(&ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)) !=
+        hipSuccess)
+        return -1.0f;
+    return ms;
+}
+
+int32_t dmc_hip_event_destroy(int64_t ev) {
+    if (!ev) return DMC_HIP_OK;
+    HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(ev)), "hipEventDestroy");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_device_cus(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ensure_init() == DMC_HIP_OK ? ctx().cus : 0;
+}
+
+const char *dmc_hip_device_arch(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return ensure_init() == DMC_HIP_OK ? ctx().arch.c_str() : "";
+}
+
+}  // extern "C"

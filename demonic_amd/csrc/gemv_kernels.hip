@@ -1,0 +1,473 @@
+// gemv_kernels.hip -- hand-written gfx950 (CDNA4) bf16-weight x f32-vector GEMV.
+//
+// The hot path of demoniC's `@` with a bf16 weight: the reference computes it
+// on the CPU in dmc_matmul_bf16 (compiler/src/jit.rs:29481-29566) and on Apple
+// GPUs in gemv_bf16_vec4cb / gemv_bf16_tiled2d (compiler/src/gpu.rs:115-183).
+// These kernels are an MI355X design, not a translation of either:
+//
+//  * HBM-bound streaming.  Every weight byte is read exactly once per launch
+//    with wave-wide coalesced loads (128-bit per lane when the row alignment
+//    allows it; 64/32/16-bit variants cover K or N that are not multiples of
+//    8, e.g. K = 4097).  No weight byte is staged through LDS: there is no
+//    reuse to exploit, so LDS only carries the cross-wave reduction.
+//  * Wave64 split-K.  RD: the 4 waves of a workgroup interleave 64*VEC-element
+//    chunks of the same ROWS rows; each lane keeps one f32 accumulator per
+//    (activation row, weight row) and the partials meet in a wave butterfly
+//    and a fixed-order cross-wave sum.  CS: lanes own VEC adjacent columns,
+//    RW k-rows ride in one wave-wide load, waves interleave k rows, and k is
+//    split over workgroups whose partials a second pass sums in slice order.
+//  * Numerics.  w = bits << 16 (exact, NaN/inf/subnormal preserving), one
+//    fmaf per product, accumulators start at +0.0f (idle lanes at -0.0f, the
+//    additive identity), no flush-to-zero
+//    (compiled with -fno-gpu-flush-denormals-to-zero, no fast-math, no fp
+//    contraction), packed-fp32 disabled.  Fixed reduction order: bit-identical
+//    results run to run.
+#include "gemv_launch.h"
+
+#include <algorithm>
+
+namespace dmc {
+namespace {
+
+constexpr int kWaves = 4;  // waves per workgroup (256 threads)
+constexpr int kThreads = 64 * kWaves;
+
+// ---- bf16 vectors ---------------------------------------------------------
+
+// VEC bf16 values loaded by one lane; element e sits in bits [16e, 16e+16).
+template <int VEC> struct WVec;
+template <> struct WVec<8> {
+    uint32_t d[4];
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+    }
+};
+template <> struct WVec<4> {
+    uint32_t d[2];
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        d[0] = v.x; d[1] = v.y;
+    }
+};
+template <> struct WVec<2> {
+    uint32_t d[1];
+    __device__ __forceinline__ void load(const uint16_t *p) {
+        d[0] = *reinterpret_cast<const uint32_t *>(p);
+    }
+};
+template <> struct WVec<1> {
+    uint32_t d[1];
+    __device__ __forceinline__ void load(const uint16_t *p) { d[0] = *p; }
+};
+
+// Exact bf16 -> f32 widen of element e (compiler/src/jit.rs:29225-29227).
+template <int VEC>
+__device__ __forceinline__ float widen(const WVec<VEC> &v, int e) {
+    const uint32_t w = v.d[e >> 1];
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
+// VEC consecutive f32 activations (the caller guarantees 4*VEC-byte alignment).
+template <int VEC>
+__device__ __forceinline__ void load_x(const float *p, float (&v)[VEC]) {
+    if constexpr (VEC == 8) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        const float4 b = *reinterpret_cast<const float4 *>(p + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else if constexpr (VEC == 4) {
+        const float4 a = *reinterpret_cast<const float4 *>(p);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else if constexpr (VEC == 2) {
+        const float2 a = *reinterpret_cast<const float2 *>(p);
+        v[0] = a.x; v[1] = a.y;
+    } else {
+        v[0] = p[0];
+    }
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the same bits (the
+// xor butterfly is symmetric and IEEE addition is commutative).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ---- RD: W [N,K] ----------------------------------------------------------
+//
+// Workgroup (blockIdx.x, blockIdx.y) computes y[m0 .. m0+MT) x [n0 .. n0+ROWS).
+// K is cut into chunks of 64*VEC elements; chunk c belongs to wave c % 4 and
+// lane l reads elements [c*64*VEC + l*VEC, +VEC) of each of the ROWS rows.
+// Rows past N and activation rows past M are clamped to valid addresses and
+// their results discarded.
+template <int VEC, int ROWS, int MT>
+__global__ void __launch_bounds__(kThreads)
+gemv_rd_kernel(const uint16_t *__restrict__ W, int64_t ldw, const float *__restrict__ X,
+               int64_t ldx, float *__restrict__ Y, int64_t ldy, int N, int K, int M) {
+    constexpr int CH = 64 * VEC;
+    constexpr int U = (ROWS * MT <= 8) ? 2 : 1;  // chunks in flight per wave
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * ROWS;
+    const int m0 = blockIdx.y * MT;
+
+    const uint16_t *wrow[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+        wrow[r] = W + (int64_t)min(n0 + r, N - 1) * ldw + lane * VEC;
+    const float *xrow[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) xrow[m] = X + (int64_t)min(m0 + m, M - 1) * ldx + lane * VEC;
+
+    // A lane with at least one element starts its chain at +0.0f, like the
+    // reference (jit.rs:29655).  A lane with none starts at -0.0f, the exact
+    // additive identity, so idle lanes cannot turn a -0.0f result (a product
+    // that underflowed) into +0.0f in the reduction.  K == 0 writes +0.0f.
+    const float init = (wave * CH + lane * VEC < K || K == 0) ? 0.0f : -0.0f;
+    float acc[MT][ROWS];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) acc[m][r] = init;
+
+    auto consume = [&](const WVec<VEC> (&wv)[ROWS], int koff) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float xv[VEC];
+            load_x<VEC>(xrow[m] + koff, xv);
+#pragma unroll
+            for (int e = 0; e < VEC; ++e)
+#pragma unroll
+                for (int r = 0; r < ROWS; ++r) acc[m][r] = fmaf(xv[e], widen<VEC>(wv[r], e), acc[m][r]);
+        }
+    };
+
+    const int nfull = K / CH;
+    int c = wave;
+    for (; c + (U - 1) * kWaves < nfull; c += U * kWaves) {
+        WVec<VEC> wv[U][ROWS];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) wv[u][r].load(wrow[r] + (int64_t)(c + u * kWaves) * CH);
+#pragma unroll
+        for (int u = 0; u < U; ++u) consume(wv[u], (c + u * kWaves) * CH);
+    }
+    for (; c < nfull; c += kWaves) {
+        WVec<VEC> wv[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) wv[r].load(wrow[r] + (int64_t)c * CH);
+        consume(wv, c * CH);
+    }
+    // Partial last chunk: VEC divides K, so a lane's vector is wholly in or out.
+    if (nfull * CH < K && wave == nfull % kWaves && nfull * CH + lane * VEC < K) {
+        WVec<VEC> wv[ROWS];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) wv[r].load(wrow[r] + (int64_t)nfull * CH);
+        consume(wv, nfull * CH);
+    }
+
+    __shared__ float red[kWaves][MT * ROWS];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const float s = wave_sum(acc[m][r]);
+            if (lane == 0) red[wave][m * ROWS + r] = s;
+        }
+    __syncthreads();
+    for (int i = threadIdx.x; i < MT * ROWS; i += kThreads) {
+        const int m = i / ROWS, r = i % ROWS;
+        float s = red[0][i];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) s += red[w][i];
+        if (n0 + r < N && m0 + m < M) Y[(int64_t)(m0 + m) * ldy + n0 + r] = s;
+    }
+}
+
+// ---- CS: W [K,N] ----------------------------------------------------------
+//
+// Workgroup (bx, slice, z) computes partial sums of columns [bx*CB, +CB) over
+// k in [slice*kslice, +kslice) for batch slice z.  A wave-wide load covers RW
+// consecutive k rows x LPR lanes x VEC columns; lane (g, cl) takes k row
+// g of each group and columns cl*VEC .. +VEC.  Waves interleave row groups.
+// Columns past N are clamped to column 0 and discarded.
+template <int VEC, int RW, int MT>
+__global__ void __launch_bounds__(kThreads)
+gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restrict__ X, int64_t ls,
+               float *__restrict__ P, int64_t p_slice, int64_t p_z, int N, int K, int M, int kslice) {
+    constexpr int LPR = 64 / RW;
+    constexpr int CB = LPR * VEC;
+    constexpr int STEP = kWaves * RW;
+    constexpr int U = (MT <= 2) ? 4 : 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane / LPR;
+    const int cl = lane % LPR;
+    const int col = blockIdx.x * CB + cl * VEC;
+    const int slice = blockIdx.y;
+    const int64_t z = blockIdx.z;
+    const int kbeg = slice * kslice;
+    const int kend = min(K, kbeg + kslice);
+
+    const uint16_t *wz = W + z * rs + (col < N ? col : 0);
+    const float *xz = X + z * ls;
+    float *pz = P + (int64_t)slice * p_slice + z * p_z;
+
+    // +0.0f for a lane that owns k rows, -0.0f (the additive identity) for an
+    // idle one; see gemv_rd_kernel.
+    const float init = (kbeg + wave * RW + g < kend || K == 0) ? 0.0f : -0.0f;
+    float acc[MT][VEC];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[m][e] = init;
+
+    auto consume = [&](const WVec<VEC> &wv, int k) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float xv = xz[(int64_t)min(m, M - 1) * K + k];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[m][e] = fmaf(xv, widen<VEC>(wv, e), acc[m][e]);
+        }
+    };
+
+    int k = kbeg + wave * RW + g;
+    for (; k + (U - 1) * STEP < kend; k += U * STEP) {
+        WVec<VEC> wv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) wv[u].load(wz + (int64_t)(k + u * STEP) * N);
+#pragma unroll
+        for (int u = 0; u < U; ++u) consume(wv[u], k + u * STEP);
+    }
+    for (; k < kend; k += STEP) {
+        WVec<VEC> wv;
+        wv.load(wz + (int64_t)k * N);
+        consume(wv, k);
+    }
+
+    // Sum the RW row groups of the wave: lanes cl, cl+LPR, cl+2*LPR, ...
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+#pragma unroll
+            for (int o = LPR; o < 64; o <<= 1) acc[m][e] += __shfl_xor(acc[m][e], o, 64);
+
+    __shared__ float red[kWaves][MT][CB];
+    if (g == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) red[wave][m][cl * VEC + e] = acc[m][e];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < MT * CB; i += kThreads) {
+        const int m = i / CB, c = i % CB;
+        const int n = blockIdx.x * CB + c;
+        float s = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) s += red[w][m][c];
+        if (n < N && m < M) pz[(int64_t)m * N + n] = s;
+    }
+}
+
+// Second CS pass: y[i] = sum over slices in ascending order of P[s][i].
+__global__ void __launch_bounds__(kThreads)
+sum_slices_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
+                  int64_t count) {
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= count) return;
+    float s = P[i];
+    for (int j = 1; j < slices; ++j) s += P[(int64_t)j * p_slice + i];
+    Y[i] = s;
+}
+
+// ---- dispatch -------------------------------------------------------------
+
+int mt_for(int64_t m) {
+    if (m <= 1) return 1;
+    if (m <= 2) return 2;
+    if (m <= 4) return 4;
+    if (m <= 8) return 8;
+    return 16;
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int env_int(const char *name, int dflt) {
+    const char *v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+template <int VEC, int ROWS, int MT>
+hipError_t rd_go(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_rd_kernel<VEC, ROWS, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.grid_y),
+                       dim3(kThreads), 0, s, p.w, p.ldw, p.x, p.ldx, p.y, p.ldy, (int)p.n, (int)p.k,
+                       (int)p.m);
+    return hipGetLastError();
+}
+
+template <int VEC, int ROWS>
+hipError_t rd_mt(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    switch (pl.mt) {
+    case 1: return rd_go<VEC, ROWS, 1>(p, pl, s);
+    case 2: return rd_go<VEC, ROWS, 2>(p, pl, s);
+    case 4: return rd_go<VEC, ROWS, 4>(p, pl, s);
+    case 8: return rd_go<VEC, ROWS, 8>(p, pl, s);
+    case 16: return rd_go<VEC, ROWS, 16>(p, pl, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int VEC>
+hipError_t rd_rows(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    switch (pl.rows) {
+    case 1: return rd_mt<VEC, 1>(p, pl, s);
+    case 2: return rd_mt<VEC, 2>(p, pl, s);
+    case 4: return rd_mt<VEC, 4>(p, pl, s);
+    case 8: return rd_mt<VEC, 8>(p, pl, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// One launch: batch slices [z0, z0+nz), activation rows [m0, m0+mc).
+template <int VEC, int RW, int MT>
+hipError_t cs_go(const CsProblem &p, const CsPlan &pl, float *P, int64_t p_slice, int64_t z0,
+                 int64_t nz, int64_t m0, int64_t mc, hipStream_t s) {
+    const int64_t p_z = p.m * p.n;
+    hipLaunchKernelGGL((gemv_cs_kernel<VEC, RW, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.slices,
+                       (unsigned)nz), dim3(kThreads), 0, s, p.w + z0 * p.rs, p.rs,
+                       p.x + z0 * p.ls + m0 * p.k, p.ls, P + z0 * p_z + m0 * p.n, p_slice, p_z,
+                       (int)p.n, (int)p.k, (int)mc, (int)pl.kslice);
+    return hipGetLastError();
+}
+
+template <int VEC, int RW>
+hipError_t cs_mt(const CsProblem &p, const CsPlan &pl, float *P, int64_t ps, int64_t z0, int64_t nz,
+                 int64_t m0, int64_t mc, hipStream_t s) {
+    switch (pl.mt) {
+    case 1: return cs_go<VEC, RW, 1>(p, pl, P, ps, z0, nz, m0, mc, s);
+    case 2: return cs_go<VEC, RW, 2>(p, pl, P, ps, z0, nz, m0, mc, s);
+    case 4: return cs_go<VEC, RW, 4>(p, pl, P, ps, z0, nz, m0, mc, s);
+    case 8: return cs_go<VEC, RW, 8>(p, pl, P, ps, z0, nz, m0, mc, s);
+    case 16: return cs_go<VEC, RW, 16>(p, pl, P, ps, z0, nz, m0, mc, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t cs_dispatch(const CsProblem &p, const CsPlan &pl, float *P, int64_t ps, int64_t z0,
+                       int64_t nz, int64_t m0, int64_t mc, hipStream_t s) {
+    if (pl.vec == 8 && pl.rw == 4) return cs_mt<8, 4>(p, pl, P, ps, z0, nz, m0, mc, s);
+    if (pl.vec == 8 && pl.rw == 1) return cs_mt<8, 1>(p, pl, P, ps, z0, nz, m0, mc, s);
+    if (pl.vec == 4 && pl.rw == 1) return cs_mt<4, 1>(p, pl, P, ps, z0, nz, m0, mc, s);
+    if (pl.vec == 2 && pl.rw == 1) return cs_mt<2, 1>(p, pl, P, ps, z0, nz, m0, mc, s);
+    if (pl.vec == 1 && pl.rw == 1) return cs_mt<1, 1>(p, pl, P, ps, z0, nz, m0, mc, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+RdPlan plan_rd(const RdProblem &p, int num_cus) {
+    RdPlan pl{};
+    // Widest load the row alignment allows: every row start, every activation
+    // row start and the base pointers must be aligned to the vector size.
+    for (int v : {8, 4, 2, 1}) {
+        if (p.k % v == 0 && p.ldw % v == 0 && p.ldx % v == 0 && aligned(p.w, 2 * v) &&
+            aligned(p.x, 4 * v)) {
+            pl.vec = v;
+            break;
+        }
+    }
+    pl.mt = mt_for(p.m);
+    // Rows per workgroup: 4 keeps >= 4 workgroups per CU at the decode
+    // shapes (N = 4096 .. 128256) with 8 KiB of weight loads in flight per
+    // wave; skinny tiles trade rows for activation registers.
+    int rows = pl.mt == 1 ? 4 : (pl.mt <= 4 ? 2 : 1);
+    const int64_t min_groups = 2LL * (num_cus > 0 ? num_cus : 256);
+    while (rows > 1 && (p.n + rows - 1) / rows < min_groups) rows >>= 1;
+    rows = env_int("DMC_HIP_RD_ROWS", rows);
+    if (rows != 1 && rows != 2 && rows != 4 && rows != 8) rows = 4;
+    pl.rows = rows;
+    pl.grid_x = (p.n + rows - 1) / rows;
+    pl.grid_y = (p.m + pl.mt - 1) / pl.mt;
+    return pl;
+}
+
+CsPlan plan_cs(const CsProblem &p, int num_cus) {
+    CsPlan pl{};
+    for (int v : {8, 4, 2, 1}) {
+        if (p.n % v == 0 && (p.batch <= 1 || p.rs % v == 0) && aligned(p.w, 2 * v)) {
+            pl.vec = v;
+            break;
+        }
+    }
+    pl.rw = pl.vec == 8 ? 4 : 1;
+    const int rw = env_int("DMC_HIP_CS_RW", pl.rw);
+    if (pl.vec == 8 && (rw == 1 || rw == 4)) pl.rw = rw;
+    pl.mt = mt_for(p.m);
+    pl.cb = (64 / pl.rw) * pl.vec;
+    pl.grid_x = (p.n + pl.cb - 1) / pl.cb;
+    // Split k so the launch has ~8 workgroups per CU, with at least 64 k rows
+    // per workgroup (a multiple of the 4*RW rows one workgroup step covers).
+    const int64_t step = (int64_t)kWaves * pl.rw;
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    const int64_t groups = pl.grid_x * std::max<int64_t>(p.batch, 1);
+    int64_t want = (8 * cus + groups - 1) / groups;
+    const int64_t kmax = std::max<int64_t>(p.k, 1);
+    int64_t kslice = (kmax + want - 1) / want;
+    kslice = std::max<int64_t>(kslice, 64);
+    kslice = (kslice + step - 1) / step * step;
+    kslice = env_int("DMC_HIP_CS_KSLICE", (int)kslice);
+    if (kslice < step) kslice = step;
+    pl.kslice = kslice;
+    pl.slices = (kmax + kslice - 1) / kslice;
+    if (pl.slices > 65535) {  // grid.y limit
+        pl.slices = 65535;
+        pl.kslice = (kmax + pl.slices - 1) / pl.slices;
+        pl.kslice = (pl.kslice + step - 1) / step * step;
+        pl.slices = (kmax + pl.kslice - 1) / pl.kslice;
+    }
+    pl.workspace_bytes =
+        pl.slices > 1 ? (size_t)pl.slices * (size_t)std::max<int64_t>(p.batch, 1) * p.m * p.n * 4 : 0;
+    return pl;
+}
+
+hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    if (p.m <= 0 || p.n <= 0) return hipSuccess;
+    switch (pl.vec) {
+    case 8: return rd_rows<8>(p, pl, s);
+    case 4: return rd_rows<4>(p, pl, s);
+    case 2: return rd_rows<2>(p, pl, s);
+    case 1: return rd_rows<1>(p, pl, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipStream_t s) {
+    if (p.m <= 0 || p.n <= 0 || p.batch <= 0) return hipSuccess;
+    const int64_t per_z = p.m * p.n;
+    const int64_t total = per_z * p.batch;
+    float *P = pl.slices > 1 ? static_cast<float *>(workspace) : p.y;
+    const int64_t p_slice = pl.slices > 1 ? total : 0;
+    const int64_t zmax = 32768;  // grid.z limit, with margin
+    for (int64_t z0 = 0; z0 < p.batch; z0 += zmax) {
+        const int64_t nz = std::min(zmax, p.batch - z0);
+        for (int64_t m0 = 0; m0 < p.m; m0 += pl.mt) {
+            const int64_t mc = std::min<int64_t>(pl.mt, p.m - m0);
+            hipError_t e = cs_dispatch(p, pl, P, p_slice, z0, nz, m0, mc, s);
+            if (e != hipSuccess) return e;
+        }
+    }
+    if (pl.slices > 1) {
+        const int64_t blocks = (total + kThreads - 1) / kThreads;
+        hipLaunchKernelGGL(sum_slices_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, P, p_slice,
+                           (int)pl.slices, p.y, total);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+}  // namespace dmc

@@ -1,0 +1,149 @@
+/*
+ * dmc_hip.h -- C ABI of libdmc_hip, the MI355X (gfx950) bf16 GEMV backend for
+ * demoniC's `@` operator.
+ *
+ * The first block is the drop-in boundary: the exact operator surface of the
+ * reference's Metal backend (compiler/src/gpu.rs:400-474), bound by the JIT as
+ * `__dmc_matmul_bf16_gpu*` symbols (compiler/src/jit.rs:3064-3072) with SysV
+ * i64 signatures (jit.rs:5389-5445).  Pointers are host addresses passed as
+ * int64; the weight `r` is bf16 bit patterns (u16), `l` and `out` are f32;
+ * all row-major.  Each output is computed on the GPU as the reference's
+ * ascending-k fma chain (docs/SPEC.md:1149-1163) up to summation order: the
+ * result is tolerance-equal (normwise <= 1e-5), with NaN/+-inf classes and the
+ * sign of exact zeros preserved.  This route is a non-deterministic fast path
+ * in the sense of docs/SPEC.md:1165-1181: a JIT must never select it inside
+ * `@deterministic` (see dmc_hip_gemv_selected).
+ *
+ * Error behaviour.  The reference entries have no error channel and degrade
+ * to a CPU kernel when Metal is absent (gpu.rs:327-332, gpu.rs:483-486).  This
+ * library has no CPU arithmetic: a caller asks dmc_hip_available() first (as
+ * the reference asks blas_gemm_available(), jit.rs:29359) and keeps its own CPU
+ * kernel otherwise.  If a void entry point still meets a device error it
+ * prints "dmc_hip: fatal: ..." to stderr and aborts rather than return wrong
+ * data.  The int32-returning entries report errors instead (0 = success,
+ * negative = DMC_HIP_E*) with a message in dmc_hip_last_error().
+ *
+ * Threading.  One process-wide context (one device, one HIP stream) guarded by
+ * a mutex; calls from several threads serialize.  The reference keeps one
+ * context per thread for the same single-threaded decode loop (gpu.rs:186-189).
+ */
+#ifndef DMC_HIP_H
+#define DMC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DMC_HIP_OK 0
+#define DMC_HIP_ENODEV (-1)  /* no usable gfx950 device, or disabled       */
+#define DMC_HIP_EINVAL (-2)  /* bad argument (negative size, null pointer) */
+#define DMC_HIP_ENOMEM (-3)  /* device or pinned allocation failed          */
+#define DMC_HIP_EDEVICE (-4) /* a HIP runtime call failed                   */
+
+/* ---- drop-in operator surface (compiler/src/gpu.rs) --------------------- */
+
+/* Replaces dmc_matmul_bf16_gpu (gpu.rs:391-408), same ABI as the CPU kernel
+ * dmc_matmul_bf16 (jit.rs:29488): out[m,n] = l[m,k] @ bf16(r[k,n]).
+ * m == 0 or n == 0 returns without touching out (gpu.rs:402); k == 0 writes
+ * +0.0 (jit.rs:29655).  Any m runs on the GPU (the reference sends m != 1 to
+ * its CPU kernel, gpu.rs:404-407).  Synchronous: out is written on return,
+ * after every deferred call has been materialized. */
+void dmc_matmul_bf16_gpu(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+
+/* Replaces dmc_matmul_bf16_gpu_batched (gpu.rs:410-437): `batch` slices; slice
+ * z reads l + z*ls f32 ([m,k]), r + z*rs u16 ([k,n]) and writes out + z*m*n
+ * f32.  Negative ls/rs, or m, k, n, batch < 0, abort. */
+void dmc_matmul_bf16_gpu_batched(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k,
+                                 int64_t n, int64_t batch, int64_t ls, int64_t rs);
+
+/* Replaces dmc_matmul_bf16_gpu_batched_deferred (gpu.rs:439-466): same ABI and
+ * result as the batched entry, but returns once the work is queued; `out` is
+ * written by the next synchronous call or by dmc_matmul_bf16_gpu_flush.  A
+ * later call whose l, r or out range overlaps a pending out range flushes
+ * first (gpu.rs:491-499).  Inputs are copied before return, so the caller may
+ * reuse l at once. */
+void dmc_matmul_bf16_gpu_batched_deferred(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k,
+                                          int64_t n, int64_t batch, int64_t ls, int64_t rs);
+
+/* Replaces dmc_matmul_bf16_gpu_flush (gpu.rs:468-474): materialize every
+ * deferred call.  No-op when nothing is pending or before first use. */
+void dmc_matmul_bf16_gpu_flush(void);
+
+/* ---- additions for MI355X (no Metal counterpart) ------------------------ */
+
+/* Transposed-RHS form of dmc_matmul_bf16_gpu: r holds W[n,k] row-major (the
+ * HF/PyTorch Linear layout), out[m,n] = sum_k l[m,k] * bf16(r[n,k]).  This is
+ * demoniC's `x @ W'` without materializing W' (the reference transposes at
+ * native width first, jit.rs:19420-19454 and jit.rs:29794-29834) and
+ * `W @ x` with x:[k,1] (m = 1).  Same error behaviour and synchronicity. */
+void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+
+/* 1 when a gfx950 device is usable (initializing the context on first call),
+ * 0 otherwise; DMC_HIP_DISABLE=1 in the environment forces 0.  The analogue
+ * of blas_gemm_available() (jit.rs:29359). */
+int32_t dmc_hip_available(void);
+
+/* The host-independent half of the route decision, shaped like
+ * blas_gemm_selected (jit.rs:29346-29351): opt-in flag on, no enclosing
+ * `@deterministic` block, and at least DMC_HIP_MIN_MACS multiply-adds.
+ * Pure function; touches no device. */
+#define DMC_HIP_MIN_MACS (1LL << 17)
+int32_t dmc_hip_gemv_selected(int32_t hip_on, int32_t deterministic_depth, int64_t m, int64_t k,
+                              int64_t n);
+
+/* Message of the last error on this thread ("" if none). */
+const char *dmc_hip_last_error(void);
+
+/* Device regions: hipMalloc-backed HBM for Forge/Vault tensors (the reserved
+ * device.vault / device.forge of docs/MEMORY.md:631-636).  Addresses are
+ * device addresses as int64, 256-byte aligned; 0 means failure. */
+int64_t dmc_hip_region_alloc(int64_t bytes);
+int32_t dmc_hip_region_free(int64_t dptr);
+int32_t dmc_hip_upload(int64_t dst_dev, int64_t src_host, int64_t bytes);   /* synchronous */
+int32_t dmc_hip_download(int64_t dst_host, int64_t src_dev, int64_t bytes); /* synchronous */
+int32_t dmc_hip_copy_device(int64_t dst_dev, int64_t src_dev, int64_t bytes); /* stream-ordered */
+
+/* Make a host weight resident ahead of its first GEMV (the content-keyed memo
+ * of gpu.rs:261-280, filled at load time instead of on first use).  Returns
+ * the device address of the resident copy (0 on failure). */
+int64_t dmc_hip_register_weight(int64_t host_ptr, int64_t bytes);
+/* Drop every resident weight (after materializing deferred work). */
+int32_t dmc_hip_release_weights(void);
+/* Number and total bytes of resident weights. */
+int64_t dmc_hip_resident_count(void);
+int64_t dmc_hip_resident_bytes(void);
+
+/* Device-pointer GEMVs, enqueued on the library stream without waiting.
+ * Column-stream: w [k,n] per slice (slice z at w + z*rs u16, x + z*ls f32,
+ * y + z*m*n f32).  Row-dot: w [n,k], x [m,k], y [m,n].  Partial sums of the
+ * column-stream split use a library-owned workspace grown on demand. */
+int32_t dmc_hip_gemv_cs(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k,
+                        int64_t n, int64_t batch, int64_t ls, int64_t rs);
+int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k,
+                        int64_t n);
+int32_t dmc_hip_synchronize(void);
+
+/* Launch plan a GEMV would use on this device (or on a 256-CU gfx950 when no
+ * device is present), for tests and reports.  out6 receives
+ * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes}. */
+int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k,
+                     int64_t n, int64_t batch, int64_t rs, int64_t *out6);
+
+/* HIP events on the library stream, for timing device work. */
+int64_t dmc_hip_event_create(void);
+int32_t dmc_hip_event_record(int64_t ev);
+int32_t dmc_hip_event_synchronize(int64_t ev);
+float dmc_hip_event_elapsed_ms(int64_t start, int64_t stop); /* < 0 on error */
+int32_t dmc_hip_event_destroy(int64_t ev);
+
+/* Device facts for reports: compute units, and the name (e.g. "gfx950"). */
+int32_t dmc_hip_device_cus(void);
+const char *dmc_hip_device_arch(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DMC_HIP_H */

@@ -1,0 +1,298 @@
+"""GPU parity: libdmc_hip (through its C ABI) against the CPU oracle.
+
+Every case runs the same seeded inputs through the device and through the
+oracle (the reference's dmc_matmul_bf16 chain, compiler/src/jit.rs:29481-29681)
+and applies tests/parity.py's rule.  Row-dot (RD) cases go through
+dmc_matmul_bf16_gpu_t / dmc_hip_gemv_rd, column-stream (CS) cases through the
+drop-in dmc_matmul_bf16_gpu / _batched / _deferred and dmc_hip_gemv_cs.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from demonic_amd import workloads as W
+from parity import check
+
+pytestmark = pytest.mark.gpu
+
+
+def case(m, k, n, seed, edge=False, scale=1.0):
+    """x [m,k] f32 and logical w [n,k] bf16; `edge` adds subnormals, +-0,
+    +-1e-38 in x and a few inf/NaN weights."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    w = W.bf16_rne(np.float32(scale) * rng.standard_normal((n, k), dtype=np.float32))
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    if edge and k > 0 and n > 0:
+        cnt = max(1, n * k // 200)
+        flat = w.reshape(-1)
+        pos = rng.integers(0, n * k, size=cnt)
+        flat[pos] = (rng.integers(0, 2, size=cnt, dtype=np.uint16) << 15) | \
+            rng.integers(1, 128, size=cnt, dtype=np.uint16)
+        xs = x.reshape(-1)
+        pos = rng.integers(0, xs.size, size=max(1, xs.size // 20))
+        xs[pos] = rng.choice(np.array([0.0, -0.0, 1e-38, -1e-38], np.float32), size=pos.size)
+        if n * k >= 64:
+            pos = rng.integers(0, n * k, size=3)
+            flat[pos] = np.array([0x7F80, 0xFF80, 0x7FC0], np.uint16)
+    return x, w
+
+
+def run_rd(hip, x, w):
+    return hip.matmul_bf16_gpu_t(x, w)
+
+
+def run_cs(hip, x, w):
+    return hip.matmul_bf16_gpu(x, np.ascontiguousarray(w.T))
+
+
+def ref(x, w):
+    return oracle.matmul_bf16_t(x, w)
+
+
+# ---- basic facts ----------------------------------------------------------------------
+
+def test_device_is_gfx950(hip):
+    info = hip.device_info()
+    assert info["arch"] == "gfx950", info
+    assert info["cus"] > 0
+
+
+def test_denormals_survive_and_inf_times_tiny_is_inf(hip):
+    # 1e-38 is an f32 subnormal; flushing it would turn 1e-38 * inf into NaN.
+    k = 1000
+    x = np.zeros((1, k), np.float32)
+    x[0, 5] = np.float32(1e-38)
+    w = np.zeros((3, k), np.uint16)
+    w[0, 5] = 0x7F80          # +inf
+    w[1, 5] = 0x3F80          # 1.0  -> y = 1e-38 exactly
+    w[2, :] = 0x0001          # smallest bf16 subnormal everywhere
+    x2 = x.copy()
+    x2[0, :] = 1.0
+    for run in (run_rd, run_cs):
+        y = run(hip, x, w)[0]
+        assert np.isposinf(y[0]), y
+        assert y[1] == np.float32(1e-38), y
+        y2 = run(hip, x2, w)[0]
+        assert y2[2] == np.float32(k) * W.bf16_to_f32(np.array([1], np.uint16))[0], y2
+
+
+# ---- shape and tail coverage ----------------------------------------------------------
+
+SHAPES = [
+    (1, 1, 1), (1, 7, 3), (1, 8, 5), (1, 63, 64), (1, 64, 65), (1, 65, 129),
+    (1, 511, 7), (1, 512, 8), (1, 513, 9), (1, 1000, 33), (1, 2048, 1), (1, 4097, 37),
+    (2, 64, 17), (3, 129, 31), (5, 1024, 100), (8, 520, 24), (16, 4096, 40),
+    (17, 300, 11), (33, 96, 65), (1, 12288, 6),
+]
+
+
+@pytest.mark.parametrize("m,k,n", SHAPES)
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_shapes(hip, m, k, n, layout):
+    x, w = case(m, k, n, seed=1000 + m * 7 + k * 13 + n, edge=True)
+    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    check(y, ref(x, w), what=f"{layout} m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_k_zero_writes_positive_zero(hip, layout):
+    x = np.zeros((2, 0), np.float32)
+    w = np.zeros((5, 0), np.uint16)
+    y = hip.matmul_bf16_gpu_t(x, w) if layout == "rd" else hip.matmul_bf16_gpu(x, w.T.copy())
+    assert y.shape == (2, 5)
+    assert np.all(y == 0) and not np.any(np.signbit(y))
+
+
+def test_m_or_n_zero_leaves_out_untouched(hip):
+    lib = hip._lib.load()
+    out = np.full(4, 7.0, np.float32)
+    x = np.ones(8, np.float32)
+    w = np.ones(8, np.uint16)
+    lib.dmc_matmul_bf16_gpu(x.ctypes.data, w.ctypes.data, out.ctypes.data, 0, 8, 4)
+    lib.dmc_matmul_bf16_gpu(x.ctypes.data, w.ctypes.data, out.ctypes.data, 1, 8, 0)
+    lib.dmc_matmul_bf16_gpu_batched(x.ctypes.data, w.ctypes.data, out.ctypes.data, 1, 8, 4, 0, 0, 0)
+    assert np.all(out == 7.0)
+
+
+# ---- the BASELINE configurations ---------------------------------------------------------
+
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_c1_full(hip, layout):
+    w, x = W.c1()
+    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    rel = check(y, ref(x, w), what=f"C1 {layout}")
+    print(f"C1 {layout} rel={rel:.3e}")
+
+
+@pytest.mark.parametrize("shape", W.C5_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_c5_numerics(hip, shape, layout):
+    n, k = shape
+    w, x, rows = W.c5(n, k)
+    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)[0]
+    y_ref = ref(x, w)[0]
+    rel = check(y, y_ref, what=f"C5 {shape} {layout}")
+    print(f"C5 {shape} {layout} rel={rel:.3e}")
+    # the rule each named row was built for (the oracle must agree, too)
+    expect = {"inf_pos": "+inf", "inf_neg_x": "+inf", "inf_both": "nan", "inf_zero": "nan",
+              "inf_nzero": "nan", "inf_tiny": "+inf", "inf_ntiny": "+inf", "nan_w": "nan",
+              "zero_row": "+0", "negzero_row": "+0"}
+    for name, cls in expect.items():
+        for v in (y[rows[name]], y_ref[rows[name]]):
+            if cls == "nan":
+                assert np.isnan(v), (name, v)
+            elif cls == "+inf":
+                assert np.isposinf(v), (name, v)
+            else:
+                assert v == 0 and not np.signbit(v), (name, v)
+    # all-subnormal weights: not flushed (nonzero, same sign), and within the
+    # rigorous forward-error bound of two length-K fma chains, 2*K*u*sum|x*w|
+    s = rows["sub_row"]
+    terms = np.abs(x[0].astype(np.float64) * W.bf16_to_f32(w[s]).astype(np.float64))
+    bound = 2 * k * 2.0 ** -24 * terms.sum()
+    assert y_ref[s] != 0 and y[s] != 0 and np.signbit(y[s]) == np.signbit(y_ref[s]), (y[s], y_ref[s])
+    assert abs(float(y[s]) - float(y_ref[s])) <= bound, (y[s], y_ref[s], bound)
+
+
+@pytest.mark.parametrize("which", ["up", "down"])
+def test_c2_sampled_rows(hip, which):
+    """Full Llama-3-8B FFN shapes through the device-pointer entries; the
+    oracle checks 512 random rows plus the first and last."""
+    w, x = W.c2()[which]
+    n, k = w.shape
+    with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * n) as dy:
+        hip.gemv_rd(dx, dw, dy, 1, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (n,))
+    rng = np.random.default_rng(5)
+    rows = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, 512)]))
+    y_ref = oracle.gemv_points(x, w, "rd", np.zeros_like(rows), rows)
+    rel = check(y[rows], y_ref, what=f"C2 {which}")
+    print(f"C2 {which} rel={rel:.3e}")
+    # the column-stream kernel on the transposed copy agrees as well
+    wt = np.ascontiguousarray(w.T)
+    with hip.DeviceBuffer.from_numpy(wt) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * n) as dy:
+        hip.gemv_cs(dx, dw, dy, 1, k, n)
+        hip.synchronize()
+        y2 = dy.download(np.float32, (n,))
+    check(y2[rows], y_ref, what=f"C2 {which} cs")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_skinny_m(hip, m, layout):
+    """The LM-head skinny batch on a 16,387-row slice of the C4 weight shape."""
+    x, w = case(m, 4096, 16387, seed=77 + m, scale=0.02)
+    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    check(y, ref(x, w), what=f"skinny m={m} {layout}")
+
+
+# ---- batched / deferred protocol (gpu.rs:410-474) ----------------------------------------
+
+def test_batched_matches_per_slice(hip):
+    k, n, batch = 256, 64, 6
+    ls, rs = k + 8, k * n + 64
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((batch - 1) * ls + k).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal((batch - 1) * rs + k * n).astype(np.float32))
+    y = hip.matmul_bf16_gpu_batched(x, w, 1, k, n, batch, ls, rs)
+    y_ref = oracle.matmul_bf16_batched(x, w, k, n, batch, ls, rs)
+    check(y, y_ref, what="batched")
+
+
+def test_batched_broadcast_activation(hip):
+    # ls = 0: every slice reads the same activation (the broadcast [B,1,S,K] case)
+    k, n, batch = 128, 32, 9
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(k).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal(batch * k * n).astype(np.float32))
+    y = hip.matmul_bf16_gpu_batched(x, w, 1, k, n, batch, 0, k * n)
+    check(y, oracle.matmul_bf16_batched(x, w, k, n, batch, 0, k * n), what="broadcast")
+
+
+def test_deferred_then_flush(hip):
+    k, n = 512, 256
+    rng = np.random.default_rng(6)
+    outs, refs = [], []
+    for i in range(5):
+        x = rng.standard_normal(k).astype(np.float32)
+        w = W.bf16_rne(rng.standard_normal(k * n).astype(np.float32))
+        refs.append(oracle.matmul_bf16_batched(x, w, k, n, 1, 0, 0))
+        out = np.full(n, np.nan, np.float32)
+        hip.matmul_bf16_gpu_batched_deferred(x, w, out, 1, k, n, 1, 0, 0)
+        x[:] = 12345.0  # inputs are copied before return; this must not leak in
+        outs.append(out)
+    hip.flush()
+    for out, y_ref in zip(outs, refs):
+        check(out, y_ref, what="deferred")
+
+
+def test_sync_call_materializes_deferred(hip):
+    k, n = 256, 128
+    rng = np.random.default_rng(8)
+    x1 = rng.standard_normal(k).astype(np.float32)
+    w1 = W.bf16_rne(rng.standard_normal(k * n).astype(np.float32))
+    out1 = np.full(n, np.nan, np.float32)
+    hip.matmul_bf16_gpu_batched_deferred(x1, w1, out1, 1, k, n, 1, 0, 0)
+    x2 = rng.standard_normal((1, k)).astype(np.float32)
+    w2 = W.bf16_rne(rng.standard_normal((k, n)).astype(np.float32))
+    y2 = hip.matmul_bf16_gpu(x2, w2)
+    check(out1, oracle.matmul_bf16_batched(x1, w1, k, n, 1, 0, 0), what="deferred by sync")
+    check(y2, oracle.matmul_bf16(x2, w2), what="sync")
+
+
+def test_overlap_with_pending_output_flushes_first(hip):
+    # the second call reads the first call's pending output as its activation
+    k = n = 128
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(k).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal(k * n).astype(np.float32))
+    mid = np.full(n, np.nan, np.float32)
+    hip.matmul_bf16_gpu_batched_deferred(x, w, mid, 1, k, n, 1, 0, 0)
+    out = np.empty(n, np.float32)
+    hip.matmul_bf16_gpu_batched_deferred(mid, w, out, 1, k, n, 1, 0, 0)
+    hip.flush()
+    ref_mid = oracle.matmul_bf16_batched(x, w, k, n, 1, 0, 0)
+    check(mid, ref_mid, what="first")
+    check(out, oracle.matmul_bf16_batched(ref_mid, w, k, n, 1, 0, 0), tol=1e-4, what="chained")
+
+
+# ---- residency and determinism -----------------------------------------------------------
+
+def test_weights_resident_by_content(hip):
+    hip.release_weights()
+    x, w = case(1, 1024, 512, seed=11)
+    wt = np.ascontiguousarray(w.T)
+    y1 = hip.matmul_bf16_gpu(x, wt)
+    assert hip.resident_count() == 1
+    wt_copy = wt.copy()                       # same bytes, new address: no upload
+    y2 = hip.matmul_bf16_gpu(x, wt_copy)
+    assert hip.resident_count() == 1
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    wt_copy[0, 0] ^= 1                        # one sampled word differs: new entry
+    hip.matmul_bf16_gpu(x, wt_copy)
+    assert hip.resident_count() == 2
+    hip.release_weights()
+    assert hip.resident_count() == 0 and hip.resident_bytes() == 0
+
+
+def test_register_weight_then_call(hip):
+    hip.release_weights()
+    x, w = case(1, 2048, 300, seed=12)
+    wt = np.ascontiguousarray(w.T)
+    assert hip.register_weight(wt) != 0
+    assert hip.resident_count() == 1
+    y = hip.matmul_bf16_gpu(x, wt)
+    assert hip.resident_count() == 1
+    check(y, ref(x, w), what="registered")
+
+
+@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_repeat_calls_bit_identical(hip, layout):
+    x, w = case(1, 14336, 1024, seed=13, scale=0.02)
+    run = run_rd if layout == "rd" else run_cs
+    a = run(hip, x, w)
+    b = run(hip, x, w)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
