@@ -1,0 +1,168 @@
+"""libdmc_hip on the CPU: the C ABI loads and exports every declared symbol,
+and the host-side logic that needs no device behaves as specified.  No GEMV is
+computed here (there is no GPU); device-free entry points only.
+"""
+import os
+import pathlib
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+import demonic_amd as d
+from demonic_amd import _lib
+
+ROOT = pathlib.Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "dmc_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(dmc_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == sorted(_lib.SIGNATURES), \
+        set(declared_functions()) ^ set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (dmc_\w+)", out))
+    assert set(declared_functions()) <= exported
+
+
+def test_reference_operator_surface_is_exported_with_reference_names():
+    # compiler/src/gpu.rs:400, 421, 449, 468
+    for name in ("dmc_matmul_bf16_gpu", "dmc_matmul_bf16_gpu_batched",
+                 "dmc_matmul_bf16_gpu_batched_deferred", "dmc_matmul_bf16_gpu_flush"):
+        assert name in declared_functions()
+    assert _lib.SIGNATURES["dmc_matmul_bf16_gpu"][1] == [_lib.i64] * 6
+    assert _lib.SIGNATURES["dmc_matmul_bf16_gpu_batched"][1] == [_lib.i64] * 9
+
+
+def test_library_is_gfx950_code_only(tmp_path):
+    """The code object bundled in our own build targets gfx950 and nothing else."""
+    fb = tmp_path / "fatbin.bin"
+    r = subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin",
+                        str(_lib.LIB_PATH), str(fb)], capture_output=True, text=True)
+    out = subprocess.run(["/opt/rocm/llvm/bin/clang-offload-bundler", "--list", "--type=o",
+                          f"--input={fb}"], capture_output=True, text=True)
+    if r.returncode != 0 or out.returncode != 0:
+        pytest.skip("offload bundle tools unavailable")
+    targets = [t for t in out.stdout.split() if "amdgcn" in t]
+    assert targets == ["hipv4-amdgcn-amd-amdhsa--gfx950"], out.stdout
+
+
+# ---- the route predicate (shape of jit.rs:39087-39113) ----------------------------------
+
+def test_selection_predicate():
+    sel = d.gemv_selected
+    assert sel(True, 0, 1, 512, 512), "eligible GEMV refused"
+    assert not sel(False, 0, 1, 512, 512), "selected with the flag off"
+    assert not sel(True, 1, 1, 512, 512), "selected inside @deterministic"
+    assert not sel(True, 3, 1, 4096, 14336), "nested @deterministic"
+    assert not sel(True, 0, 1, 128, 128), "small GEMV selected"
+    assert sel(True, 0, 1, 1, d.MIN_MACS), "at the threshold"
+    assert not sel(True, 0, 1, 1, d.MIN_MACS - 1), "one under the threshold"
+    assert sel(True, 0, 64, 64, 64), "threshold is a MAC count, not per-dimension"
+    assert not sel(True, 0, 0, 4096, 4096) and not sel(True, 0, 1, 0, 4096)
+
+
+# ---- launch planning (pure host computation) ----------------------------------------------
+
+@pytest.mark.parametrize("k,align,vec", [(4096, 256, 8), (4100, 256, 4), (4098, 256, 2),
+                                         (4097, 256, 1), (4096, 258, 1), (4096, 260, 2),
+                                         (4096, 264, 4)])
+def test_rowdot_vector_width_follows_alignment(k, align, vec):
+    p = d.plan("rd", 1, k, 14336, x_addr=256, w_addr=align)
+    assert p.vec == vec, p
+
+
+def test_rowdot_plans_at_decode_shapes():
+    up = d.plan("rd", 1, 4096, 14336, x_addr=256, w_addr=256)
+    assert (up.vec, up.rows_or_rw, up.mt, up.grid_x) == (8, 4, 1, 3584)
+    small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
+    assert small.grid_x >= 512
+    for m, mt in [(1, 1), (2, 2), (3, 4), (5, 8), (16, 16), (17, 16)]:
+        assert d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256).mt == mt
+
+
+def test_column_stream_plans_split_k_and_size_workspace():
+    p = d.plan("cs", 1, 14336, 4096, x_addr=256, w_addr=256)
+    assert p.vec == 8 and p.slices > 1
+    assert p.workspace_bytes == p.slices * 4096 * 4
+    one = d.plan("cs", 1, 64, 4096, x_addr=256, w_addr=256)
+    assert one.slices == 1 and one.workspace_bytes == 0
+    odd = d.plan("cs", 1, 4097, 11007, x_addr=256, w_addr=256)
+    assert odd.vec == 1
+    zero_k = d.plan("cs", 1, 0, 512, x_addr=256, w_addr=256)
+    assert zero_k.slices == 1
+
+
+# ---- errors without a device ------------------------------------------------------------------
+
+def test_int_entries_reject_bad_shapes_before_touching_a_device():
+    lib = _lib.load()
+    assert lib.dmc_hip_gemv_rd(0, 0, 0, -1, 4, 4) == -2
+    assert lib.dmc_hip_gemv_cs(0, 0, 0, 1, 4, 4, -1, 0, 0) == -2
+    assert lib.dmc_hip_gemv_rd(0, 0, 0, 1, 1 << 31, 4) == -2
+    assert lib.dmc_hip_region_alloc(0) == 0
+    assert b"positive" in lib.dmc_hip_last_error()
+    assert lib.dmc_hip_gemv_rd(0, 0, 0, 0, 4, 4) == 0  # m == 0: no-op, no device needed
+
+
+def test_python_api_validates_before_calling():
+    with pytest.raises(TypeError):
+        d.matmul_bf16_gpu(np.ones((1, 4), np.float64), np.ones((4, 2), np.uint16))
+    with pytest.raises(ValueError):
+        d.matmul_bf16_gpu(np.ones((1, 4), np.float32), np.ones((5, 2), np.uint16))
+    with pytest.raises(ValueError):
+        d.matmul_bf16_gpu_t(np.ones((1, 4), np.float32), np.ones((2, 5), np.uint16))
+    with pytest.raises(ValueError):
+        d.matmul_bf16_gpu_batched(np.ones(4, np.float32), np.ones(8, np.uint16), 1, 4, 2, 3, 4, 8)
+
+
+def _run_isolated(code: str, **env):
+    e = dict(os.environ)
+    e.update(env)
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=e,
+                          cwd=str(ROOT), timeout=120)
+
+
+def test_unavailable_when_disabled():
+    r = _run_isolated("import demonic_amd as d; print(d.available()); "
+                      "print(d._lib.load().dmc_hip_last_error().decode())", DMC_HIP_DISABLE="1")
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.split("\n")[0] == "False"
+    assert "DMC_HIP_DISABLE" in r.stdout
+
+
+def test_dropin_entry_fails_loudly_without_a_device():
+    """No CPU fallback: with the device unavailable the void entry aborts with
+    a message instead of writing anything (callers ask dmc_hip_available first)."""
+    code = ("import numpy as np, demonic_amd as d\n"
+            "x = np.ones((1, 8), np.float32); w = np.ones((8, 4), np.uint16)\n"
+            "d.matmul_bf16_gpu(x, w)\nprint('returned')\n")
+    r = _run_isolated(code, DMC_HIP_DISABLE="1")
+    assert r.returncode != 0
+    assert "dmc_hip: fatal: dmc_matmul_bf16_gpu" in r.stderr
+    assert "returned" not in r.stdout
+
+
+def test_flush_before_first_use_is_a_noop():
+    r = _run_isolated("import demonic_amd as d; d.flush(); print('ok')", DMC_HIP_DISABLE="1")
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr
+
+
+def test_package_has_no_cpu_gemv_and_never_imports_the_oracle():
+    src = "\n".join(p.read_text() for p in (ROOT / "demonic_amd").rglob("*.py"))
+    src += "\n".join(p.read_text() for p in (ROOT / "demonic_amd" / "csrc").glob("*"))
+    assert "import oracle" not in src and "from oracle" not in src
+    assert "fmaf(" not in (ROOT / "demonic_amd" / "csrc" / "dmc_hip_runtime.cpp").read_text()
