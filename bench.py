@@ -4,20 +4,28 @@
 Workload (one "step"): the two Llama-3-8B FFN decode GEMVs of config C2 in the
 row-dot layout -- up/gate W [14336,4096] @ x[4096] and down W [4096,14336] @
 x[14336] -- bf16 weights ~N(0,0.02), f32 activations ~N(0,1), seed 0, weights
-resident in HBM.  Cold cache: each weight has COPIES distinct device copies
-and consecutive steps rotate through them, so >= 1 GiB of other weights is
-streamed between two reads of the same bytes (MI355X's Infinity Cache is
-256 MB).  Every launch is bracketed by HIP events on the library stream.
+and activations resident in HBM before the timed region starts.  Cold cache:
+each weight has COPIES distinct device copies and consecutive steps rotate
+through them, so >= 1 GiB of other weights streams between two reads of the
+same bytes (MI355X's Infinity Cache is 256 MB).
 
-value      whole-job throughput: algorithmic bytes of the K timed steps over
-           their wall time (inputs already resident).
-roofline   algorithmic bytes per launch / average kernel duration (events),
-           against MI355X's 8 TB/s HBM peak.
+value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
+              of the K timed steps over their host wall time.
+roofline      algorithmic bytes per launch / average launch duration of the
+              row-dot streaming kernel, from HIP events on the library stream
+              around the timed region (2K back-to-back launches).  Each
+              duration includes the fixed cost of a dispatch, which
+              `dispatch_floor_us` measures alone with empty launches (rocprof
+              counts it inside a kernel's duration too).  Peak: MI355X's
+              8 TB/s HBM3E.  `us_per_launch` times each shape in its own
+              back-to-back batch.
+read_ceiling  the same weights streamed by a read-only probe with the same
+              128-bit nontemporal loads, timed the same way.
 cpu_baseline  the oracle's restatement of the reference CPU kernel
-           dmc_matmul_bf16 (same fmaf chain and threading policy) timed on
-           this host on a bounded sample of the same workload.
+              dmc_matmul_bf16 (same fmaf chain and threading policy) on this
+              host, on a bounded sample of the same workload.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--extended]
+    python bench.py [--gpus 1] [--steps 200] [--warmup 10] [--extended]
 """
 from __future__ import annotations
 
@@ -35,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 
 PEAK_GBS = 8000.0
 METRIC = "bf16 GEMV achieved HBM GB/s (% of peak) + µs/call at 4096×14336, 1 GPU"
+TRAFFIC_PROFILE = ROOT / "profiles" / "gemv_rd_stream_c2_traffic.md"
 
 
 def b_alg(n: int, k: int, m: int = 1) -> int:
@@ -46,24 +55,23 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def traffic_from_profiles(kernel_prefix: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, scaled by the copy-kernel calibration), read from the committed
-    summary under profiles/; None when absent."""
-    p = ROOT / "profiles" / "traffic.md"
-    if not p.exists():
+def traffic_from_profile():
+    """HBM bytes per launch of the C2 row-dot GEMVs measured by rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel of known size),
+    averaged over the two shapes like `achieved`; read from the committed
+    summary (a line `traffic_bytes_per_launch: N`), None when absent."""
+    if not TRAFFIC_PROFILE.exists():
         return None
-    for line in p.read_text().splitlines():
-        parts = line.strip().strip("|").split("|")
-        if len(parts) >= 3 and parts[0].strip() == kernel_prefix:
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
             try:
-                return int(float(parts[2].strip()))
+                return int(float(line.split(":", 1)[1].strip()))
             except ValueError:
                 return None
     return None
 
 
-def cpu_baseline(seconds: float = 12.0) -> dict:
+def cpu_baseline(seconds: float) -> dict:
     """The reference CPU path restated (oracle, 'port' build: scalar fmaf like
     the reference's x86 build) on C2's up/gate GEMV in the reference kernel's
     own layout, x @ W with W [4096,14336] (pre-transposed so no transpose is
@@ -75,37 +83,74 @@ def cpu_baseline(seconds: float = 12.0) -> dict:
     wt = np.ascontiguousarray(w.T)
     k, n = wt.shape
     threads = oracle.gemv_ways(k, n)
-    oracle.matmul_bf16(x, wt)  # warm caches/pages
+    oracle.matmul_bf16(x, wt)  # warm caches and pages
     calls, t0 = 0, time.perf_counter()
     while True:
         oracle.matmul_bf16(x, wt)
         calls += 1
         el = time.perf_counter() - t0
-        if el >= seconds or calls >= 200:
+        if el >= seconds or calls >= 5000:
             break
     per = el / calls
     gbs = b_alg(n, k) / per / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"C2 up/gate x@W W[{k},{n}] bf16, m=1, {calls} calls in {el:.1f}s "
-                      f"({per * 1e6:.0f} us/call), oracle restatement of dmc_matmul_bf16 "
-                      f"(jit.rs:29488), scalar fmaf, {threads} threads by the reference policy, "
-                      f"host nproc={os.cpu_count()}"}
+            "sample": f"C2 up/gate x@W, W[{k},{n}] bf16, m=1: {calls} calls in {el:.1f}s "
+                      f"({per * 1e6:.0f} us/call); oracle restatement of dmc_matmul_bf16 "
+                      f"(jit.rs:29488): scalar libm fmaf chain, {threads} threads by the reference's "
+                      f"column-split policy (jit.rs:29527-29529); host nproc={os.cpu_count()}"}
+
+
+class Rotating:
+    """COPIES device copies of one weight, plus its x and y regions."""
+
+    def __init__(self, d, w: np.ndarray, x: np.ndarray, copies: int, n_out: int | None = None):
+        self.d = d
+        self.shape = w.shape
+        first = d.DeviceBuffer.from_numpy(w)
+        self.w = [first]
+        for _ in range(copies - 1):
+            c = d.DeviceBuffer(w.nbytes)
+            c.copy_from(first)
+            self.w.append(c)
+        self.x = d.DeviceBuffer.from_numpy(x)
+        rows = x.shape[0] if x.ndim == 2 else 1
+        self.y = d.DeviceBuffer(4 * rows * (w.shape[0] if n_out is None else n_out))
+        self.m = rows
+
+    def free(self):
+        for b in self.w + [self.x, self.y]:
+            b.free()
+
+
+def batch_us(d, fn, reps: int) -> float:
+    """Average duration of `reps` back-to-back launches, HIP events on the
+    library stream around the whole batch."""
+    e0, e1 = d.Event(), d.Event()
+    d.synchronize()
+    e0.record()
+    for i in range(reps):
+        fn(i)
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_ms(e1) * 1e3 / reps
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=5, help="distinct device copies per weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
-    ap.add_argument("--extended", action="store_true", help="also time C1, C4, C5 and the CS layout (stderr)")
+    ap.add_argument("--extended", action="store_true",
+                    help="also time C1, C4, C5 and the column-stream layout (stderr + 'extended')")
     a = ap.parse_args(argv)
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the GEMV shards by output rows with "
-              "no reduction; see DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the GEMV shards by weight rows "
+              "with no reduction, so N GPUs would each run this kernel on N-th of the rows); "
+              "run with --gpus 1", file=sys.stderr)
         return 2
 
     import demonic_amd as d
@@ -115,73 +160,67 @@ def main(argv=None) -> int:
         print("bench.py: no usable gfx950 device: " + d._lib.load().dmc_hip_last_error().decode(),
               file=sys.stderr)
         return 1
-    info = d.device_info()
-    log(f"device {info}")
+    log(f"device {d.device_info()}")
 
     t = time.perf_counter()
     c2 = W.c2()
-    log(f"generated C2 inputs in {time.perf_counter() - t:.1f}s")
-    shapes = {}
-    bufs = []
-    for name, (w, x) in c2.items():
-        n, k = w.shape
-        first = d.DeviceBuffer.from_numpy(w)
-        copies = [first]
-        for _ in range(a.copies - 1):
-            c = d.DeviceBuffer(w.nbytes)
-            c.copy_from(first)
-            copies.append(c)
-        dx = d.DeviceBuffer.from_numpy(x)
-        dy = d.DeviceBuffer(4 * n)
-        shapes[name] = (n, k, copies, dx, dy)
-        bufs += copies + [dx, dy]
+    shapes = {name: Rotating(d, w, x, a.copies) for name, (w, x) in c2.items()}
     d.synchronize()
+    log(f"C2 inputs resident in {time.perf_counter() - t:.1f}s")
     order = ["up", "down"]
 
-    def launch(name, step):
-        n, k, copies, dx, dy = shapes[name]
-        d.gemv_rd(dx, copies[step % len(copies)], dy, 1, k, n)
+    def launch(name, i):
+        s = shapes[name]
+        n, k = s.shape
+        d.gemv_rd(s.x, s.w[i % len(s.w)], s.y, 1, k, n)
 
     for i in range(a.warmup):
         for name in order:
             launch(name, i)
     d.synchronize()
 
-    evs = [d.Event() for _ in range(a.steps * len(order) * 2)]
+    # timed region: K steps, each the two GEMVs, inputs resident
+    e0, e1 = d.Event(), d.Event()
     t0 = time.perf_counter()
-    e = 0
+    e0.record()
     for i in range(a.steps):
         for name in order:
-            evs[e].record()
             launch(name, i)
-            evs[e + 1].record()
-            e += 2
+    e1.record()
     d.synchronize()
     wall = time.perf_counter() - t0
-
-    per_shape = {name: [] for name in order}
-    e = 0
-    for i in range(a.steps):
-        for name in order:
-            per_shape[name].append(evs[e].elapsed_ms(evs[e + 1]) * 1e3)
-            e += 2
-    bytes_step = sum(b_alg(shapes[nm][0], shapes[nm][1]) for nm in order)
+    ev_ms = e0.elapsed_ms(e1)
+    bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
     value = bytes_step * a.steps / wall / 1e9
-    kern_us = {nm: float(np.mean(v)) for nm, v in per_shape.items()}
-    avg_us = float(np.mean([u for v in per_shape.values() for u in v]))
-    achieved = np.mean([b_alg(shapes[nm][0], shapes[nm][1]) for nm in order]) / (avg_us * 1e-6) / 1e9
-    # parity spot check of the timed outputs (first rows only; full parity is in tests/)
-    for nm in order:
-        n, k, copies, dx, dy = shapes[nm]
-        y = dy.download(np.float32, (n,))
-        assert np.all(np.isfinite(y)), nm
 
-    roofline = {"bound": "hbm", "achieved": round(float(achieved), 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(float(achieved) / PEAK_GBS, 4),
-                "traffic": traffic_from_profiles("gemv_rd_kernel<8,4,1>"),
-                "kernel": "gemv_rd_kernel<VEC=8,ROWS=4,MT=1>",
-                "bytes_per_launch": int(b_alg(14336, 4096))}
-    cpu = None if a.no_cpu else cpu_baseline(a.cpu_seconds)
+    # per-shape launch durations, the read ceiling and the dispatch floor
+    us = {nm: batch_us(d, lambda i, nm=nm: launch(nm, i), a.steps) for nm in order}
+    read_us = {nm: batch_us(d, lambda i, nm=nm: d.probe_read(shapes[nm].w[i % a.copies]), a.steps)
+               for nm in order}
+    floor_us = batch_us(d, lambda i: d.probe_read(None, 0), a.steps)
+    for nm in order:
+        y = shapes[nm].y.download(np.float32, (shapes[nm].shape[0],))
+        assert np.all(np.isfinite(y)), nm  # full parity lives in tests/
+
+    b_up, b_down = (b_alg(*shapes[nm].shape) for nm in order)
+    launch_us = ev_ms * 1e3 / (a.steps * len(order))
+    achieved = (b_up + b_down) / 2 / (launch_us * 1e-6) / 1e9
+    w_bytes = {nm: 2 * shapes[nm].shape[0] * shapes[nm].shape[1] for nm in order}
+    read_gbs = sum(w_bytes.values()) / (sum(read_us.values()) * 1e-6) / 1e9
+    plans = {nm: d.plan("rd", 1, shapes[nm].shape[1], shapes[nm].shape[0],
+                        x_addr=shapes[nm].x.addr, w_addr=shapes[nm].w[0].addr) for nm in order}
+    roofline = {
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_from_profile(),
+        "kernel": "gemv_rd_stream_kernel (row-dot streaming GEMV)",
+        "bytes_per_launch": {"up": b_up, "down": b_down},
+        "avg_launch_us": round(launch_us, 3),
+        "us_per_launch": {nm: round(u, 3) for nm, u in us.items()},
+        "frac_of_read_ceiling": round(achieved / read_gbs, 4),
+    }
+    for b in shapes.values():
+        b.free()
+
     result = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall / a.steps * 1e3, 4),
@@ -190,59 +229,51 @@ def main(argv=None) -> int:
         "config": {"workload": "C2 Llama-3-8B FFN decode GEMVs, row-dot layout: up/gate W[14336,4096] "
                                "and down W[4096,14336], m=1, weights resident, cold cache "
                                f"({a.copies} rotating copies each)",
-                   "us_per_call": {nm: round(u, 3) for nm, u in kern_us.items()},
-                   "frac_of_peak_value": round(value / PEAK_GBS, 4)},
+                   "us_per_call": {nm: round(u, 3) for nm, u in us.items()},
+                   "frac_of_peak_value": round(value / PEAK_GBS, 4),
+                   "event_ms_per_step": round(ev_ms / a.steps, 4),
+                   "plans": {nm: {"waves": p.waves, "kvec": p.slices, "rows_per_group": p.rows_per_group,
+                                  "rows_per_step": p.rows_or_rw, "groups": p.grid_x}
+                             for nm, p in plans.items()}},
         "roofline": roofline,
-        "cpu_baseline": cpu,
+        "read_ceiling": {"GB/s": round(read_gbs, 1), "us": {nm: round(u, 3) for nm, u in read_us.items()},
+                         "frac_of_peak": round(read_gbs / PEAK_GBS, 4)},
+        "dispatch_floor_us": round(floor_us, 3),
+        "cpu_baseline": None if a.no_cpu else cpu_baseline(a.cpu_seconds),
     }
     if a.extended:
-        result["extended"] = extended(d, W)
-    for b in bufs:
-        b.free()
+        result["extended"] = extended(d, W, a.steps)
     print(json.dumps(result), flush=True)
     return 0
 
 
-def _time_calls(d, fn, reps):
-    evs = [d.Event() for _ in range(2 * reps)]
-    for i in range(reps):
-        evs[2 * i].record()
-        fn(i)
-        evs[2 * i + 1].record()
-    d.synchronize()
-    return float(np.mean([evs[2 * i].elapsed_ms(evs[2 * i + 1]) * 1e3 for i in range(reps)]))
-
-
-def extended(d, W) -> dict:
+def extended(d, W, reps: int) -> dict:
     """Secondary configurations (stderr + the JSON 'extended' field)."""
     out = {}
-    cases = [("C1 rd 4096x4096", W.c1(), "rd", 1)]
-    c2 = W.c2()
-    cases += [("C2 cs up [4096,14336]", c2["up"], "cs", 1), ("C2 cs down [14336,4096]", c2["down"], "cs", 1)]
-    for label, (w, x), layout, m in cases:
-        n, k = w.shape
-        wl = w if layout == "rd" else np.ascontiguousarray(w.T)
-        reps = max(2, int(1.2e9 // wl.nbytes) + 2)
-        copies = [d.DeviceBuffer.from_numpy(wl)]
-        for _ in range(min(reps, 10) - 1):
-            c = d.DeviceBuffer(wl.nbytes)
-            c.copy_from(copies[0])
-            copies.append(c)
-        dx = d.DeviceBuffer.from_numpy(x)
-        dy = d.DeviceBuffer(4 * n * m)
-        f = (lambda i: d.gemv_rd(dx, copies[i % len(copies)], dy, m, k, n)) if layout == "rd" else \
-            (lambda i: d.gemv_cs(dx, copies[i % len(copies)], dy, m, k, n))
-        for i in range(3):
-            f(i)
-        us = _time_calls(d, f, 30)
+
+    def record(label, us, n, k, m=1):
         gbs = b_alg(n, k, m) / (us * 1e-6) / 1e9
         out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
-        for c in copies:
-            c.free()
-        dx.free()
-        dy.free()
-    # C4 LM head, skinny M (one resident copy: 1.05 GB exceeds the 256 MB cache)
+
+    c2 = W.c2()
+    cases = [("C1 rd [4096,4096]", W.c1(), "rd"),
+             ("C2 cs up x@W W[4096,14336]", c2["up"], "cs"),
+             ("C2 cs down x@W W[14336,4096]", c2["down"], "cs")]
+    for label, (w, x), layout in cases:
+        n, k = w.shape
+        wl = w if layout == "rd" else np.ascontiguousarray(w.T)
+        copies = max(2, min(12, int(1.2e9 // wl.nbytes) + 1))
+        s = Rotating(d, wl, x, copies, n_out=n)
+        if layout == "rd":
+            f = lambda i: d.gemv_rd(s.x, s.w[i % copies], s.y, 1, k, n)  # noqa: E731
+        else:
+            f = lambda i: d.gemv_cs(s.x, s.w[i % copies], s.y, 1, k, n)  # noqa: E731
+        for i in range(3):
+            f(i)
+        record(label, batch_us(d, f, reps), n, k)
+        s.free()
+    # C4 LM head, skinny M: one resident copy (1.05 GB exceeds the 256 MB cache)
     t = time.perf_counter()
     w, _ = W.dense(W.LM_HEAD[0], W.LM_HEAD[1], seed=0, m=1)
     log(f"C4 weight generated in {time.perf_counter() - t:.1f}s")
@@ -254,13 +285,23 @@ def extended(d, W) -> dict:
         dy = d.DeviceBuffer(4 * n * m)
         f = lambda i: d.gemv_rd(dx, dw, dy, m, k, n)  # noqa: E731
         f(0)
-        us = _time_calls(d, f, 10)
-        gbs = b_alg(n, k, m) / (us * 1e-6) / 1e9
-        out[f"C4 rd m={m}"] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
-        log(f"C4 rd m={m}: {us:.1f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
+        record(f"C4 rd m={m}", batch_us(d, f, 10), n, k, m)
         dx.free()
         dy.free()
     dw.free()
+    # C5 edge shapes, both layouts (timed, not gated)
+    for (n, k) in W.C5_SHAPES:
+        w, x, _ = W.c5(n, k)
+        for layout in ("rd", "cs"):
+            wl = w if layout == "rd" else np.ascontiguousarray(w.T)
+            s = Rotating(d, wl, x, 3, n_out=n)
+            if layout == "rd":
+                f = lambda i: d.gemv_rd(s.x, s.w[i % 3], s.y, 1, k, n)  # noqa: E731
+            else:
+                f = lambda i: d.gemv_cs(s.x, s.w[i % 3], s.y, 1, k, n)  # noqa: E731
+            f(0)
+            record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
+            s.free()
     return out
 
 

@@ -24,7 +24,7 @@ __all__ = [
     "BackendMissing", "HipError", "available", "gemv_selected", "MIN_MACS",
     "matmul_bf16_gpu", "matmul_bf16_gpu_t", "matmul_bf16_gpu_batched",
     "matmul_bf16_gpu_batched_deferred", "flush", "DeviceBuffer", "gemv_cs", "gemv_rd",
-    "synchronize", "Event", "plan", "register_weight", "release_weights",
+    "synchronize", "probe_read", "Event", "plan", "register_weight", "release_weights",
     "resident_count", "resident_bytes", "device_info",
 ]
 
@@ -204,6 +204,13 @@ def synchronize() -> None:
     _lib.check(_lib.load().dmc_hip_synchronize())
 
 
+def probe_read(buf, nbytes: int | None = None) -> None:
+    """Enqueue a read-only pass over a device region (the stream-read ceiling
+    probe); nbytes=0 enqueues an empty launch (the dispatch floor)."""
+    n = buf.nbytes if nbytes is None else int(nbytes)
+    _lib.check(_lib.load().dmc_hip_probe_read(_addr(buf) if n else 0, n))
+
+
 class Event:
     """A HIP event recorded on the library stream."""
 
@@ -238,14 +245,16 @@ class Plan:
     rows_or_rw: int
     mt: int
     grid_x: int
-    slices: int
+    slices: int            # cs: k slices; rd: 8-element k vectors per lane (0 = general kernel)
     workspace_bytes: int
+    waves: int
+    rows_per_group: int    # rd: weight rows per workgroup; cs: columns per workgroup
 
 
 def plan(layout: str, m: int, k: int, n: int, batch: int = 1, rs: int = 0,
          x_addr: int = 0, w_addr: int = 0) -> Plan:
     """Launch plan for layout 'rd' or 'cs' (pure host computation)."""
-    out = (ctypes.c_int64 * 6)()
+    out = (ctypes.c_int64 * 8)()
     _lib.check(_lib.load().dmc_hip_plan(int(layout == "rd"), x_addr, w_addr, m, k, n, batch, rs, out))
     return Plan(*[int(v) for v in out])
 

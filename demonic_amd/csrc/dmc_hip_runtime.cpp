@@ -136,6 +136,7 @@ struct Ctx {
     size_t hx_off = 0, hy_off = 0;
     std::vector<Pending> pending;
     void *dummy = nullptr;  // non-null device address for zero-byte weights
+    void *sink = nullptr;   // probe output words
     bool timing = false;
     Stats st;
 };
@@ -599,6 +600,18 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
     return DMC_HIP_OK;
 }
 
+int32_t dmc_hip_probe_read(int64_t src_dev, int64_t bytes) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (bytes < 0 || (bytes > 0 && !src_dev)) return fail(DMC_HIP_EINVAL, "bad probe range");
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    if (!c.sink) HIP_TRY(hipMalloc(&c.sink, dmc::probe_sink_bytes()), "hipMalloc(probe sink)");
+    hipError_t e = dmc::launch_probe_read(reinterpret_cast<const void *>(src_dev), bytes, c.sink, c.stream);
+    if (e != hipSuccess) return hip_fail(e, "probe launch");
+    return DMC_HIP_OK;
+}
+
 int32_t dmc_hip_synchronize(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     int rc = ensure_init();
@@ -608,8 +621,8 @@ int32_t dmc_hip_synchronize(void) {
 }
 
 int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k, int64_t n,
-                     int64_t batch, int64_t rs, int64_t *out6) {
-    if (!out6 || !valid_dims(m, k, n) || batch < 0 || rs < 0) return fail(DMC_HIP_EINVAL, "bad plan query");
+                     int64_t batch, int64_t rs, int64_t *out8) {
+    if (!out8 || !valid_dims(m, k, n) || batch < 0 || rs < 0) return fail(DMC_HIP_EINVAL, "bad plan query");
     int cus;
     {
         std::lock_guard<std::mutex> lk(g_mu);
@@ -619,14 +632,15 @@ int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t 
         dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_addr), k, reinterpret_cast<const float *>(x_addr),
                          k, nullptr, n, m, k, n};
         const dmc::RdPlan pl = dmc::plan_rd(p, cus);
-        const int64_t v[6] = {pl.vec, pl.rows, pl.mt, pl.grid_x, 1, 0};
-        memcpy(out6, v, sizeof v);
+        const int64_t v[8] = {pl.vec, pl.rows, pl.mt, pl.grid_x, pl.kvec, 0, pl.waves, pl.rpw};
+        memcpy(out8, v, sizeof v);
     } else {
         dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_addr), reinterpret_cast<const float *>(x_addr),
                          nullptr, m, k, n, batch, 0, rs};
         const dmc::CsPlan pl = dmc::plan_cs(p, cus);
-        const int64_t v[6] = {pl.vec, pl.rw, pl.mt, pl.grid_x, pl.slices, (int64_t)pl.workspace_bytes};
-        memcpy(out6, v, sizeof v);
+        const int64_t v[8] = {pl.vec, pl.rw, pl.mt, pl.grid_x, pl.slices, (int64_t)pl.workspace_bytes,
+                              4, pl.cb};
+        memcpy(out8, v, sizeof v);
     }
     return DMC_HIP_OK;
 }

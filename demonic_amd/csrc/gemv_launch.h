@@ -39,10 +39,21 @@ struct CsProblem {
 
 // Launch shape chosen for a problem; exposed so the host library can report
 // and test its planning without a device.
+//
+// Two row-dot kernels:
+//   streaming (vec == 8, k <= 32768): the workgroup's `waves` waves split k,
+//     each lane keeps its slice of x in registers for the whole workgroup, and
+//     the workgroup walks `rpw` consecutive weight rows, `rows` at a time,
+//     with the next rows' weights in flight while the current ones are summed;
+//   general (any alignment or k): 4 waves split k of `rows` rows, x re-read
+//     per chunk.
 struct RdPlan {
     int vec;    // bf16 elements per lane per weight load (8 = 128-bit loads)
-    int rows;   // output rows per workgroup
+    int rows;   // weight rows per step (streaming) / per workgroup (general)
     int mt;     // activation rows per workgroup (skinny-M tile)
+    int waves;  // waves per workgroup
+    int kvec;   // 8-element vectors of k per lane (streaming), 0 = general kernel
+    int rpw;    // weight rows per workgroup
     int64_t grid_x, grid_y;
 };
 
@@ -63,6 +74,13 @@ CsPlan plan_cs(const CsProblem &p, int num_cus);
 // Enqueue on `stream`.  `workspace` must hold plan.workspace_bytes when
 // plan.slices > 1.  Returns hipSuccess or the launch error.
 hipError_t launch_rd(const RdProblem &p, const RdPlan &plan, hipStream_t stream);
+
 hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hipStream_t stream);
+
+// Measurement probe: a read-only nontemporal pass over [src, src+bytes) in
+// 16-byte granules (bytes == 0: an empty launch, the dispatch floor).  `sink`
+// holds probe_sink_bytes().
+size_t probe_sink_bytes();
+hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
 
 }  // namespace dmc

@@ -126,10 +126,22 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
 int32_t dmc_hip_synchronize(void);
 
 /* Launch plan a GEMV would use on this device (or on a 256-CU gfx950 when no
- * device is present), for tests and reports.  out6 receives
- * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes}. */
+ * device is present), for tests and reports.  out8 receives
+ * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes, waves, rows_per_group}:
+ * for the row-dot layout kvec-streaming plans report waves = 1..8 and
+ * rows_per_group = weight rows per workgroup; `slices` is then the number of
+ * 8-element k vectors per lane (0 for the general kernel). */
 int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k,
-                     int64_t n, int64_t batch, int64_t rs, int64_t *out6);
+                     int64_t n, int64_t batch, int64_t rs, int64_t *out8);
+
+/* Measurement probe for reports: enqueue a read-only pass over the device
+ * range [src_dev, src_dev + bytes) with the same nontemporal 128-bit loads
+ * the GEMV kernels use (the stream-read ceiling of the GEMV's weight
+ * traffic); bytes == 0 enqueues an empty launch (the dispatch floor).  No
+ * reference counterpart: it reproduces nothing in demoniC and exists so a
+ * report can state a GEMV's bandwidth as a fraction of what a pure read
+ * reaches on the same device. */
+int32_t dmc_hip_probe_read(int64_t src_dev, int64_t bytes);
 
 /* HIP events on the library stream, for timing device work. */
 int64_t dmc_hip_event_create(void);

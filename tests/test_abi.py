@@ -86,12 +86,34 @@ def test_rowdot_vector_width_follows_alignment(k, align, vec):
 
 
 def test_rowdot_plans_at_decode_shapes():
+    # streaming kernel: 8 waves split k = 4096 one 8-element vector per lane,
+    # 4 weight rows per workgroup, 2 per step
     up = d.plan("rd", 1, 4096, 14336, x_addr=256, w_addr=256)
-    assert (up.vec, up.rows_or_rw, up.mt, up.grid_x) == (8, 4, 1, 3584)
+    assert (up.vec, up.waves, up.slices, up.rows_per_group, up.rows_or_rw, up.mt, up.grid_x) == \
+        (8, 8, 1, 4, 2, 1, 3584)
+    down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
+    assert (down.waves, down.slices, down.grid_x) == (8, 4, 1024)  # ceil(14336 / 4096) vectors
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
-    for m, mt in [(1, 1), (2, 2), (3, 4), (5, 8), (16, 16), (17, 16)]:
+    # activation rows held in registers: MT * vectors-per-lane <= 8
+    for m, mt in [(1, 1), (2, 2), (3, 4), (5, 8), (16, 8), (17, 8)]:
         assert d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256).mt == mt
+    assert d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256).mt == 2
+
+
+@pytest.mark.parametrize("k,waves,kvec", [(8, 1, 1), (512, 1, 1), (520, 2, 1), (1024, 2, 1),
+                                          (2048, 4, 1), (4096, 8, 1), (4104, 8, 2),
+                                          (11008, 8, 3), (32768, 8, 8)])
+def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
+    p = d.plan("rd", 1, k, 1000, x_addr=256, w_addr=256)
+    assert (p.waves, p.slices) == (waves, kvec), p
+    assert waves * kvec * 512 >= k > (waves * kvec - waves) * 512 or kvec == 1
+
+
+def test_rowdot_falls_back_to_general_kernel():
+    for k, w in [(32776, 256), (4097, 256), (4096, 258), (0, 256)]:
+        p = d.plan("rd", 1, k, 1000, x_addr=256, w_addr=w)
+        assert p.slices == 0 and p.waves == 4, (k, w, p)
 
 
 def test_column_stream_plans_split_k_and_size_workspace():
