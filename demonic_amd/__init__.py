@@ -248,7 +248,8 @@ class Plan:
     slices: int            # cs: k slices; rd: 8-element k vectors per lane (0 = general kernel)
     workspace_bytes: int
     waves: int
-    rows_per_group: int    # rd: weight rows per workgroup; cs: columns per workgroup
+    rows_per_group: int    # rd: weight rows per workgroup; cs: k rows per workgroup
+                           # (streaming kernel) or columns per workgroup (general)
 
 
 def plan(layout: str, m: int, k: int, n: int, batch: int = 1, rs: int = 0,

@@ -417,6 +417,125 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
     }
 }
 
+// ---- CS streaming: W [K,N], N % 8 == 0, 16-byte aligned rows ------------------
+//
+// Workgroup (cb, s, z) owns output columns [cb*512, +512) of batch slice z and
+// k rows [s*kslice, +kslice).  Lane l owns columns cb*512 + 8l .. +8 and loads
+// them 16 bytes at a time (nontemporal); the NW waves take contiguous chunks
+// of the workgroup's k rows, so x[m][k] is the same for the whole wave and
+// comes through the scalar cache.  The waves' partials meet in LDS in a fixed
+// order; with one k slice the workgroup writes y, otherwise its partial goes
+// to P[s] and sum_slices_stream_kernel adds the slices in slice order.
+// (Finishing inside the same launch needs device-scope fences, which on a
+// multi-XCD part write back and invalidate the whole L2 per workgroup:
+// measured 5x slower than the second launch.)
+constexpr int kCsCols = 512;
+
+template <int NW, int MT>
+__global__ void __launch_bounds__(64 * NW)
+gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restrict__ X, int64_t ls,
+                      float *__restrict__ Y, float *__restrict__ P, int64_t z_stride, int64_t p_slice, int N,
+                      int K, int M, int kslice, int slices) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cb = blockIdx.x;
+    const int s = blockIdx.y;
+    const int64_t z = blockIdx.z;
+    const int col = cb * kCsCols + lane * 8;
+    const bool live = col < N;
+
+    const int kb = s * kslice;
+    const int ke = min(K, kb + kslice);
+    const int per = (ke - kb + NW - 1) / NW;
+    const int r0 = min(ke, kb + wave * per);
+    const int r1 = min(ke, r0 + per);
+
+    const float *xz = X + z * ls;
+    const __amdgpu_buffer_rsrc_t rsw =
+        weight_rsrc(W + z * rs + (int64_t)r0 * N, (uint32_t)((int64_t)(r1 - r0) * N * 2));
+    const uint32_t row_bytes = (uint32_t)N * 2;
+    const uint32_t lane_off = (uint32_t)col * 2;
+
+    // +0.0f when this lane sums at least one product (or K == 0, which must
+    // write +0.0f), -0.0f, the additive identity, otherwise.
+    const float init = ((r0 < r1 && live) || K == 0) ? 0.0f : -0.0f;
+    float acc[MT][8];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[m][e] = init;
+
+    auto consume = [&](const u32x4 &wv, int k) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float xv = xz[(int64_t)min(m, M - 1) * K + k];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t d = wv[e >> 1];
+                acc[m][e] = fmaf(xv, (e & 1) ? widen_hi(d) : widen_lo(d), acc[m][e]);
+            }
+        }
+    };
+
+    constexpr int U = MT <= 2 ? 8 : 4;
+    int r = r0;
+    if (live) {
+        for (; r + U <= r1; r += U) {
+            u32x4 wv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) wv[u] = load_w16(rsw, (uint32_t)(r - r0 + u) * row_bytes + lane_off);
+#pragma unroll
+            for (int u = 0; u < U; ++u) consume(wv[u], r + u);
+        }
+        for (; r < r1; ++r) consume(load_w16(rsw, (uint32_t)(r - r0) * row_bytes + lane_off), r);
+    }
+
+    __shared__ float red[NW][MT][kCsCols];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wave][m][lane * 8 + e] = acc[m][e];
+    __syncthreads();
+
+    const int c0 = cb * kCsCols;
+    const int ncol = min(kCsCols, N - c0);
+    float *out = slices == 1 ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
+    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {
+        const int m = t / kCsCols, c = t - m * kCsCols;
+        if (m >= M || c >= ncol) continue;
+        float v = red[0][m][c];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[w][m][c];
+        out[(int64_t)m * N + c0 + c] = v;
+    }
+}
+
+// Second pass of the streaming column-stream kernel: y[i] = sum over slices
+// of P[j][i] in ascending j.  A workgroup owns 64 consecutive outputs; its 4
+// waves take slices j = w, w+4, ... (coalesced 256-byte reads), and the four
+// partial sums meet in LDS in wave order.  Every element's order is fixed.
+__global__ void __launch_bounds__(256)
+sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
+                         int64_t count) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+    float s = -0.0f;
+    bool first = true;
+    if (i < count) {
+#pragma unroll 8
+        for (int j = wave; j < slices; j += 4) {
+            const float v = P[(int64_t)j * p_slice + i];
+            s = first ? v : s + v;
+            first = false;
+        }
+    }
+    __shared__ float part[4][64];
+    part[wave][lane] = s;
+    __syncthreads();
+    if (wave == 0 && i < count) Y[i] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+}
+
 // Second CS pass: y[i] = sum over slices in ascending order of P[s][i].
 __global__ void __launch_bounds__(kThreads)
 sum_slices_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
@@ -589,6 +708,35 @@ hipError_t cs_mt(const CsProblem &p, const CsPlan &pl, float *P, int64_t ps, int
     return hipErrorInvalidValue;
 }
 
+template <int NW, int MT>
+hipError_t css_go(const CsProblem &p, const CsPlan &pl, float *P, int64_t z0, int64_t nz, int64_t m0,
+                  int64_t mc, hipStream_t s) {
+    const int64_t zs = p.m * p.n;
+    hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.slices, (unsigned)nz),
+                       dim3(64 * NW), 0, s, p.w + z0 * p.rs, p.rs, p.x + z0 * p.ls + m0 * p.k, p.ls,
+                       p.y + z0 * zs + m0 * p.n, P ? P + z0 * zs + m0 * p.n : nullptr, zs, p.batch * zs,
+                       (int)p.n, (int)p.k, (int)mc, (int)pl.kslice, (int)pl.slices);
+    return hipGetLastError();
+}
+
+hipError_t css_dispatch(const CsProblem &p, const CsPlan &pl, float *P, int64_t z0, int64_t nz, int64_t m0,
+                        int64_t mc, hipStream_t s) {
+#define DMC_CSS(NW)                                                 \
+    switch (pl.mt) {                                                \
+    case 1: return css_go<NW, 1>(p, pl, P, z0, nz, m0, mc, s);      \
+    case 2: return css_go<NW, 2>(p, pl, P, z0, nz, m0, mc, s);      \
+    case 4: return css_go<NW, 4>(p, pl, P, z0, nz, m0, mc, s);      \
+    }                                                               \
+    return hipErrorInvalidValue;
+    switch (pl.waves) {
+    case 2: DMC_CSS(2)
+    case 4: DMC_CSS(4)
+    case 8: DMC_CSS(8)
+    }
+#undef DMC_CSS
+    return hipErrorInvalidValue;
+}
+
 hipError_t cs_dispatch(const CsProblem &p, const CsPlan &pl, float *P, int64_t ps, int64_t z0,
                        int64_t nz, int64_t m0, int64_t mc, hipStream_t s) {
     if (pl.vec == 8 && pl.rw == 4) return cs_mt<8, 4>(p, pl, P, ps, z0, nz, m0, mc, s);
@@ -666,6 +814,45 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
             break;
         }
     }
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    const int64_t batch = std::max<int64_t>(p.batch, 1);
+    const int64_t kmax = std::max<int64_t>(p.k, 1);
+
+    // Streaming kernel: 128-bit column vectors.
+    if (pl.vec == 8 && env_int("DMC_HIP_CS_STREAM", 1) != 0) {
+        int nw = env_int("DMC_HIP_CS_WAVES", 4);
+        if (nw != 2 && nw != 4 && nw != 8) nw = 4;
+        pl.stream = true;
+        pl.waves = nw;
+        pl.rw = 1;
+        pl.mt = std::min(mt_for(p.m), 4);
+        pl.cb = kCsCols;
+        pl.grid_x = (p.n + kCsCols - 1) / kCsCols;
+        // Split k so the launch has ~4 workgroups per CU (env-tunable), each
+        // wave with at least 8 rows.
+        const int64_t groups = pl.grid_x * std::min<int64_t>(batch, 32768) * ((p.m + pl.mt - 1) / pl.mt);
+        const int64_t target = (int64_t)env_int("DMC_HIP_CS_GROUPS_PER_CU", 4) * cus;
+        const int64_t want = std::max<int64_t>(1, (target + groups - 1) / groups);
+        int64_t kslice = (kmax + want - 1) / want;
+        kslice = std::max<int64_t>(kslice, 8 * nw);
+        kslice = (kslice + nw - 1) / nw * nw;
+        kslice = std::max<int64_t>(nw, env_int("DMC_HIP_CS_KSLICE", (int)std::min<int64_t>(kslice, INT32_MAX)));
+        pl.kslice = kslice;
+        pl.slices = (kmax + kslice - 1) / kslice;
+        // A wave's rows must fit a 32-bit buffer range; the grid's y extent
+        // is limited to 65535.
+        const int64_t per_wave = (kslice + nw - 1) / nw;
+        if (pl.slices <= 65535 && per_wave * p.n * 2 <= INT32_MAX) {
+            pl.workspace_bytes = pl.slices > 1 ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
+            return pl;
+        }
+        pl = CsPlan{};
+        pl.vec = 8;
+    }
+
+    // General kernel with a second summation pass.
+    pl.stream = false;
+    pl.waves = kWaves;
     pl.rw = pl.vec == 8 ? 4 : 1;
     const int rw = env_int("DMC_HIP_CS_RW", pl.rw);
     if (pl.vec == 8 && (rw == 1 || rw == 4)) pl.rw = rw;
@@ -675,15 +862,11 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
     // Split k so the launch has ~8 workgroups per CU, with at least 64 k rows
     // per workgroup (a multiple of the 4*RW rows one workgroup step covers).
     const int64_t step = (int64_t)kWaves * pl.rw;
-    const int64_t cus = num_cus > 0 ? num_cus : 256;
-    const int64_t groups = pl.grid_x * std::max<int64_t>(p.batch, 1);
+    const int64_t groups = pl.grid_x * batch;
     int64_t want = (8 * cus + groups - 1) / groups;
-    const int64_t kmax = std::max<int64_t>(p.k, 1);
     int64_t kslice = (kmax + want - 1) / want;
     kslice = std::max<int64_t>(kslice, 64);
     kslice = (kslice + step - 1) / step * step;
-    kslice = env_int("DMC_HIP_CS_KSLICE", (int)kslice);
-    if (kslice < step) kslice = step;
     pl.kslice = kslice;
     pl.slices = (kmax + kslice - 1) / kslice;
     if (pl.slices > 65535) {  // grid.y limit
@@ -692,8 +875,7 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         pl.kslice = (pl.kslice + step - 1) / step * step;
         pl.slices = (kmax + pl.kslice - 1) / pl.kslice;
     }
-    pl.workspace_bytes =
-        pl.slices > 1 ? (size_t)pl.slices * (size_t)std::max<int64_t>(p.batch, 1) * p.m * p.n * 4 : 0;
+    pl.workspace_bytes = pl.slices > 1 ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
     return pl;
 }
 
@@ -711,6 +893,25 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
 
 hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipStream_t s) {
     if (p.m <= 0 || p.n <= 0 || p.batch <= 0) return hipSuccess;
+    const int64_t zmax_s = 32768;  // grid.z limit, with margin
+    if (pl.stream) {
+        float *P = pl.slices > 1 ? static_cast<float *>(workspace) : nullptr;
+        for (int64_t z0 = 0; z0 < p.batch; z0 += zmax_s) {
+            const int64_t nz = std::min(zmax_s, p.batch - z0);
+            for (int64_t m0 = 0; m0 < p.m; m0 += pl.mt) {
+                const int64_t mc = std::min<int64_t>(pl.mt, p.m - m0);
+                hipError_t e = css_dispatch(p, pl, P, z0, nz, m0, mc, s);
+                if (e != hipSuccess) return e;
+            }
+        }
+        if (pl.slices > 1) {
+            const int64_t total = p.m * p.n * p.batch;
+            hipLaunchKernelGGL(sum_slices_stream_kernel, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, s, P,
+                               total, (int)pl.slices, p.y, total);
+            return hipGetLastError();
+        }
+        return hipSuccess;
+    }
     const int64_t per_z = p.m * p.n;
     const int64_t total = per_z * p.batch;
     float *P = pl.slices > 1 ? static_cast<float *>(workspace) : p.y;

@@ -57,13 +57,21 @@ struct RdPlan {
     int64_t grid_x, grid_y;
 };
 
+// Two column-stream kernels:
+//   streaming (vec == 8): lanes own 8 columns, a workgroup owns 512 columns
+//     and a k slice, `waves` waves split the slice;
+//   general (any N): 4 waves, RW k rows per wave-wide load.
+// Either way, when k is split over several workgroups a second launch sums
+// the slice partials in slice order.
 struct CsPlan {
     int vec;        // bf16 columns per lane per load
     int rw;         // k-rows covered by one wave-wide load
     int mt;         // activation rows per workgroup
     int cb;         // output columns per workgroup
+    int waves;      // waves per workgroup
+    bool stream;    // streaming kernel
     int64_t kslice; // k rows per workgroup (split-K)
-    int64_t slices; // number of k slices (1 = no second pass)
+    int64_t slices; // number of k slices (1 = no reduction across workgroups)
     int64_t grid_x;
     size_t workspace_bytes;  // partial sums when slices > 1
 };

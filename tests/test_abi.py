@@ -117,13 +117,20 @@ def test_rowdot_falls_back_to_general_kernel():
 
 
 def test_column_stream_plans_split_k_and_size_workspace():
+    # streaming kernel: 512 columns per workgroup, k split so ~4 workgroups per CU
     p = d.plan("cs", 1, 14336, 4096, x_addr=256, w_addr=256)
-    assert p.vec == 8 and p.slices > 1
+    assert p.vec == 8 and p.waves == 4 and p.grid_x == 8 and p.slices > 1
     assert p.workspace_bytes == p.slices * 4096 * 4
-    one = d.plan("cs", 1, 64, 4096, x_addr=256, w_addr=256)
+    assert p.grid_x * p.slices >= 1024 - p.grid_x
+    assert p.rows_per_group * p.slices >= 14336 > p.rows_per_group * (p.slices - 1)
+    up = d.plan("cs", 1, 4096, 14336, x_addr=256, w_addr=256)
+    assert up.grid_x == 28 and up.rows_per_group % 4 == 0
+    one = d.plan("cs", 1, 32, 4096, x_addr=256, w_addr=256)  # >= 8 k rows per wave
     assert one.slices == 1 and one.workspace_bytes == 0
+    assert d.plan("cs", 16, 4096, 4096, x_addr=256, w_addr=256).mt == 4
+    # general kernel for N not a multiple of 8
     odd = d.plan("cs", 1, 4097, 11007, x_addr=256, w_addr=256)
-    assert odd.vec == 1
+    assert odd.vec == 1 and odd.waves == 4
     zero_k = d.plan("cs", 1, 0, 512, x_addr=256, w_addr=256)
     assert zero_k.slices == 1
 

@@ -296,3 +296,33 @@ def test_repeat_calls_bit_identical(hip, layout):
     a = run(hip, x, w)
     b = run(hip, x, w)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- column-stream split-K finish (last workgroup sums the slices) ----------------------
+
+@pytest.mark.parametrize("m,k,n,batch", [(1, 3000, 1032, 1), (9, 3000, 1032, 1), (1, 2048, 520, 40),
+                                         (3, 14336, 4096, 1), (2, 777, 8, 5)])
+def test_cs_split_k_counters_reset(hip, m, k, n, batch):
+    """Several calls in a row through the split-K streaming kernel: each must
+    match the oracle and repeat bit for bit (the slice counters return to zero
+    after every launch; a stale counter would finish a column block early)."""
+    rng = np.random.default_rng(m * 131 + k + n + batch)
+    ls, rs = m * k, k * n
+    x = rng.standard_normal(batch * m * k).astype(np.float32)
+    w = W.bf16_rne(np.float32(0.05) * rng.standard_normal(batch * k * n).astype(np.float32))
+    plan = hip.plan("cs", m, k, n, batch=batch, rs=rs, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert plan.vec == 8 and plan.waves > 0
+    if k >= 2048:
+        assert plan.slices > 1, plan
+    ref_parts = []
+    for z in range(batch):
+        ref_parts.append(oracle.matmul_bf16(x[z * ls:(z + 1) * ls].reshape(m, k),
+                                            w[z * rs:(z + 1) * rs].reshape(k, n)).reshape(-1))
+    y_ref = np.concatenate(ref_parts)
+    first = None
+    for _ in range(3):
+        y = hip.matmul_bf16_gpu_batched(x, w, m, k, n, batch, ls, rs)
+        check(y, y_ref, what=f"cs split-K m={m} k={k} n={n} batch={batch}")
+        if first is None:
+            first = y.copy()
+        assert np.array_equal(y.view(np.uint32), first.view(np.uint32))
