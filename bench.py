@@ -30,6 +30,7 @@ cpu_baseline  the oracle's restatement of the reference CPU kernel
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -144,7 +145,8 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extended", action="store_true",
-                    help="also time C1, C4, C5 and the column-stream layout (stderr + 'extended')")
+                    help="also time C1, C3, C4, C5 and the column-stream layout (stderr + 'extended')")
+    ap.add_argument("--c3", action="store_true", help="also time C3, the 32-layer decode sweep")
     a = ap.parse_args(argv)
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -243,6 +245,8 @@ def main(argv=None) -> int:
     }
     if a.extended:
         result["extended"] = extended(d, W, a.steps)
+    if a.extended or a.c3:
+        result["c3"] = c3(d, W)
     print(json.dumps(result), flush=True)
     return 0
 
@@ -302,6 +306,82 @@ def extended(d, W, reps: int) -> dict:
             f(0)
             record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
             s.free()
+    return out
+
+
+def c3(d, W, tokens: int = 10) -> dict:
+    """C3: one decode token = 32 layers x 7 row-dot GEMVs of Llama-3-8B
+    (13.97 GB of bf16 weights, generated in HBM by the counter generator),
+    each layer's activations drawn from the seed.  Scheduled as a decode step
+    would be: q/k/v in one grouped launch, o, gate/up in one grouped launch,
+    down -- 4 launches per layer -- and replayed from a HIP graph.  Also timed:
+    the same token as 7 single launches per layer."""
+    lib = d._lib.load()
+    t = time.perf_counter()
+    table = d.DeviceBuffer.from_numpy(W.normal_table(W.C3_SCALE))
+    names = [nm for nm, _, _ in W.LLAMA3_8B_LAYER]
+    shape = {nm: (n, k) for nm, n, k in W.LLAMA3_8B_LAYER}
+    layers = []
+    for layer in range(W.LLAMA3_8B_LAYERS):
+        ws = {}
+        for idx, nm in enumerate(names):
+            n, k = shape[nm]
+            ws[nm] = d.DeviceBuffer(2 * n * k)
+            d.fill_counter_bf16(ws[nm], n * k, W.counter_seed(0, W.c3_tensor(layer, idx)), table)
+        layers.append((ws, d.DeviceBuffer.from_numpy(W.c3_x(layer, 4096)),
+                       d.DeviceBuffer.from_numpy(W.c3_x(layer, 14336))))
+    ys = {nm: d.DeviceBuffer(4 * shape[nm][0]) for nm in names}
+    d.synchronize()
+    log(f"C3 weights generated in HBM in {time.perf_counter() - t:.1f}s")
+    b_token = sum(b_alg(*shape[nm]) for nm in names) * W.LLAMA3_8B_LAYERS
+
+    def arr(v):
+        return (ctypes.c_int64 * len(v))(*v)
+
+    grouped_calls, single_calls = [], []
+    for ws, x, x2 in layers:
+        def g(nms, xb):
+            return (len(nms), arr([xb.addr] * len(nms)), arr([ws[nm].addr for nm in nms]),
+                    arr([ys[nm].addr for nm in nms]), arr([shape[nm][0] for nm in nms]), 1, shape[nms[0]][1])
+        grouped_calls += [g(["q", "k", "v"], x), g(["o"], x), g(["gate", "up"], x), g(["down"], x2)]
+        for nm in names:
+            xb = x2 if nm == "down" else x
+            single_calls.append((xb.addr, ws[nm].addr, ys[nm].addr, 1, shape[nm][1], shape[nm][0]))
+
+    def run_grouped():
+        for c in grouped_calls:
+            d._lib.check(lib.dmc_hip_gemv_rd_grouped(*c))
+
+    def run_single():
+        for c in single_calls:
+            d._lib.check(lib.dmc_hip_gemv_rd(*c))
+
+    out = {"tokens": tokens, "bytes_per_token": b_token}
+    for label, fn, launches in (("grouped_4_per_layer", run_grouped, 4), ("single_7_per_layer", run_single, 7)):
+        fn()
+        d.synchronize()
+        g = d.Graph()
+        with g:
+            fn()
+        g.launch()
+        d.synchronize()
+        ms_graph = batch_us(d, lambda i: g.launch(), tokens) / 1e3
+        ms_eager = batch_us(d, lambda i: fn(), tokens) / 1e3
+        g.destroy()
+        gbs = b_token / (ms_graph * 1e-3) / 1e9
+        out[label] = {"launches_per_token": launches * W.LLAMA3_8B_LAYERS, "ms_per_token_graph": round(ms_graph, 4),
+                      "ms_per_token_eager": round(ms_eager, 4), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"C3 {label}: graph {ms_graph:.3f} ms/token ({gbs:.0f} GB/s, {gbs / PEAK_GBS:.1%}), "
+            f"eager {ms_eager:.3f} ms/token")
+    for nm in names:
+        y = ys[nm].download(np.float32, (shape[nm][0],))
+        assert np.all(np.isfinite(y)), nm  # parity of the sweep lives in tests/
+    for ws, x, x2 in layers:
+        for b in list(ws.values()) + [x, x2]:
+            b.free()
+    for b in list(ys.values()) + [table]:
+        b.free()
     return out
 
 

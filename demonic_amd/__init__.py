@@ -24,7 +24,7 @@ __all__ = [
     "BackendMissing", "HipError", "available", "gemv_selected", "MIN_MACS",
     "matmul_bf16_gpu", "matmul_bf16_gpu_t", "matmul_bf16_gpu_batched",
     "matmul_bf16_gpu_batched_deferred", "flush", "DeviceBuffer", "gemv_cs", "gemv_rd",
-    "synchronize", "probe_read", "Event", "plan", "register_weight", "release_weights",
+    "synchronize", "probe_read", "gemv_rd_grouped", "fill_counter_bf16", "Graph", "Event", "plan", "register_weight", "release_weights",
     "resident_count", "resident_bytes", "device_info",
 ]
 
@@ -200,6 +200,26 @@ def gemv_rd(x, w, y, m: int, k: int, n: int) -> None:
     _lib.check(_lib.load().dmc_hip_gemv_rd(_addr(x), _addr(w), _addr(y), m, k, n))
 
 
+def gemv_rd_grouped(xs, ws, ys, ns, m: int, k: int) -> None:
+    """Enqueue y_i = x_i @ bf16(w_i)' for independent problems sharing m and k
+    (w_i [n_i, k] row-dot weights), one launch per 8 problems."""
+    cnt = len(ns)
+    if not (len(xs) == len(ws) == len(ys) == cnt):
+        raise ValueError("xs, ws, ys and ns must have the same length")
+    arr = lambda v: (ctypes.c_int64 * max(cnt, 1))(*[int(a) for a in v])  # noqa: E731
+    _lib.check(_lib.load().dmc_hip_gemv_rd_grouped(
+        cnt, arr(_addr(b) for b in xs), arr(_addr(b) for b in ws), arr(_addr(b) for b in ys),
+        arr(ns), m, k))
+
+
+def fill_counter_bf16(dst, count: int, key: int, table, offset: int = 0) -> None:
+    """Fill a device region with counter-generated bf16 bits (the generator of
+    workloads.counter_bf16, run in HBM); `table` is a device copy of the
+    65,536-entry table."""
+    _lib.check(_lib.load().dmc_hip_fill_counter_bf16(_addr(dst), count, offset, key & ((1 << 64) - 1),
+                                                     _addr(table)))
+
+
 def synchronize() -> None:
     _lib.check(_lib.load().dmc_hip_synchronize())
 
@@ -209,6 +229,40 @@ def probe_read(buf, nbytes: int | None = None) -> None:
     probe); nbytes=0 enqueues an empty launch (the dispatch floor)."""
     n = buf.nbytes if nbytes is None else int(nbytes)
     _lib.check(_lib.load().dmc_hip_probe_read(_addr(buf) if n else 0, n))
+
+
+class Graph:
+    """A captured sequence of device-pointer GEMVs, replayed with one call.
+
+        with Graph() as g:      # capture
+            gemv_rd(...); gemv_rd_grouped(...)
+        g.launch()              # replay on the library stream
+    """
+
+    def __init__(self):
+        self.exec = 0
+
+    def __enter__(self):
+        _lib.check(_lib.load().dmc_hip_capture_begin())
+        return self
+
+    def __exit__(self, exc_type, *exc):
+        ex = _lib.load().dmc_hip_capture_end()
+        if exc_type is None:
+            if not ex:
+                _lib.check(-4)
+            self.exec = ex
+        elif ex:
+            _lib.load().dmc_hip_graph_destroy(ex)
+        return False
+
+    def launch(self) -> None:
+        _lib.check(_lib.load().dmc_hip_graph_launch(self.exec))
+
+    def destroy(self) -> None:
+        if self.exec:
+            _lib.check(_lib.load().dmc_hip_graph_destroy(self.exec))
+            self.exec = 0
 
 
 class Event:

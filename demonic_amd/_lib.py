@@ -38,7 +38,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dmc_hip_gemv_rd": (i32, [i64] * 6),
     "dmc_hip_synchronize": (i32, []),
     "dmc_hip_probe_read": (i32, [i64, i64]),
+    "dmc_hip_gemv_rd_grouped": (i32, [i64, ctypes.POINTER(i64), ctypes.POINTER(i64),
+                                      ctypes.POINTER(i64), ctypes.POINTER(i64), i64, i64]),
+    "dmc_hip_fill_counter_bf16": (i32, [i64, i64, i64, ctypes.c_uint64, i64]),
     "dmc_hip_plan": (i32, [i32, i64, i64, i64, i64, i64, i64, i64, ctypes.POINTER(i64)]),
+    "dmc_hip_capture_begin": (i32, []),
+    "dmc_hip_capture_end": (i64, []),
+    "dmc_hip_graph_launch": (i32, [i64]),
+    "dmc_hip_graph_destroy": (i32, [i64]),
     "dmc_hip_event_create": (i64, []),
     "dmc_hip_event_record": (i32, [i64]),
     "dmc_hip_event_synchronize": (i32, [i64]),

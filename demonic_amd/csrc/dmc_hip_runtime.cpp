@@ -19,6 +19,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
@@ -609,6 +610,102 @@ int32_t dmc_hip_probe_read(int64_t src_dev, int64_t bytes) {
     if (!c.sink) HIP_TRY(hipMalloc(&c.sink, dmc::probe_sink_bytes()), "hipMalloc(probe sink)");
     hipError_t e = dmc::launch_probe_read(reinterpret_cast<const void *>(src_dev), bytes, c.sink, c.stream);
     if (e != hipSuccess) return hip_fail(e, "probe launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int64_t *w_devs,
+                                const int64_t *y_devs, const int64_t *ns, int64_t m, int64_t k) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (count < 0 || (count > 0 && (!x_devs || !w_devs || !y_devs || !ns)) || !valid_dims(m, k, 0))
+        return fail(DMC_HIP_EINVAL, "bad grouped GEMV arguments");
+    for (int64_t i = 0; i < count; ++i) {
+        if (ns[i] < 0 || ns[i] > INT32_MAX) return fail(DMC_HIP_EINVAL, "bad grouped GEMV row count");
+        if (m > 0 && ns[i] > 0 && (!y_devs[i] || (k > 0 && (!x_devs[i] || !w_devs[i]))))
+            return fail(DMC_HIP_EINVAL, "null pointer in grouped GEMV");
+    }
+    if (count == 0 || m == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    for (int64_t b = 0; b < count; b += dmc::kMaxGroup) {
+        dmc::RdGroup g{};
+        g.count = (int)std::min<int64_t>(dmc::kMaxGroup, count - b);
+        g.m = m;
+        g.k = k;
+        for (int i = 0; i < g.count; ++i) {
+            g.w[i] = reinterpret_cast<const uint16_t *>(w_devs[b + i]);
+            g.x[i] = reinterpret_cast<const float *>(x_devs[b + i]);
+            g.y[i] = reinterpret_cast<float *>(y_devs[b + i]);
+            g.n[i] = ns[b + i];
+        }
+        const dmc::RdPlan gp = dmc::plan_rd_group(g, c.cus);
+        if (gp.kvec > 0) {
+            hipError_t e = dmc::launch_rd_group(g, gp, c.stream);
+            if (e != hipSuccess) return hip_fail(e, "grouped kernel launch");
+            continue;
+        }
+        for (int i = 0; i < g.count; ++i) {  // outside the streaming kernel's range: one launch each
+            if (g.n[i] == 0) continue;
+            dmc::RdProblem p{g.w[i], k, g.x[i], k, g.y[i], g.n[i], m, k, g.n[i]};
+            hipError_t e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+            if (e != hipSuccess) return hip_fail(e, "kernel launch");
+        }
+    }
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_fill_counter_bf16(int64_t dst_dev, int64_t count, int64_t offset, uint64_t key,
+                                  int64_t table_dev) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (count < 0 || offset < 0 || (count > 0 && (!dst_dev || !table_dev)))
+        return fail(DMC_HIP_EINVAL, "bad fill arguments");
+    if (count == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = dmc::launch_fill_counter_bf16(reinterpret_cast<uint16_t *>(dst_dev), count, offset, key,
+                                                 reinterpret_cast<const uint16_t *>(table_dev), ctx().stream);
+    if (e != hipSuccess) return hip_fail(e, "fill launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_capture_begin(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    int rc = ensure_init();
+    if (rc) return rc;
+    HIP_TRY(hipStreamBeginCapture(ctx().stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    return DMC_HIP_OK;
+}
+
+int64_t dmc_hip_capture_end(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (ensure_init()) return 0;
+    hipGraph_t graph = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx().stream, &graph);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture (an entry that allocates or waits was "
+                                            "called while capturing)"), 0;
+    hipGraphExec_t exec = nullptr;
+    e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate"), 0;
+    return reinterpret_cast<int64_t>(exec);
+}
+
+int32_t dmc_hip_graph_launch(int64_t exec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!exec) return fail(DMC_HIP_EINVAL, "null graph");
+    int rc = ensure_init();
+    if (rc) return rc;
+    HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), ctx().stream), "hipGraphLaunch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_graph_destroy(int64_t exec) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!exec) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)), "hipGraphExecDestroy");
     return DMC_HIP_OK;
 }
 

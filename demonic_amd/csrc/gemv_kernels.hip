@@ -135,6 +135,9 @@ __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w
 
 // ---- RD streaming: W [N,K], 16-byte aligned rows, K <= 32768 ------------------
 //
+// One launch serves up to kMaxGroup independent problems sharing K and M
+// (a single GEMV is a group of one); each workgroup first finds its problem.
+//
 // The NW waves of a workgroup split k: lane `lane` of wave `wave` owns the
 // KV vectors of 8 elements starting at ((j*NW + wave)*64 + lane)*8, j < KV, so
 // for every j the workgroup reads NW*1 KiB of a row contiguously.  The lane
@@ -145,13 +148,30 @@ __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w
 // barrier at the end, then a fixed-order sum over the waves.
 constexpr int kMaxRpw = 64;
 
+// Kernel-argument form of RdGroup: problem g owns workgroups
+// [gstart[g], gstart[g+1]) of the launch.
+struct RdGroupArgs {
+    const uint16_t *w[kMaxGroup];
+    const float *x[kMaxGroup];
+    float *y[kMaxGroup];
+    int n[kMaxGroup];
+    int gstart[kMaxGroup + 1];
+    int count;
+};
+
 template <int NW, int KV, int ROWS, int MT>
 __global__ void __launch_bounds__(64 * NW)
-gemv_rd_stream_kernel(const uint16_t *__restrict__ W, int64_t ldw, const float *__restrict__ X,
-                      int64_t ldx, float *__restrict__ Y, int64_t ldy, int N, int K, int M, int rpw) {
+gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rb = blockIdx.x * rpw;
+    int gi = 0;
+    while (gi + 1 < ga.count && (int)blockIdx.x >= ga.gstart[gi + 1]) ++gi;
+    const uint16_t *__restrict__ W = ga.w[gi];
+    const float *__restrict__ X = ga.x[gi];
+    float *__restrict__ Y = ga.y[gi];
+    const int N = ga.n[gi];
+    const int64_t ldw = K, ldx = K, ldy = N;
+    const int rb = ((int)blockIdx.x - ga.gstart[gi]) * rpw;
     const int re = min(N, rb + rpw);
     const int m0 = blockIdx.y * MT;
 
@@ -580,6 +600,21 @@ probe_read_kernel(const uint8_t *__restrict__ src, uint64_t n16, uint32_t *__res
     if (threadIdx.x == 0) sink[blockIdx.x] = acc;
 }
 
+// Synthetic weights: dst[i] = table[splitmix64((offset + i) ^ key) >> 48].
+// Integer-only, so a host regenerates any element bit for bit.
+__global__ void __launch_bounds__(kThreads)
+fill_counter_bf16_kernel(uint16_t *__restrict__ dst, uint64_t count, uint64_t offset, uint64_t key,
+                         const uint16_t *__restrict__ table) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+         i += (uint64_t)gridDim.x * kThreads) {
+        uint64_t z = ((offset + i) ^ key) + 0x9E3779B97F4A7C15ull;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        z ^= z >> 31;
+        dst[i] = table[z >> 48];
+    }
+}
+
 // ---- dispatch -------------------------------------------------------------
 
 int mt_for(int64_t m) {
@@ -629,56 +664,55 @@ hipError_t rd_rows(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
 }
 
 template <int NW, int KV, int ROWS, int MT>
-hipError_t rs_go(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+hipError_t rs_go(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     static_assert(MT * KV <= 8 && ROWS * KV <= 8, "register budget");
-    hipLaunchKernelGGL((gemv_rd_stream_kernel<NW, KV, ROWS, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.grid_y),
-                       dim3(64 * NW), 0, s, p.w, p.ldw, p.x, p.ldx, p.y, p.ldy, (int)p.n, (int)p.k, (int)p.m,
-                       pl.rpw);
+    hipLaunchKernelGGL((gemv_rd_stream_kernel<NW, KV, ROWS, MT>), dim3((unsigned)ga.gstart[ga.count], (unsigned)pl.grid_y),
+                       dim3(64 * NW), 0, s, ga, (int)g.k, (int)g.m, pl.rpw);
     return hipGetLastError();
 }
 
 // The streaming variants that are built: MT * KV <= 8 and ROWS * KV <= 8 keep
 // x and the two weight buffers within ~128 VGPRs.
 template <int NW, int KV, int ROWS>
-hipError_t rs_mt(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+hipError_t rs_mt(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     switch (pl.mt) {
-    case 1: return rs_go<NW, KV, ROWS, 1>(p, pl, s);
-    case 2: if constexpr (KV <= 4) return rs_go<NW, KV, ROWS, 2>(p, pl, s); break;
-    case 4: if constexpr (KV <= 2) return rs_go<NW, KV, ROWS, 4>(p, pl, s); break;
-    case 8: if constexpr (KV <= 1) return rs_go<NW, KV, ROWS, 8>(p, pl, s); break;
+    case 1: return rs_go<NW, KV, ROWS, 1>(ga, g, pl, s);
+    case 2: if constexpr (KV <= 4) return rs_go<NW, KV, ROWS, 2>(ga, g, pl, s); break;
+    case 4: if constexpr (KV <= 2) return rs_go<NW, KV, ROWS, 4>(ga, g, pl, s); break;
+    case 8: if constexpr (KV <= 1) return rs_go<NW, KV, ROWS, 8>(ga, g, pl, s); break;
     }
     return hipErrorInvalidValue;
 }
 
 template <int NW, int KV>
-hipError_t rs_rows(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+hipError_t rs_rows(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     switch (pl.rows) {
-    case 1: return rs_mt<NW, KV, 1>(p, pl, s);
-    case 2: if constexpr (KV <= 4) return rs_mt<NW, KV, 2>(p, pl, s); break;
-    case 4: if constexpr (KV <= 2) return rs_mt<NW, KV, 4>(p, pl, s); break;
+    case 1: return rs_mt<NW, KV, 1>(ga, g, pl, s);
+    case 2: if constexpr (KV <= 4) return rs_mt<NW, KV, 2>(ga, g, pl, s); break;
+    case 4: if constexpr (KV <= 2) return rs_mt<NW, KV, 4>(ga, g, pl, s); break;
     }
     return hipErrorInvalidValue;
 }
 
-hipError_t rs_dispatch(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+hipError_t rs_dispatch(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     if (pl.waves == 8) {
         switch (pl.kvec) {
-        case 1: return rs_rows<8, 1>(p, pl, s);
-        case 2: return rs_rows<8, 2>(p, pl, s);
-        case 3: return rs_rows<8, 3>(p, pl, s);
-        case 4: return rs_rows<8, 4>(p, pl, s);
-        case 5: return rs_rows<8, 5>(p, pl, s);
-        case 6: return rs_rows<8, 6>(p, pl, s);
-        case 7: return rs_rows<8, 7>(p, pl, s);
-        case 8: return rs_rows<8, 8>(p, pl, s);
+        case 1: return rs_rows<8, 1>(ga, g, pl, s);
+        case 2: return rs_rows<8, 2>(ga, g, pl, s);
+        case 3: return rs_rows<8, 3>(ga, g, pl, s);
+        case 4: return rs_rows<8, 4>(ga, g, pl, s);
+        case 5: return rs_rows<8, 5>(ga, g, pl, s);
+        case 6: return rs_rows<8, 6>(ga, g, pl, s);
+        case 7: return rs_rows<8, 7>(ga, g, pl, s);
+        case 8: return rs_rows<8, 8>(ga, g, pl, s);
         }
         return hipErrorInvalidValue;
     }
     if (pl.kvec != 1) return hipErrorInvalidValue;
     switch (pl.waves) {
-    case 1: return rs_rows<1, 1>(p, pl, s);
-    case 2: return rs_rows<2, 1>(p, pl, s);
-    case 4: return rs_rows<4, 1>(p, pl, s);
+    case 1: return rs_rows<1, 1>(ga, g, pl, s);
+    case 2: return rs_rows<2, 1>(ga, g, pl, s);
+    case 4: return rs_rows<4, 1>(ga, g, pl, s);
     }
     return hipErrorInvalidValue;
 }
@@ -749,6 +783,44 @@ hipError_t cs_dispatch(const CsProblem &p, const CsPlan &pl, float *P, int64_t p
 
 }  // namespace
 
+namespace {
+
+// Streaming plan for `count` packed problems of n[i] rows sharing m and k.
+// False when k is outside the kernel's register budget.
+bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus, RdPlan &pl) {
+    if (k < 1 || k > 32768 || env_int("DMC_HIP_RD_STREAM", 1) == 0) return false;
+    const int nw = k <= 512 ? 1 : k <= 1024 ? 2 : k <= 2048 ? 4 : 8;
+    const int kv = (int)((k + nw * 512 - 1) / (nw * 512));
+    const int mt_cap = kv == 1 ? 8 : kv == 2 ? 4 : kv <= 4 ? 2 : 1;
+    const int mt = std::min(mt_for(m), mt_cap);
+    int rows = env_int("DMC_HIP_RD_ROWS", kv <= 4 ? 2 : 1);
+    if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = kv <= 4 ? 2 : 1;
+    const int64_t gy = (m + mt - 1) / mt;
+    auto blocks = [&](int64_t r) {
+        int64_t b = 0;
+        for (int i = 0; i < count; ++i) b += (n[i] + r - 1) / r;
+        return b;
+    };
+    // 4 rows per workgroup measured best at the decode shapes (C1, C2);
+    // fewer when that would leave under 4 workgroups per CU.
+    int rpw = env_int("DMC_HIP_RD_RPW", 4);
+    if (rpw < 1) rpw = 4;
+    while (rpw > rows && blocks(rpw) * gy < 4 * cus) rpw >>= 1;
+    rpw = std::max(rows, std::min(kMaxRpw, (rpw + rows - 1) / rows * rows));
+    if ((int64_t)rpw * k * 2 > INT32_MAX || blocks(rpw) > INT32_MAX || gy > 65535) return false;
+    pl.vec = 8;
+    pl.rows = rows;
+    pl.mt = mt;
+    pl.waves = nw;
+    pl.kvec = kv;
+    pl.rpw = rpw;
+    pl.grid_x = blocks(rpw);
+    pl.grid_y = gy;
+    return true;
+}
+
+}  // namespace
+
 RdPlan plan_rd(const RdProblem &p, int num_cus) {
     RdPlan pl{};
     // Widest load the row alignment allows: every row start, every activation
@@ -762,31 +834,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
-    // Streaming kernel: 128-bit rows and k within the register budget.
-    if (pl.vec == 8 && p.k >= 1 && p.k <= 32768 && env_int("DMC_HIP_RD_STREAM", 1) != 0) {
-        const int nw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
-        const int kv = (int)((p.k + nw * 512 - 1) / (nw * 512));
-        const int mt_cap = kv == 1 ? 8 : kv == 2 ? 4 : kv <= 4 ? 2 : 1;
-        const int mt = std::min(mt_for(p.m), mt_cap);
-        int rows = env_int("DMC_HIP_RD_ROWS", kv <= 4 ? 2 : 1);
-        if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = kv <= 4 ? 2 : 1;
-        const int64_t gy = (p.m + mt - 1) / mt;
-        // 4 rows per workgroup measured best at the decode shapes (C1, C2);
-        // fewer when that would leave under 4 workgroups per CU.
-        int rpw = env_int("DMC_HIP_RD_RPW", 4);
-        if (rpw < 1) rpw = 4;
-        while (rpw > rows && ((p.n + rpw - 1) / rpw) * gy < 4 * cus) rpw >>= 1;
-        rpw = std::max(rows, std::min(kMaxRpw, (rpw + rows - 1) / rows * rows));
-        if ((int64_t)rpw * p.ldw * 2 <= INT32_MAX) {
-            pl.rows = rows;
-            pl.mt = mt;
-            pl.waves = nw;
-            pl.kvec = kv;
-            pl.rpw = rpw;
-            pl.grid_x = (p.n + rpw - 1) / rpw;
-            pl.grid_y = gy;
-            return pl;
-        }
+    // Streaming kernel: packed 128-bit rows and k within the register budget.
+    if (pl.vec == 8 && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n) {
+        RdPlan sp{};
+        if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) return sp;
     }
 
     // General kernel.
@@ -803,6 +854,16 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     pl.rpw = rows;
     pl.grid_x = (p.n + rows - 1) / rows;
     pl.grid_y = (p.m + pl.mt - 1) / pl.mt;
+    return pl;
+}
+
+RdPlan plan_rd_group(const RdGroup &g, int num_cus) {
+    RdPlan pl{};
+    if (g.count < 1 || g.count > kMaxGroup || g.k % 8 != 0) return pl;
+    for (int i = 0; i < g.count; ++i)
+        if (!aligned(g.w[i], 16) || !aligned(g.x[i], 32) || g.n[i] < 0) return pl;
+    RdPlan sp{};
+    if (plan_stream(g.m, g.k, g.n, g.count, num_cus > 0 ? num_cus : 256, sp)) return sp;
     return pl;
 }
 
@@ -879,9 +940,38 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
     return pl;
 }
 
+hipError_t launch_rd_group(const RdGroup &g, const RdPlan &pl, hipStream_t s) {
+    if (g.m <= 0 || g.count <= 0) return hipSuccess;
+    if (pl.kvec <= 0 || g.count > kMaxGroup) return hipErrorInvalidValue;
+    RdGroupArgs ga{};
+    int64_t acc = 0;
+    for (int i = 0; i < g.count; ++i) {
+        ga.w[i] = g.w[i];
+        ga.x[i] = g.x[i];
+        ga.y[i] = g.y[i];
+        ga.n[i] = (int)g.n[i];
+        ga.gstart[i] = (int)acc;
+        acc += (g.n[i] + pl.rpw - 1) / pl.rpw;
+    }
+    ga.gstart[g.count] = (int)acc;
+    ga.count = g.count;
+    if (acc == 0) return hipSuccess;
+    return rs_dispatch(ga, g, pl, s);
+}
+
 hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
     if (p.m <= 0 || p.n <= 0) return hipSuccess;
-    if (pl.kvec > 0) return rs_dispatch(p, pl, s);
+    if (pl.kvec > 0) {
+        RdGroup g{};
+        g.w[0] = p.w;
+        g.x[0] = p.x;
+        g.y[0] = p.y;
+        g.n[0] = p.n;
+        g.count = 1;
+        g.m = p.m;
+        g.k = p.k;
+        return launch_rd_group(g, pl, s);
+    }
     switch (pl.vec) {
     case 8: return rd_rows<8>(p, pl, s);
     case 4: return rd_rows<4>(p, pl, s);
@@ -935,6 +1025,15 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
 }
 
 size_t probe_sink_bytes() { return (size_t)kProbeGroups * 4; }
+
+hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset, uint64_t key,
+                                    const uint16_t *table, hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    const uint64_t groups = std::min<uint64_t>(65536, ((uint64_t)count + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(fill_counter_bf16_kernel, dim3((unsigned)groups), dim3(kThreads), 0, s, dst,
+                       (uint64_t)count, (uint64_t)offset, key, table);
+    return hipGetLastError();
+}
 
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t s) {
     const uint64_t n16 = (uint64_t)(bytes > 0 ? bytes : 0) / 16;

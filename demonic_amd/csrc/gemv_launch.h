@@ -76,12 +76,30 @@ struct CsPlan {
     size_t workspace_bytes;  // partial sums when slices > 1
 };
 
+// Up to kMaxGroup independent row-dot problems that share m and k (and x's
+// alignment class), run by one launch of the streaming kernel -- e.g. the
+// q/k/v or gate/up projections of one decode step.  All are packed:
+// w_g [n_g, k], x_g [m, k], y_g [m, n_g].
+constexpr int kMaxGroup = 8;
+struct RdGroup {
+    const uint16_t *w[kMaxGroup];
+    const float *x[kMaxGroup];
+    float *y[kMaxGroup];
+    int64_t n[kMaxGroup];
+    int count;
+    int64_t m, k;
+};
+
 RdPlan plan_rd(const RdProblem &p, int num_cus);
+// Streaming plan for a group; kvec == 0 when the streaming kernel cannot take
+// it (the caller then launches the problems one by one).
+RdPlan plan_rd_group(const RdGroup &g, int num_cus);
 CsPlan plan_cs(const CsProblem &p, int num_cus);
 
 // Enqueue on `stream`.  `workspace` must hold plan.workspace_bytes when
 // plan.slices > 1.  Returns hipSuccess or the launch error.
 hipError_t launch_rd(const RdProblem &p, const RdPlan &plan, hipStream_t stream);
+hipError_t launch_rd_group(const RdGroup &g, const RdPlan &plan, hipStream_t stream);
 
 hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hipStream_t stream);
 
@@ -90,5 +108,10 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hi
 // holds probe_sink_bytes().
 size_t probe_sink_bytes();
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
+
+// Synthetic weights for measurements: dst[i] = table[h(offset + i) >> 48],
+// h(j) = splitmix64(j ^ key), table = 65,536 bf16 bit patterns.
+hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset, uint64_t key,
+                                    const uint16_t *table, hipStream_t stream);
 
 }  // namespace dmc

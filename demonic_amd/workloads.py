@@ -193,6 +193,31 @@ def counter_bf16(seed: int, tensor: int, count: int, offset: int = 0, scale: flo
     return normal_table(scale)[(h >> np.uint64(48)).astype(np.int64)]
 
 
+# ---- C3: the 32-layer decode sweep --------------------------------------------------
+
+C3_SCALE = 0.02
+
+
+def c3_tensor(layer: int, idx: int) -> int:
+    """Counter-generator tensor id of projection idx (LLAMA3_8B_LAYER order) of a layer."""
+    return layer * len(LLAMA3_8B_LAYER) + idx
+
+
+def c3_x(layer: int, k: int, seed: int = 0) -> np.ndarray:
+    """The layer's activation of length k (4096, or 14336 for down), ~N(0,1)."""
+    return counter_f32_normal(seed, 1_000_000 + 2 * layer + (k != 4096), k)
+
+
+def c3_rows(layer: int, idx: int, rows, seed: int = 0) -> np.ndarray:
+    """Rows `rows` of projection idx of a layer, regenerated on the host
+    (bit-identical to the device fill)."""
+    _, n, k = LLAMA3_8B_LAYER[idx]
+    out = np.empty((len(rows), k), np.uint16)
+    for j, r in enumerate(rows):
+        out[j] = counter_bf16(seed, c3_tensor(layer, idx), k, offset=int(r) * k, scale=C3_SCALE)
+    return out
+
+
 def counter_f32_normal(seed: int, tensor: int, count: int) -> np.ndarray:
     """Activation vector for the sweep: N(0,1) float32 from PCG64(seed, tensor)."""
     rng = np.random.Generator(np.random.PCG64([seed, tensor]))

@@ -125,6 +125,17 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
                         int64_t n);
 int32_t dmc_hip_synchronize(void);
 
+/* Grouped row-dot GEMV on device pointers: `count` independent problems
+ * y_i[m, n_i] = x_i[m, k] @ bf16(w_i[n_i, k])', all packed and sharing m and
+ * k, enqueued as one launch per 8 problems when rows are 16-byte aligned and
+ * k <= 32768 (else one launch per problem).  For the projections of one
+ * decode step that read the same activation (q/k/v, gate/up).  The MI355X
+ * counterpart of the reference's one-dispatch batched projection
+ * (gpu.rs:410-437, jit.rs:19897-19956) for weights that are separate tensors
+ * rather than one affine-strided array. */
+int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int64_t *w_devs,
+                                const int64_t *y_devs, const int64_t *ns, int64_t m, int64_t k);
+
 /* Launch plan a GEMV would use on this device (or on a 256-CU gfx950 when no
  * device is present), for tests and reports.  out8 receives
  * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes, waves, rows_per_group}:
@@ -142,6 +153,27 @@ int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t 
  * report can state a GEMV's bandwidth as a fraction of what a pure read
  * reaches on the same device. */
 int32_t dmc_hip_probe_read(int64_t src_dev, int64_t bytes);
+
+/* Synthetic weights for measurements, generated in HBM: dst[i] (u16, i <
+ * count) = table[splitmix64((offset + i) ^ key) >> 48], `table` being 65,536
+ * bf16 bit patterns on the device.  Integer-only, so a host regenerates any
+ * element bit for bit (the 14 GB decode sweep cannot be generated on the
+ * host in reasonable time).  No reference counterpart. */
+int32_t dmc_hip_fill_counter_bf16(int64_t dst_dev, int64_t count, int64_t offset, uint64_t key,
+                                  int64_t table_dev);
+
+/* HIP graphs of the library stream.  Between capture_begin and capture_end,
+ * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
+ * split-K workspace is already large enough, i.e. after one uncaptured call of
+ * the same shape) are recorded instead of run; capture_end returns an
+ * executable graph (0 on error: an entry that allocates or waits was called
+ * while capturing) that graph_launch replays on the library stream.  The
+ * MI355X form of the reference's pipelined command buffers (gpu.rs:206-219,
+ * gpu.rs:539-624): one host call issues a whole decode step. */
+int32_t dmc_hip_capture_begin(void);
+int64_t dmc_hip_capture_end(void);
+int32_t dmc_hip_graph_launch(int64_t exec);
+int32_t dmc_hip_graph_destroy(int64_t exec);
 
 /* HIP events on the library stream, for timing device work. */
 int64_t dmc_hip_event_create(void);

@@ -43,3 +43,18 @@ def check(y, y_ref, tol=TOL, what=""):
     rel = nd / nr
     assert rel <= tol, f"{what}: normwise relative error {rel:.3e} > {tol:.0e}"
     return rel
+
+
+def check_bound(y, y_ref, x, w_rows, what=""):
+    """Elementwise: |y - y_ref| <= 2*K*u*sum_k |x_k * w_k| (u = 2^-24) for every
+    finite reference output -- the rigorous forward-error bound of two
+    length-K fma chains of the same products in different orders.  x is the
+    activation row, w_rows the widened weights of the checked outputs [n, K]."""
+    y = np.asarray(y, np.float64)
+    y_ref = np.asarray(y_ref, np.float64)
+    k = x.shape[-1]
+    s = np.abs(w_rows.astype(np.float64)) @ np.abs(x.astype(np.float64))
+    fin = np.isfinite(y_ref)
+    bound = 2 * k * 2.0 ** -24 * s + 2.0 ** -149
+    bad = fin & (np.abs(y - y_ref) > bound)
+    assert not bad.any(), f"{what}: error beyond the rigorous bound at {np.flatnonzero(bad)[:8]}"

@@ -11,7 +11,7 @@ import pytest
 
 import oracle
 from demonic_amd import workloads as W
-from parity import check
+from parity import check, check_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -326,3 +326,147 @@ def test_cs_split_k_counters_reset(hip, m, k, n, batch):
         if first is None:
             first = y.copy()
         assert np.array_equal(y.view(np.uint32), first.view(np.uint32))
+
+
+# ---- grouped row-dot launch and the device weight generator ------------------------------
+
+@pytest.mark.parametrize("k,ns,m", [(4096, [4096, 1024, 1024], 1), (14336, [4096, 520], 2),
+                                    (4097, [300, 7], 1), (1000, [64, 0, 33], 3),
+                                    (512, [1, 2, 3, 4, 5, 6, 7, 8, 9, 10], 1)])
+def test_grouped_rowdot_matches_each_problem(hip, k, ns, m):
+    """Independent problems sharing x's shape in one launch (q/k/v, gate/up):
+    each output equals its own GEMV's reference; more than 8 problems and
+    shapes outside the streaming kernel take the per-launch path."""
+    rng = np.random.default_rng(k + len(ns) * 7 + m)
+    xs, ws = [], []
+    for i, n in enumerate(ns):
+        xs.append(rng.standard_normal((m, k)).astype(np.float32))
+        ws.append(W.bf16_rne(np.float32(0.02) * rng.standard_normal((n, k)).astype(np.float32)))
+    dxs = [hip.DeviceBuffer.from_numpy(x) for x in xs]
+    dws = [hip.DeviceBuffer.from_numpy(w) if w.size else hip.DeviceBuffer(16) for w in ws]
+    dys = [hip.DeviceBuffer(max(4 * m * n, 4)) for n in ns]
+    try:
+        hip.gemv_rd_grouped(dxs, dws, dys, ns, m, k)
+        hip.synchronize()
+        got, want = [], []
+        for i, n in enumerate(ns):
+            if n == 0:
+                continue
+            y = dys[i].download(np.float32, (m, n))
+            rows = np.arange(n) if n <= 1100 else np.unique(np.r_[0, n - 1, rng.integers(0, n, 300)])
+            mi, ni = np.meshgrid(np.arange(m), rows, indexing="ij")
+            y_ref = oracle.gemv_points(xs[i], ws[i], "rd", mi.reshape(-1), ni.reshape(-1))
+            yd = y[:, rows].reshape(-1)
+            wf = W.bf16_to_f32(ws[i][rows])
+            for r in range(m):
+                check_bound(y[r, rows], y_ref.reshape(m, -1)[r], xs[i][r], wf, what=f"grouped problem {i}")
+            if n >= 256:
+                check(yd, y_ref, what=f"grouped k={k} problem {i} n={n}")
+            got.append(yd)
+            want.append(y_ref)
+        # the normwise rule over the whole group (a one-output problem alone is
+        # ill-conditioned for a norm)
+        check(np.concatenate(got), np.concatenate(want), what=f"grouped k={k} all problems")
+    finally:
+        for b in dxs + dws + dys:
+            b.free()
+
+
+def test_device_fill_matches_host_generator(hip):
+    table = W.normal_table(0.02)
+    n, off = 1_000_003, 123_457
+    key = W.counter_seed(0, 5)
+    with hip.DeviceBuffer.from_numpy(table) as dt, hip.DeviceBuffer(2 * n) as dst:
+        hip.fill_counter_bf16(dst, n, key, dt, offset=off)
+        hip.synchronize()
+        got = dst.download(np.uint16, (n,))
+    assert np.array_equal(got, W.counter_bf16(0, 5, n, offset=off))
+
+
+def test_graph_replay_matches_oracle_each_time(hip):
+    """A captured step (one GEMV and one grouped pair) replayed three times,
+    with new activations uploaded eagerly between replays: every replay must
+    read the live inputs and match the reference."""
+    k = 4096
+    rng = np.random.default_rng(21)
+    ns = [1000, 300, 520]
+    ws = [W.bf16_rne(np.float32(0.02) * rng.standard_normal((n, k)).astype(np.float32)) for n in ns]
+    dws = [hip.DeviceBuffer.from_numpy(w) for w in ws]
+    dx = hip.DeviceBuffer(4 * k)
+    dys = [hip.DeviceBuffer(4 * n) for n in ns]
+    try:
+        dx.upload(rng.standard_normal(k).astype(np.float32))
+        hip.gemv_rd(dx, dws[0], dys[0], 1, k, ns[0])          # eager warm-up of the same shapes
+        hip.gemv_rd_grouped([dx, dx], dws[1:], dys[1:], ns[1:], 1, k)
+        hip.synchronize()
+        g = hip.Graph()
+        with g:
+            hip.gemv_rd(dx, dws[0], dys[0], 1, k, ns[0])
+            hip.gemv_rd_grouped([dx, dx], dws[1:], dys[1:], ns[1:], 1, k)
+        try:
+            for rep in range(3):
+                x = rng.standard_normal(k).astype(np.float32)
+                dx.upload(x)
+                for b, n in zip(dys, ns):
+                    b.upload(np.full(n, np.nan, np.float32))
+                g.launch()
+                hip.synchronize()
+                for i, n in enumerate(ns):
+                    y = dys[i].download(np.float32, (n,))
+                    check(y, oracle.matmul_bf16_t(x, ws[i])[0], what=f"graph replay {rep} problem {i}")
+        finally:
+            g.destroy()
+    finally:
+        for b in dws + dys + [dx]:
+            b.free()
+
+
+def test_c3_layer_schedule(hip):
+    """One layer of the C3 decode sweep as the bench runs it: weights filled in
+    HBM by the counter generator, q/k/v and gate/up as grouped launches, o and
+    down single, all captured in a graph; sampled rows of every projection
+    against the reference on host-regenerated rows."""
+    layer = 7
+    names = [nm for nm, _, _ in W.LLAMA3_8B_LAYER]
+    shape = {nm: (n, k) for nm, n, k in W.LLAMA3_8B_LAYER}
+    table = hip.DeviceBuffer.from_numpy(W.normal_table(W.C3_SCALE))
+    ws = {nm: hip.DeviceBuffer(2 * shape[nm][0] * shape[nm][1]) for nm in names}
+    x, x2 = W.c3_x(layer, 4096), W.c3_x(layer, 14336)
+    dx, dx2 = hip.DeviceBuffer.from_numpy(x), hip.DeviceBuffer.from_numpy(x2)
+    ys = {nm: hip.DeviceBuffer(4 * shape[nm][0]) for nm in names}
+    try:
+        for idx, nm in enumerate(names):
+            n, k = shape[nm]
+            hip.fill_counter_bf16(ws[nm], n * k, W.counter_seed(0, W.c3_tensor(layer, idx)), table)
+
+        def step():
+            hip.gemv_rd_grouped([dx] * 3, [ws["q"], ws["k"], ws["v"]], [ys["q"], ys["k"], ys["v"]],
+                                [4096, 1024, 1024], 1, 4096)
+            hip.gemv_rd(dx, ws["o"], ys["o"], 1, 4096, 4096)
+            hip.gemv_rd_grouped([dx] * 2, [ws["gate"], ws["up"]], [ys["gate"], ys["up"]], [14336] * 2, 1, 4096)
+            hip.gemv_rd(dx2, ws["down"], ys["down"], 1, 14336, 4096)
+
+        step()
+        hip.synchronize()
+        g = hip.Graph()
+        with g:
+            step()
+        try:
+            for b in ys.values():
+                b.upload(np.full(b.nbytes // 4, np.nan, np.float32))
+            g.launch()
+            hip.synchronize()
+        finally:
+            g.destroy()
+        rng = np.random.default_rng(layer)
+        for idx, nm in enumerate(names):
+            n, k = shape[nm]
+            rows = np.unique(np.r_[0, n - 1, rng.integers(0, n, 40)])
+            wr = W.c3_rows(layer, idx, rows)
+            xv = x2 if nm == "down" else x
+            y_ref = oracle.matmul_bf16_t(xv, wr)[0]
+            y = ys[nm].download(np.float32, (n,))
+            check(y[rows], y_ref, what=f"C3 layer {layer} {nm}")
+    finally:
+        for b in list(ws.values()) + list(ys.values()) + [dx, dx2, table]:
+            b.free()
