@@ -47,7 +47,11 @@ struct CsProblem {
 //     with the next rows' weights in flight while the current ones are summed;
 //   general (any alignment or k): 4 waves split k of `rows` rows, x re-read
 //     per chunk.
+//   mfma (mfma == true; M >= a threshold, K % 64 == 0, 16-byte rows): bf16
+//     MFMA on 16-row weight tiles against x split into three bf16 terms,
+//     `rpw` = 64 weight rows and 16 activation rows per workgroup.
 struct RdPlan {
+    bool mfma;  // skinny-M MFMA kernel
     int vec;    // bf16 elements per lane per weight load (8 = 128-bit loads)
     int rows;   // weight rows per step (streaming) / per workgroup (general)
     int mt;     // activation rows per workgroup (skinny-M tile)

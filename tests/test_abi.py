@@ -96,9 +96,17 @@ def test_rowdot_plans_at_decode_shapes():
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
     # activation rows held in registers: MT * vectors-per-lane <= 8
-    for m, mt in [(1, 1), (2, 2), (3, 4), (5, 8), (16, 8), (17, 8)]:
-        assert d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256).mt == mt
-    assert d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256).mt == 2
+    for m, mt in [(1, 1), (2, 2), (3, 4)]:
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert p.mt == mt and p.slices >= 1, p
+    # M >= 4 with k % 64 == 0: the MFMA kernel (slices == -1), 16 activation rows per tile
+    for m in (4, 5, 16, 17):
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-1, 16, 64, 2004), p
+    small = d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256)
+    assert small.slices == -1 and small.waves == 8 and small.grid_x * 16 >= 4096
+    # k not a multiple of 64: back to the streaming kernel
+    assert d.plan("rd", 16, 4104, 1000, x_addr=256, w_addr=256).slices > 0
 
 
 @pytest.mark.parametrize("k,waves,kvec", [(8, 1, 1), (512, 1, 1), (520, 2, 1), (1024, 2, 1),

@@ -470,3 +470,47 @@ def test_c3_layer_schedule(hip):
     finally:
         for b in list(ws.values()) + list(ys.values()) + [dx, dx2, table]:
             b.free()
+
+
+# ---- skinny M on MFMA: special values through the three-term split ---------------------
+
+@pytest.mark.parametrize("m", [4, 8, 16, 20])
+def test_skinny_mfma_special_values(hip, m):
+    """The MFMA path (M >= 4) against the reference chain on data full of
+    special values: bf16 subnormal weights, +-inf / NaN weights, +-0 and
+    f32-subnormal activations, an infinite and a NaN activation, the smallest
+    subnormals (whose bf16 truncation is 0), and an all-zero weight row."""
+    k, n = 1024, 333
+    x, w = case(m, k, n, seed=900 + m, edge=True)
+    x[0, 5] = np.inf
+    x[1, 7] = np.nan
+    x[2, 9] = np.float32(1.4e-45)      # 2^-149
+    x[3, 11] = np.float32(-1.4e-45)
+    w[10, 9] = 0x7F80                  # +inf against 2^-149: +inf (not NaN)
+    w[11, 11] = 0xFF80                 # -inf against -2^-149: +inf
+    w[12, :] = 0                       # exact zero products: +0
+    w[13, 100] = 0x7F80                # +inf against a normal x in every row
+    w[14, 200] = 0x7FC1                # NaN
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert p.slices == -1, "expected the MFMA kernel"
+    y = run_rd(hip, x, w)
+    y_ref = ref(x, w)
+    check(y, y_ref, what=f"mfma specials m={m}")
+    assert np.isposinf(y_ref[2, 10]) and np.isposinf(y[2, 10])
+    assert np.isposinf(y_ref[3, 11]) and np.isposinf(y[3, 11])
+    assert np.all(y[:, 12][np.isfinite(y_ref[:, 12])] == 0)
+
+
+@pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000)])
+def test_skinny_mfma_shapes_within_bound(hip, m, k, n):
+    """MFMA tiles, k split over waves, partial tiles: every element within the
+    rigorous forward-error bound of the reference chain."""
+    x, w = case(m, k, n, seed=m + k + n, scale=0.02)
+    assert hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -1
+    y = run_rd(hip, x, w)
+    rows = np.unique(np.r_[0, n - 1, np.random.default_rng(1).integers(0, n, 200)])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    wf = W.bf16_to_f32(w[rows])
+    for r in range(m):
+        check_bound(y[r, rows], y_ref[r], x[r], wf, what=f"mfma m={m} k={k} n={n} row {r}")
+    check(y[:, rows], y_ref, what=f"mfma m={m} k={k} n={n}")
