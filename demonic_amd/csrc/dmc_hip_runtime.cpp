@@ -729,7 +729,8 @@ int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t 
         dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_addr), k, reinterpret_cast<const float *>(x_addr),
                          k, nullptr, n, m, k, n};
         const dmc::RdPlan pl = dmc::plan_rd(p, cus);
-        const int64_t v[8] = {pl.vec, pl.rows, pl.mt, pl.grid_x, pl.mfma ? -1 : pl.kvec, 0, pl.waves, pl.rpw};
+        const int64_t v[8] = {pl.vec, pl.rows, pl.mt, pl.grid_x, pl.mfma ? -pl.mkind : pl.kvec, 0, pl.waves,
+                              pl.rpw};
         memcpy(out8, v, sizeof v);
     } else {
         dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_addr), reinterpret_cast<const float *>(x_addr),

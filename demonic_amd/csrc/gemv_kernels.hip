@@ -6,19 +6,20 @@
 // These kernels are an MI355X design, not a translation of either:
 //
 //  * HBM-bound streaming.  Every weight byte is read exactly once per launch
-//    with wave-wide coalesced loads (128-bit per lane when the row alignment
-//    allows it; 64/32/16-bit variants cover K or N that are not multiples of
-//    8, e.g. K = 4097).  No weight byte is staged through LDS: there is no
-//    reuse to exploit, so LDS only carries the cross-wave reduction.
-//  * Wave64 split-K.  RD: the 4 waves of a workgroup interleave 64*VEC-element
-//    chunks of the same ROWS rows; each lane keeps one f32 accumulator per
-//    (activation row, weight row) and the partials meet in a wave butterfly
-//    and a fixed-order cross-wave sum.  CS: lanes own VEC adjacent columns,
-//    RW k-rows ride in one wave-wide load, waves interleave k rows, and k is
-//    split over workgroups whose partials a second pass sums in slice order.
+//    with wave-wide coalesced 128-bit nontemporal loads (64/32/16-bit
+//    variants in the general kernels cover K or N that are not multiples of
+//    8, e.g. K = 4097).
+//  * Row-dot (W [N,K]): the streaming kernel splits k over a workgroup's
+//    waves with x held in registers; the general kernel covers any alignment.
+//    Skinny M (>= 4 activation rows) runs on bf16 MFMA against x split into
+//    three bf16 terms, with weights and x staged through LDS.
+//  * Column-stream (W [K,N]): lanes own 8 columns, x[k] is wave-uniform
+//    (scalar loads), waves split a workgroup's k slice, and k slices over
+//    workgroups are summed by a second launch in slice order.
 //  * Numerics.  w = bits << 16 (exact, NaN/inf/subnormal preserving), one
-//    fmaf per product, accumulators start at +0.0f (idle lanes at -0.0f, the
-//    additive identity), no flush-to-zero
+//    fmaf per product in the FMA kernels (the MFMA kernels multiply exactly
+//    and round once per 32-element block), accumulators start at +0.0f
+//    (idle lanes at -0.0f, the additive identity), no flush-to-zero
 //    (compiled with -fno-gpu-flush-denormals-to-zero, no fast-math, no fp
 //    contraction), packed-fp32 disabled.  Fixed reduction order: bit-identical
 //    results run to run.
@@ -297,6 +298,21 @@ __device__ __forceinline__ uint32_t inf_nan_mask(uint32_t d) {
     return (t >> 15) * 0xffffu;
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Running per-half maximum of bf16 magnitudes: a half holding an inf or NaN
+// reaches 0x7f80.  Two instructions per dword (and, packed max); the exact
+// per-element mask is computed only when a wave's screen fires.
+__device__ __forceinline__ uint32_t max_mag(uint32_t acc, uint32_t d) {
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, acc),
+                                                                  __builtin_bit_cast(u16x2, d & 0x7fff7fffu)));
+}
+
+__device__ __forceinline__ bool wave_has_inf_nan(uint32_t mx) {
+    const bool mine = (mx & 0xffffu) >= 0x7f80u || (mx >> 16) >= 0x7f80u;
+    return __builtin_amdgcn_ballot_w64(mine) != 0;
+}
+
 // The three bf16 terms of one f32.
 __device__ __forceinline__ void split3(float v, uint32_t &h, uint32_t &m, uint32_t &l) {
     const uint32_t u = __float_as_uint(v);
@@ -370,12 +386,12 @@ gemv_rd_mfma_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X,
         u32x4 hA, mA, lA, hB, mB, lB;
         split8(xv, hA, mA, lA);
         split8(xv + 8, hB, mB, lB);
-        uint32_t sp = 0;
+        uint32_t mx = 0;
 #pragma unroll
         for (int t = 0; t < R; ++t)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sp |= inf_nan_mask(wa[t][q]) | inf_nan_mask(wb[t][q]);
-        const bool any_special = __builtin_amdgcn_ballot_w64(sp != 0) != 0;
+            for (int q = 0; q < 4; ++q) mx = max_mag(max_mag(mx, wa[t][q]), wb[t][q]);
+        const bool any_special = wave_has_inf_nan(mx);
 #pragma unroll
         for (int t = 0; t < R; ++t) {
             acc[t] = mfma_bf16(wa[t], hA, acc[t]);
@@ -412,6 +428,141 @@ gemv_rd_mfma_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X,
             const int row = t * 16 + (l >> 4) * 4 + r;
             if (row < nrows) Y[(int64_t)m * N + row0 + row] = s[r];
         }
+    }
+}
+
+// Fourth MFMA layout ("wide"): what bounds the MFMA kernels on MI355X is the
+// bytes every vector load moves into the CU -- activation re-reads cost as
+// much as weight bytes, even from L2 -- and the MFMA operand pattern (16 rows
+// x 64 bytes per load) moves them ~15% slower than whole cache lines.  So:
+// 256 weight rows per workgroup (8 waves x 2 tiles, each wave owning its
+// tiles: no cross-wave reduction), k in chunks of 64 so each row's chunk is
+// one 128-byte line, weights loaded 8 whole lines per instruction into a
+// 144-byte-pitch LDS tile (operand reads conflict-free), x's chunk (16 x 64)
+// split once per workgroup into LDS planes.  x bytes are 1/8 of weight bytes.
+// Each wave stages and consumes only its own 32 rows, so its tile needs only
+// the wave's own program order (LDS executes a wave's operations in order);
+// the shared x planes are double-buffered behind one barrier per chunk.
+// Loads run two chunks ahead in registers.
+constexpr int kWideRows = 256;
+constexpr int kWidePitch = 144;
+
+__global__ void __launch_bounds__(512)
+gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                         int K, int M) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * kWideRows;
+    const int nrows = min(kWideRows, N - row0);
+    const int m0 = blockIdx.y * 16;
+    const int nchunks = K / 64;
+
+    __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 36 KiB
+    __shared__ u32x4 xpl[2][2][3][64];                                           // 2 x 6 KiB
+    uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
+
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
+    // Staging: load j (0..3) covers the wave's rows 8j + lane/8, bytes 16*(lane%8) of the chunk.
+    const int scol = (lane & 7) * 16;
+    const int slr = lane >> 3;
+    uint32_t soff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        soff[j] = (uint32_t)min(wave * 32 + slr + 8 * j, nrows - 1) * (uint32_t)K * 2u + scol;
+    // x items: threads 0..127 = (k-block b = tid/64, operand lane = tid%64).
+    const bool xthread = tid < 128;
+    const int xm = m0 + (lane & 15);
+    const float *xp = X + (int64_t)min(xm, M - 1) * K + (tid >> 6) * 32 + (lane >> 4) * 8;
+    const bool xlive = xthread && xm < M;
+
+    struct Regs {
+        u32x4 w[4];
+        float x[8];
+    };
+    auto load = [&](int c, Regs &r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + (uint32_t)c * 128u);
+        if (xlive) {
+            const float4 a = *reinterpret_cast<const float4 *>(xp + c * 64);
+            const float4 b = *reinterpret_cast<const float4 *>(xp + c * 64 + 4);
+            r.x[0] = a.x; r.x[1] = a.y; r.x[2] = a.z; r.x[3] = a.w;
+            r.x[4] = b.x; r.x[5] = b.y; r.x[6] = b.z; r.x[7] = b.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) r.x[e] = 0.0f;
+        }
+    };
+    auto store = [&](const Regs &r, int xbuf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
+        if (xthread) {
+            u32x4 hi, md, lo;
+            split8(r.x, hi, md, lo);
+            xpl[xbuf][tid >> 6][0][lane] = hi;
+            xpl[xbuf][tid >> 6][1][lane] = md;
+            xpl[xbuf][tid >> 6][2][lane] = lo;
+        }
+    };
+
+    f32x4 acc[2] = {f32x4{0.0f, 0.0f, 0.0f, 0.0f}, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+    auto compute = [&](int xbuf) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const u32x4 hi = xpl[xbuf][b][0][lane], md = xpl[xbuf][b][1][lane], lo = xpl[xbuf][b][2][lane];
+            u32x4 a[2];
+            uint32_t mx = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
+            }
+            const bool any_special = wave_has_inf_nan(mx);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                acc[t] = mfma_bf16(a[t], hi, acc[t]);
+                u32x4 a2 = a[t];
+                if (any_special) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) a2[v] &= ~inf_nan_mask(a2[v]);
+                }
+                acc[t] = mfma_bf16(a2, md, acc[t]);
+                acc[t] = mfma_bf16(a2, lo, acc[t]);
+            }
+        }
+    };
+
+    // Chunk c is in LDS (x planes in buffer c&1); chunk c+1 waits in one
+    // register set and chunk c+2 loads into the other.
+    Regs ra, rb;
+    if (nchunks > 0) load(0, ra);
+    if (nchunks > 1) load(1, rb);
+    if (nchunks > 0) store(ra, 0);
+    __syncthreads();
+    auto step = [&](int c, Regs &rnext, Regs &rfree) {
+        if (c + 2 < nchunks) load(c + 2, rfree);
+        compute(c & 1);
+        if (c + 1 < nchunks) store(rnext, (c + 1) & 1);
+        __syncthreads();
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+        step(c, rb, ra);
+        if (c + 1 >= nchunks) break;
+        step(c + 1, ra, rb);
+    }
+
+    const int m = m0 + i16;
+    if (m < M) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = (wave * 2 + t) * 16 + g * 4 + r;
+                if (row < nrows) Y[(int64_t)m * N + row0 + row] = acc[t][r];
+            }
     }
 }
 
@@ -1003,11 +1154,23 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.vec = 8;
         mp.rows = 16;
         mp.mt = 16;
-        mp.waves = p.k >= 8192 ? 8 : 4;
         mp.kvec = 0;
-        int tiles = kMfmaTiles;
-        while (tiles > 1 && ((p.n + tiles * 16 - 1) / (tiles * 16)) * ((p.m + 15) / 16) < 2 * cus) tiles >>= 1;
-        mp.rpw = tiles * 16;
+        const int64_t gy = (p.m + 15) / 16;
+        // The wide layout when its 256-row workgroups still give >= 1.5 per
+        // CU; otherwise the k-split layout, whose workgroups shrink to fill
+        // the device.
+        const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus;
+        mp.mkind = env_int("DMC_HIP_RD_MFMA_KIND", wide_fits ? 6 : 1) == 1 ? 1 : 6;
+        if (mp.mkind == 6) {
+            mp.waves = 8;
+            mp.rpw = kWideRows;
+        } else {
+            mp.waves = env_int("DMC_HIP_RD_MFMA_WAVES", p.k >= 8192 ? 8 : 4) == 8 ? 8 : 4;
+            int tiles = env_int("DMC_HIP_RD_MFMA_TILES", kMfmaTiles);
+            if (tiles != 1 && tiles != 2 && tiles != 4) tiles = kMfmaTiles;
+            while (tiles > 1 && ((p.n + tiles * 16 - 1) / (tiles * 16)) * gy < 2 * cus) tiles >>= 1;
+            mp.rpw = tiles * 16;
+        }
         mp.grid_x = (p.n + mp.rpw - 1) / mp.rpw;
         mp.grid_y = (p.m + 15) / 16;
         return mp;
@@ -1142,6 +1305,11 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
     if (p.m <= 0 || p.n <= 0) return hipSuccess;
     if (pl.mfma) {
         const dim3 grid((unsigned)pl.grid_x, (unsigned)pl.grid_y);
+        if (pl.mkind == 6) {
+            hipLaunchKernelGGL(gemv_rd_mfma_wide_kernel, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n, (int)p.k,
+                               (int)p.m);
+            return hipGetLastError();
+        }
 #define DMC_RDM(NW, R)                                                                                        \
     if (pl.waves == NW && pl.rpw == R * 16) {                                                                 \
         hipLaunchKernelGGL((gemv_rd_mfma_kernel<NW, R>), grid, dim3(64 * NW), 0, s, p.w, p.x, p.y, (int)p.n, \

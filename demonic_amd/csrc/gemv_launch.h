@@ -49,9 +49,11 @@ struct CsProblem {
 //     per chunk.
 //   mfma (mfma == true; M >= a threshold, K % 64 == 0, 16-byte rows): bf16
 //     MFMA on 16-row weight tiles against x split into three bf16 terms,
-//     `rpw` = 64 weight rows and 16 activation rows per workgroup.
+//     `rpw` weight rows and 16 activation rows per workgroup.
 struct RdPlan {
     bool mfma;  // skinny-M MFMA kernel
+    int mkind;  // MFMA layout: 1 = the workgroup's waves split k over R 16-row tiles;
+                // 6 = 256 rows per workgroup, weights and x staged through LDS
     int vec;    // bf16 elements per lane per weight load (8 = 128-bit loads)
     int rows;   // weight rows per step (streaming) / per workgroup (general)
     int mt;     // activation rows per workgroup (skinny-M tile)

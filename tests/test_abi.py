@@ -99,12 +99,10 @@ def test_rowdot_plans_at_decode_shapes():
     for m, mt in [(1, 1), (2, 2), (3, 4)]:
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert p.mt == mt and p.slices >= 1, p
-    # M >= 4 with k % 64 == 0: the MFMA kernel (slices == -1), 16 activation rows per tile
+    # M >= 4 with k % 64 == 0: an MFMA kernel (slices == -kind), 16 activation rows per tile
     for m in (4, 5, 16, 17):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-1, 16, 64, 2004), p
-    small = d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256)
-    assert small.slices == -1 and small.waves == 8 and small.grid_x * 16 >= 4096
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
     # k not a multiple of 64: back to the streaming kernel
     assert d.plan("rd", 16, 4104, 1000, x_addr=256, w_addr=256).slices > 0
 
@@ -116,6 +114,22 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
     p = d.plan("rd", 1, k, 1000, x_addr=256, w_addr=256)
     assert (p.waves, p.slices) == (waves, kvec), p
     assert waves * kvec * 512 >= k > (waves * kvec - waves) * 512 or kvec == 1
+
+
+def test_rowdot_mfma_layouts(monkeypatch):
+    # small N: the k-split layout, tiles shrinking to fill the device
+    p = d.plan("rd", 8, 4096, 16387, x_addr=256, w_addr=256)
+    assert p.slices == -1 and p.grid_x >= 512, p
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "1")
+    p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
+    assert (p.slices, p.rows_per_group, p.grid_x) == (-1, 64, 2004), p
+    small = d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256)
+    assert small.slices == -1 and small.waves == 8 and small.grid_x * 16 >= 4096
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "6")
+    p = d.plan("rd", 16, 4096, 1000, x_addr=256, w_addr=256)
+    assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "0")  # disabled: the FMA kernels
+    assert d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256).slices > 0
 
 
 def test_rowdot_falls_back_to_general_kernel():

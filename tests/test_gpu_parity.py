@@ -474,8 +474,9 @@ def test_c3_layer_schedule(hip):
 
 # ---- skinny M on MFMA: special values through the three-term split ---------------------
 
+@pytest.mark.parametrize("kind", [1, 6])
 @pytest.mark.parametrize("m", [4, 8, 16, 20])
-def test_skinny_mfma_special_values(hip, m):
+def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     """The MFMA path (M >= 4) against the reference chain on data full of
     special values: bf16 subnormal weights, +-inf / NaN weights, +-0 and
     f32-subnormal activations, an infinite and a NaN activation, the smallest
@@ -491,8 +492,9 @@ def test_skinny_mfma_special_values(hip, m):
     w[12, :] = 0                       # exact zero products: +0
     w[13, 100] = 0x7F80                # +inf against a normal x in every row
     w[14, 200] = 0x7FC1                # NaN
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
-    assert p.slices == -1, "expected the MFMA kernel"
+    assert p.slices == -kind, "expected the MFMA kernel"
     y = run_rd(hip, x, w)
     y_ref = ref(x, w)
     check(y, y_ref, what=f"mfma specials m={m}")
@@ -501,12 +503,17 @@ def test_skinny_mfma_special_values(hip, m):
     assert np.all(y[:, 12][np.isfinite(y_ref[:, 12])] == 0)
 
 
-@pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000)])
-def test_skinny_mfma_shapes_within_bound(hip, m, k, n):
-    """MFMA tiles, k split over waves, partial tiles: every element within the
-    rigorous forward-error bound of the reference chain."""
+@pytest.mark.parametrize("kind", [1, 6])
+@pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000),
+                                   (16, 4096, 40000), (3, 320, 300)])
+def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
+    """MFMA tiles, k split over waves or chunked through LDS, partial tiles
+    and chunks: every element within the rigorous forward-error bound of the
+    reference chain."""
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "3")
     x, w = case(m, k, n, seed=m + k + n, scale=0.02)
-    assert hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -1
+    assert hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
     y = run_rd(hip, x, w)
     rows = np.unique(np.r_[0, n - 1, np.random.default_rng(1).integers(0, n, 200)])
     y_ref = oracle.matmul_bf16_t(x, w[rows])
