@@ -277,6 +277,7 @@ def extended(d, W, reps: int) -> dict:
             f(i)
         record(label, batch_us(d, f, reps), n, k)
         s.free()
+    out.update(dropin(d, W, min(reps, 100)))
     # C4 LM head, skinny M: one resident copy (1.05 GB exceeds the 256 MB cache)
     t = time.perf_counter()
     w, _ = W.dense(W.LM_HEAD[0], W.LM_HEAD[1], seed=0, m=1)
@@ -306,6 +307,37 @@ def extended(d, W, reps: int) -> dict:
             f(0)
             record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
             s.free()
+    return out
+
+
+def dropin(d, W, reps: int) -> dict:
+    """The drop-in entries with HOST x and y -- the PCIe-inclusive rate, never
+    `value`.  C2 up/gate through dmc_matmul_bf16_gpu_t (x @ W', W [N,K]) and
+    dmc_matmul_bf16_gpu (x @ W, W [K,N], the reference's layout).  Each call
+    copies x in, launches, copies y out and synchronizes; weights are made
+    resident by their first call (content key), and three distinct weights
+    rotate so every call reads cold bytes.  Host wall time per call."""
+    lib = d._lib.load()
+    n, k = 14336, 4096
+    out = {}
+    mats = [W.dense(n, k, seed=100 + s, m=1)[0] for s in range(3)]
+    x = np.random.default_rng(0).standard_normal(k).astype(np.float32)
+    y = np.empty(n, np.float32)
+    for label, entry, ws in (("drop-in rd x@W' host x/y", lib.dmc_matmul_bf16_gpu_t, mats),
+                             ("drop-in cs x@W host x/y", lib.dmc_matmul_bf16_gpu,
+                              [np.ascontiguousarray(w.T) for w in mats])):
+        ptrs = [w.ctypes.data for w in ws]
+        for p in ptrs:
+            entry(x.ctypes.data, p, y.ctypes.data, 1, k, n)
+        t0 = time.perf_counter()
+        for i in range(reps):
+            entry(x.ctypes.data, ptrs[i % 3], y.ctypes.data, 1, k, n)
+        us = (time.perf_counter() - t0) / reps * 1e6
+        gbs = b_alg(n, k) / (us * 1e-6) / 1e9
+        out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"{label}: {us:.2f} us/call  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%} (PCIe-inclusive)")
+        assert np.all(np.isfinite(y)), label
+    d.release_weights()
     return out
 
 

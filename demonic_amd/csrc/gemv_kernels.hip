@@ -143,11 +143,20 @@ __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w
 // KV vectors of 8 elements starting at ((j*NW + wave)*64 + lane)*8, j < KV, so
 // for every j the workgroup reads NW*1 KiB of a row contiguously.  The lane
 // loads its x slice (MT activation rows) into registers once, then the
-// workgroup walks weight rows [rb, rb+rpw) ROWS at a time, loading the next
-// ROWS rows before it sums the current ones.  Each (activation row, weight
-// row) partial is reduced across the wave with DPP and parked in LDS; one
-// barrier at the end, then a fixed-order sum over the waves.
+// workgroup walks weight rows [rb, rb+rpw) ROWS at a time through two
+// register buffers: the next ROWS rows are in flight while the current ones
+// are summed.  Each (activation row, weight row) partial is reduced across
+// the wave with DPP and parked in LDS; one barrier at the end, then a
+// fixed-order sum over the waves.
+//
+// Every load is unconditional, so the compiler can count the loads in flight
+// and wait only for the buffer being summed (a load under a branch makes it
+// wait for all of them, which serialises the two buffers).  A lane that owns
+// no element, and a row past the workgroup's last, load from offset
+// kOutOfRange, beyond the buffer resource's size: the hardware returns zeros
+// and reads no memory.
 constexpr int kMaxRpw = 64;
+constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // Kernel-argument form of RdGroup: problem g owns workgroups
 // [gstart[g], gstart[g+1]) of the launch.
@@ -160,66 +169,77 @@ struct RdGroupArgs {
     int count;
 };
 
-template <int NW, int KV, int ROWS, int MT>
+// GROUP = false: a single problem, read straight from entry 0 of the
+// arguments.  GROUP = true: the problem index is counted branch-free from
+// gstart (entries past the last problem hold INT32_MAX), so all of gstart
+// arrives in one scalar load; a search loop would chain dependent scalar
+// loads before the first weight load (measured 0.3-1 us per launch).
+template <int NW, int KV, int ROWS, int MT, bool GROUP>
 __global__ void __launch_bounds__(64 * NW)
 gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int gi = 0;
-    while (gi + 1 < ga.count && (int)blockIdx.x >= ga.gstart[gi + 1]) ++gi;
+    if constexpr (GROUP) {
+#pragma unroll
+        for (int g = 1; g < kMaxGroup; ++g) gi += (int)blockIdx.x >= ga.gstart[g] ? 1 : 0;
+    }
     const uint16_t *__restrict__ W = ga.w[gi];
     const float *__restrict__ X = ga.x[gi];
     float *__restrict__ Y = ga.y[gi];
     const int N = ga.n[gi];
-    const int64_t ldw = K, ldx = K, ldy = N;
+    const int64_t ldw = K, ldy = N;
     const int rb = ((int)blockIdx.x - ga.gstart[gi]) * rpw;
     const int re = min(N, rb + rpw);
     const int m0 = blockIdx.y * MT;
+    const int mrows = min(MT, M - m0);
 
-    float xr[MT][KV][8];
-    bool has[KV];
+    // x rows [m0, m0 + mrows): activation row m0 + m reads row min(m, mrows - 1).
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4);
     uint32_t eoff[KV];
+    u32x4 xa[MT][KV], xb[MT][KV];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
         const int e = ((j * NW + wave) * 64 + lane) * 8;
-        has[j] = e < K;
-        eoff[j] = (uint32_t)e * 2;
+        const bool has = e < K;
+        eoff[j] = has ? (uint32_t)e * 2 : kOutOfRange;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            if (has[j]) {
-                const float *p = X + (int64_t)min(m0 + m, M - 1) * ldx + e;
-                const float4 a = *reinterpret_cast<const float4 *>(p);
-                const float4 b = *reinterpret_cast<const float4 *>(p + 4);
-                xr[m][j][0] = a.x; xr[m][j][1] = a.y; xr[m][j][2] = a.z; xr[m][j][3] = a.w;
-                xr[m][j][4] = b.x; xr[m][j][5] = b.y; xr[m][j][6] = b.z; xr[m][j][7] = b.w;
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q) xr[m][j][q] = 0.0f;
-            }
+            const uint32_t xo = has ? ((uint32_t)min(m, mrows - 1) * (uint32_t)K + (uint32_t)e) * 4 : kOutOfRange;
+            xa[m][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+            xb[m][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0);
         }
     }
     // +0.0f for a lane that owns elements (the reference's chain start,
     // jit.rs:29655), -0.0f, the additive identity, for a lane that owns none.
-    const float init = has[0] ? 0.0f : -0.0f;
+    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
 
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * ldw, (uint32_t)((int64_t)(re - rb) * ldw * 2));
     const uint32_t row_bytes = (uint32_t)ldw * 2;
     __shared__ float red[NW][MT][kMaxRpw];
 
-    u32x4 cur[ROWS][KV], nxt[ROWS][KV];
+    u32x4 ba[ROWS][KV], bb[ROWS][KV];
     auto load = [&](u32x4 (&wv)[ROWS][KV], int r0) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
-            const uint32_t base = (uint32_t)(min(r0 + q, re - 1) - rb) * row_bytes;
+            const uint32_t base = (uint32_t)(r0 + q - rb) * row_bytes;
 #pragma unroll
-            for (int j = 0; j < KV; ++j)
-                wv[q][j] = has[j] ? load_w16(rs, base + eoff[j]) : u32x4{0u, 0u, 0u, 0u};
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, base + eoff[j]);
         }
     };
+    load(ba, rb);
+    float xr[MT][KV][8];
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xr[m][j][q] = __uint_as_float(xa[m][j][q]);
+                xr[m][j][q + 4] = __uint_as_float(xb[m][j][q]);
+            }
 
-    load(cur, rb);
-    for (int r0 = rb; r0 < re; r0 += ROWS) {
-        if (r0 + ROWS < re) load(nxt, r0 + ROWS);
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
         float acc[MT][ROWS];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
@@ -231,7 +251,7 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
             for (int e = 0; e < 8; ++e)
 #pragma unroll
                 for (int q = 0; q < ROWS; ++q) {
-                    const uint32_t d = cur[q][j][e >> 1];
+                    const uint32_t d = wv[q][j][e >> 1];
                     const float w = (e & 1) ? widen_hi(d) : widen_lo(d);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
@@ -243,10 +263,13 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
                 const float s = wave_sum_dpp(acc[m][q]);
                 if (lane == 0 && r0 + q < re) red[wave][m][r0 - rb + q] = s;
             }
-#pragma unroll
-        for (int q = 0; q < ROWS; ++q)
-#pragma unroll
-            for (int j = 0; j < KV; ++j) cur[q][j] = nxt[q][j];
+    };
+    for (int r0 = rb; r0 < re; r0 += 2 * ROWS) {
+        load(bb, r0 + ROWS);
+        sum_rows(ba, r0);
+        if (r0 + ROWS >= re) break;
+        load(ba, r0 + 2 * ROWS);
+        sum_rows(bb, r0 + ROWS);
     }
     __syncthreads();
     const int nr = re - rb;
@@ -255,7 +278,7 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
         float s = red[0][m][r];
 #pragma unroll
         for (int w = 1; w < NW; ++w) s += red[w][m][r];
-        if (m0 + m < M) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
+        if (m < mrows) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
     }
 }
 
@@ -974,8 +997,13 @@ hipError_t rd_rows(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
 template <int NW, int KV, int ROWS, int MT>
 hipError_t rs_go(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     static_assert(MT * KV <= 8 && ROWS * KV <= 8, "register budget");
-    hipLaunchKernelGGL((gemv_rd_stream_kernel<NW, KV, ROWS, MT>), dim3((unsigned)ga.gstart[ga.count], (unsigned)pl.grid_y),
-                       dim3(64 * NW), 0, s, ga, (int)g.k, (int)g.m, pl.rpw);
+    const dim3 grid((unsigned)ga.gstart[ga.count], (unsigned)pl.grid_y);
+    if (ga.count == 1)
+        hipLaunchKernelGGL((gemv_rd_stream_kernel<NW, KV, ROWS, MT, false>), grid, dim3(64 * NW), 0, s, ga,
+                           (int)g.k, (int)g.m, pl.rpw);
+    else
+        hipLaunchKernelGGL((gemv_rd_stream_kernel<NW, KV, ROWS, MT, true>), grid, dim3(64 * NW), 0, s, ga,
+                           (int)g.k, (int)g.m, pl.rpw);
     return hipGetLastError();
 }
 
@@ -1109,11 +1137,15 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
         for (int i = 0; i < count; ++i) b += (n[i] + r - 1) / r;
         return b;
     };
-    // 4 rows per workgroup measured best at the decode shapes (C1, C2);
-    // fewer when that would leave under 4 workgroups per CU.
-    int rpw = env_int("DMC_HIP_RD_RPW", 4);
-    if (rpw < 1) rpw = 4;
-    while (rpw > rows && blocks(rpw) * gy < 4 * cus) rpw >>= 1;
+    // Rows per workgroup, measured on MI355X: 4 for short rows (k <= 4096
+    // per 8 waves: up/gate 18.1 us, 8 rows 18.5), fewer when that would leave
+    // under 4 workgroups per CU; 8 for long ones (down, k = 14336: 19.0 us,
+    // 4 rows 19.8), fewer when that would leave under 2 per CU.
+    const int rpw_default = kv >= 2 ? 8 : 4;
+    const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
+    int rpw = env_int("DMC_HIP_RD_RPW", rpw_default);
+    if (rpw < 1) rpw = rpw_default;
+    while (rpw > rows && blocks(rpw) * gy < min_blocks) rpw >>= 1;
     rpw = std::max(rows, std::min(kMaxRpw, (rpw + rows - 1) / rows * rows));
     if ((int64_t)rpw * k * 2 > INT32_MAX || blocks(rpw) > INT32_MAX || gy > 65535) return false;
     pl.vec = 8;
@@ -1296,6 +1328,7 @@ hipError_t launch_rd_group(const RdGroup &g, const RdPlan &pl, hipStream_t s) {
         acc += (g.n[i] + pl.rpw - 1) / pl.rpw;
     }
     ga.gstart[g.count] = (int)acc;
+    for (int i = g.count + 1; i <= kMaxGroup; ++i) ga.gstart[i] = INT32_MAX;
     ga.count = g.count;
     if (acc == 0) return hipSuccess;
     return rs_dispatch(ga, g, pl, s);

@@ -91,8 +91,9 @@ def test_rowdot_plans_at_decode_shapes():
     up = d.plan("rd", 1, 4096, 14336, x_addr=256, w_addr=256)
     assert (up.vec, up.waves, up.slices, up.rows_per_group, up.rows_or_rw, up.mt, up.grid_x) == \
         (8, 8, 1, 4, 2, 1, 3584)
+    # long rows: ceil(14336 / 4096) vectors per lane, 8 rows per workgroup
     down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
-    assert (down.waves, down.slices, down.grid_x) == (8, 4, 1024)  # ceil(14336 / 4096) vectors
+    assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (8, 4, 8, 512)
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
     # activation rows held in registers: MT * vectors-per-lane <= 8
