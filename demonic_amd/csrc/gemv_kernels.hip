@@ -828,17 +828,36 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
         }
     };
 
+    // Two register buffers of U rows: the next U rows are in flight while the
+    // current ones are summed.  Loads are unconditional (a dead lane, and a
+    // row past this wave's range, read from past the buffer's end and get
+    // zeros without touching memory), so the compiler waits only for the
+    // buffer it sums; the row guard sits on the arithmetic, which also keeps
+    // x[k] in range.
     constexpr int U = MT <= 2 ? 8 : 4;
-    int r = r0;
-    if (live) {
-        for (; r + U <= r1; r += U) {
-            u32x4 wv[U];
+    const uint32_t loff = live ? lane_off : kOutOfRange;
+    u32x4 ba[U], bb[U];
+    auto load = [&](u32x4 (&b)[U], int r) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) wv[u] = load_w16(rsw, (uint32_t)(r - r0 + u) * row_bytes + lane_off);
+        for (int u = 0; u < U; ++u) b[u] = load_w16(rsw, (uint32_t)(r - r0 + u) * row_bytes + loff);
+    };
+    auto sum_rows = [&](const u32x4 (&b)[U], int r) {
+        if (r + U <= r1) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) consume(wv[u], r + u);
+            for (int u = 0; u < U; ++u) consume(b[u], r + u);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (r + u < r1) consume(b[u], r + u);
         }
-        for (; r < r1; ++r) consume(load_w16(rsw, (uint32_t)(r - r0) * row_bytes + lane_off), r);
+    };
+    load(ba, r0);
+    for (int r = r0; r < r1; r += 2 * U) {
+        load(bb, r + U);
+        sum_rows(ba, r);
+        if (r + U >= r1) break;
+        load(ba, r + 2 * U);
+        sum_rows(bb, r + U);
     }
 
     __shared__ float red[NW][MT][kCsCols];
@@ -1191,8 +1210,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // The wide layout when its 256-row workgroups still give >= 1.5 per
         // CU; otherwise the k-split layout, whose workgroups shrink to fill
         // the device.
-        const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus;
+        const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus &&
+                               (int64_t)kWideRows * p.k * 2 <= INT32_MAX;
         mp.mkind = env_int("DMC_HIP_RD_MFMA_KIND", wide_fits ? 6 : 1) == 1 ? 1 : 6;
+        if ((int64_t)kWideRows * p.k * 2 > INT32_MAX) mp.mkind = 1;  // 256-row buffer range
         if (mp.mkind == 6) {
             mp.waves = 8;
             mp.rpw = kWideRows;
@@ -1274,10 +1295,10 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         kslice = std::max<int64_t>(nw, env_int("DMC_HIP_CS_KSLICE", (int)std::min<int64_t>(kslice, INT32_MAX)));
         pl.kslice = kslice;
         pl.slices = (kmax + kslice - 1) / kslice;
-        // A wave's rows must fit a 32-bit buffer range; the grid's y extent
-        // is limited to 65535.
+        // A wave's rows, plus the 16 rows its last loads run past them, must
+        // fit a 31-bit buffer offset; the grid's y extent is limited to 65535.
         const int64_t per_wave = (kslice + nw - 1) / nw;
-        if (pl.slices <= 65535 && per_wave * p.n * 2 <= INT32_MAX) {
+        if (pl.slices <= 65535 && (per_wave + 16) * p.n * 2 <= INT32_MAX) {
             pl.workspace_bytes = pl.slices > 1 ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
             return pl;
         }
