@@ -284,7 +284,9 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
 
 // ---- RD skinny M on MFMA: W [N,K] x X [M,K], K % 64 == 0 ---------------------------
 //
-// For M >= 4 the FMA path is issue-bound (M fmas per weight element), so the
+// From M = 2 the FMA path loses to the matrix cores (M fmas per weight element,
+// MT activation rows of registers; on the LM-head shape M = 2 takes 174-183 us
+// there against 161-166 here, M = 3 212-240 against 166-173), so the
 // products go to v_mfma_f32_16x16x32_bf16: A = a 16-row weight tile, B = x^T
 // for 16 activation rows.  x is f32, so it enters as three bf16 terms,
 // x == hi + mid + lo, each taken by truncation: every residual is exact in
@@ -1193,10 +1195,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
-    // MFMA kernel for skinny M: packed rows, k a multiple of 64.  Tiles per
+    // MFMA kernel for skinny M >= 2: packed rows, k a multiple of 64.  Tiles per
     // workgroup shrink (4 -> 2 -> 1) until the grid has >= 2 workgroups per
     // CU; 8 waves split k when it is long.
-    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 4);
+    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 2);
     if (mfma_min_m > 0 && p.m >= mfma_min_m && p.k >= 64 && p.k % 64 == 0 && p.k <= INT32_MAX / 2 &&
         aligned(p.w, 16) && aligned(p.x, 16) && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n &&
         (int64_t)kMfmaTiles * 16 * p.k * 2 <= INT32_MAX && (p.m + 15) / 16 <= 65535) {

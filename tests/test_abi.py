@@ -96,16 +96,19 @@ def test_rowdot_plans_at_decode_shapes():
     assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (8, 4, 8, 512)
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
-    # activation rows held in registers: MT * vectors-per-lane <= 8
-    for m, mt in [(1, 1), (2, 2), (3, 4)]:
-        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
-        assert p.mt == mt and p.slices >= 1, p
-    # M >= 4 with k % 64 == 0: an MFMA kernel (slices == -kind), 16 activation rows per tile
-    for m in (4, 5, 16, 17):
+    # M = 1: the streaming kernel
+    p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
+    assert p.mt == 1 and p.slices >= 1, p
+    # M >= 2 with k % 64 == 0: an MFMA kernel (slices == -kind), 16 activation rows per tile
+    for m in (2, 3, 4, 5, 16, 17):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
-    # k not a multiple of 64: back to the streaming kernel
+    # k not a multiple of 64: back to the streaming kernel, activation rows held in
+    # registers (MT * vectors-per-lane <= 8)
     assert d.plan("rd", 16, 4104, 1000, x_addr=256, w_addr=256).slices > 0
+    for m, mt in [(2, 2), (3, 4)]:
+        p = d.plan("rd", m, 4104, 1000, x_addr=256, w_addr=256)
+        assert p.mt == mt and p.slices >= 1, p
 
 
 @pytest.mark.parametrize("k,waves,kvec", [(8, 1, 1), (512, 1, 1), (520, 2, 1), (1024, 2, 1),

@@ -475,9 +475,9 @@ def test_c3_layer_schedule(hip):
 # ---- skinny M on MFMA: special values through the three-term split ---------------------
 
 @pytest.mark.parametrize("kind", [1, 6])
-@pytest.mark.parametrize("m", [4, 8, 16, 20])
+@pytest.mark.parametrize("m", [2, 3, 4, 8, 16, 20])
 def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
-    """The MFMA path (M >= 4) against the reference chain on data full of
+    """The MFMA path (M >= 2) against the reference chain on data full of
     special values: bf16 subnormal weights, +-inf / NaN weights, +-0 and
     f32-subnormal activations, an infinite and a NaN activation, the smallest
     subnormals (whose bf16 truncation is 0), and an all-zero weight row."""
@@ -485,8 +485,9 @@ def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     x, w = case(m, k, n, seed=900 + m, edge=True)
     x[0, 5] = np.inf
     x[1, 7] = np.nan
-    x[2, 9] = np.float32(1.4e-45)      # 2^-149
-    x[3, 11] = np.float32(-1.4e-45)
+    if m >= 4:
+        x[2, 9] = np.float32(1.4e-45)      # 2^-149
+        x[3, 11] = np.float32(-1.4e-45)
     w[10, 9] = 0x7F80                  # +inf against 2^-149: +inf (not NaN)
     w[11, 11] = 0xFF80                 # -inf against -2^-149: +inf
     w[12, :] = 0                       # exact zero products: +0
@@ -498,20 +499,20 @@ def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     y = run_rd(hip, x, w)
     y_ref = ref(x, w)
     check(y, y_ref, what=f"mfma specials m={m}")
-    assert np.isposinf(y_ref[2, 10]) and np.isposinf(y[2, 10])
-    assert np.isposinf(y_ref[3, 11]) and np.isposinf(y[3, 11])
+    if m >= 4:
+        assert np.isposinf(y_ref[2, 10]) and np.isposinf(y[2, 10])
+        assert np.isposinf(y_ref[3, 11]) and np.isposinf(y[3, 11])
     assert np.all(y[:, 12][np.isfinite(y_ref[:, 12])] == 0)
 
 
 @pytest.mark.parametrize("kind", [1, 6])
 @pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000),
-                                   (16, 4096, 40000), (3, 320, 300)])
+                                   (16, 4096, 40000), (3, 320, 300), (2, 4096, 16387), (2, 64, 70)])
 def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
     """MFMA tiles, k split over waves or chunked through LDS, partial tiles
     and chunks: every element within the rigorous forward-error bound of the
     reference chain."""
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
-    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "3")
     x, w = case(m, k, n, seed=m + k + n, scale=0.02)
     assert hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
     y = run_rd(hip, x, w)
