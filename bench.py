@@ -277,7 +277,7 @@ def extended(d, W, reps: int) -> dict:
             f(i)
         record(label, batch_us(d, f, reps), n, k)
         s.free()
-    out.update(dropin(d, W, min(reps, 100)))
+    out.update(dropin(d, W, 300))
     # C4 LM head, skinny M: one resident copy (1.05 GB exceeds the 256 MB cache)
     t = time.perf_counter()
     w, _ = W.dense(W.LM_HEAD[0], W.LM_HEAD[1], seed=0, m=1)

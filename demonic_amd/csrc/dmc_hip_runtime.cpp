@@ -263,15 +263,35 @@ int release_weights_locked() {
     return DMC_HIP_OK;
 }
 
+// hipMalloc with the residency policy: on out-of-memory, drop every resident
+// weight once and retry.
+int weight_alloc(void **d, size_t bytes) {
+    hipError_t e = hipMalloc(d, bytes);
+    if (e == hipErrorOutOfMemory) {
+        (void)hipGetLastError();
+        int rc = release_weights_locked();
+        if (rc) return rc;
+        e = hipMalloc(d, bytes);
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc(weight)");
+    return DMC_HIP_OK;
+}
+
 // Device copy of the host weight [host, host+bytes), uploading on a miss.
-int resident(const void *host, int64_t bytes, void **dev) {
+// With t_rows > 0 the host bytes hold W [t_rows, t_cols] and the device copy
+// is W^T [t_cols, t_rows]: the drop-in x @ W keeps its weight in the row-dot
+// layout, whose kernel needs one launch where the column-stream layout needs
+// two.  The layout and the column count are part of the key, so the same
+// bytes used through another entry or shape get their own copy.
+int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, int64_t t_cols = 0) {
     Ctx &c = ctx();
     if (bytes <= 0) {
         *dev = c.dummy;
         return DMC_HIP_OK;
     }
     auto t0 = std::chrono::steady_clock::now();
-    const Key key = content_key(host, bytes);
+    Key key = content_key(host, bytes);
+    if (t_rows > 0) key.b = mix64(key.b ^ 0x7472616e73706f73ULL ^ ((uint64_t)t_cols * 0x9E3779B97F4A7C15ULL));
     auto t1 = std::chrono::steady_clock::now();
     c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
     auto it = c.weights.find(key);
@@ -283,17 +303,19 @@ int resident(const void *host, int64_t bytes, void **dev) {
         int rc = release_weights_locked();
         if (rc) return rc;
     }
-    void *d = nullptr;
-    hipError_t e = hipMalloc(&d, (size_t)bytes);
-    if (e == hipErrorOutOfMemory) {  // make room once: drop every resident weight
-        (void)hipGetLastError();
-        int rc = release_weights_locked();
-        if (rc) return rc;
-        e = hipMalloc(&d, (size_t)bytes);
+    void *d = nullptr, *raw = nullptr;
+    int rc = weight_alloc(&d, (size_t)bytes);
+    if (rc) return rc;
+    if (t_rows > 0 && (rc = weight_alloc(&raw, (size_t)bytes))) {
+        (void)hipFree(d);
+        return rc;
     }
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(weight)");
-    e = hipMemcpyAsync(d, host, (size_t)bytes, hipMemcpyHostToDevice, c.stream);
+    hipError_t e = hipMemcpyAsync(raw ? raw : d, host, (size_t)bytes, hipMemcpyHostToDevice, c.stream);
+    if (e == hipSuccess && raw)
+        e = dmc::launch_transpose_bf16(static_cast<const uint16_t *>(raw), static_cast<uint16_t *>(d), t_rows,
+                                       t_cols, c.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
+    if (raw) (void)hipFree(raw);
     if (e != hipSuccess) {
         (void)hipFree(d);
         return hip_fail(e, "weight upload");
@@ -305,7 +327,8 @@ int resident(const void *host, int64_t bytes, void **dev) {
                           std::chrono::steady_clock::now() - t1)
                           .count();
     if (env_flag("DMC_HIP_DEBUG"))
-        fprintf(stderr, "[hip] upload #%zu %lld MB\n", c.weights.size(), (long long)(bytes >> 20));
+        fprintf(stderr, "[hip] upload #%zu %lld MB%s\n", c.weights.size(), (long long)(bytes >> 20),
+                raw ? " (transposed)" : "");
     *dev = d;
     return DMC_HIP_OK;
 }
@@ -403,12 +426,17 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
         HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
     c.st.stage_ns += ns_since(t0);
 
+    // x @ W with one slice runs on the row-dot kernel over a transposed
+    // resident copy (DMC_HIP_CS_LAYOUT=1 keeps the column-stream kernels);
+    // batched calls keep the column-stream kernels, whose one launch covers
+    // every slice.
+    const bool cs_as_rd = !rd && batch == 1 && !env_flag("DMC_HIP_CS_LAYOUT");
     void *dw = nullptr;
-    if ((rc = resident(r, (int64_t)w_bytes, &dw))) return rc;
+    if ((rc = cs_as_rd ? resident(r, (int64_t)w_bytes, &dw, k, n) : resident(r, (int64_t)w_bytes, &dw))) return rc;
 
     auto t1 = std::chrono::steady_clock::now();
     hipError_t e;
-    if (rd) {
+    if (rd || cs_as_rd) {
         dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
                          ydst, n, m, k, n};
         e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);

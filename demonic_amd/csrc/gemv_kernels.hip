@@ -967,6 +967,33 @@ fill_counter_bf16_kernel(uint16_t *__restrict__ dst, uint64_t count, uint64_t of
     }
 }
 
+// Weight layout change for residency: dst [cols, rows] = src [rows, cols]^T,
+// bf16 bit patterns moved unchanged.  64 x 64 tiles through LDS (the row
+// pitch of 66 halves spreads a tile column over the banks); both grid
+// dimensions stride, so any shape fits the 65535-workgroup limit.
+constexpr int kTile = 64;
+
+__global__ void __launch_bounds__(kThreads)
+transpose_bf16_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst, int64_t rows, int64_t cols) {
+    __shared__ uint16_t tile[kTile][kTile + 2];
+    const int tx = threadIdx.x & (kTile - 1);
+    const int ty = threadIdx.x / kTile;  // 0..3
+    for (int64_t r0 = (int64_t)blockIdx.y * kTile; r0 < rows; r0 += (int64_t)gridDim.y * kTile) {
+        for (int64_t c0 = (int64_t)blockIdx.x * kTile; c0 < cols; c0 += (int64_t)gridDim.x * kTile) {
+            for (int i = ty; i < kTile; i += kThreads / kTile) {
+                const int64_t r = r0 + i, c = c0 + tx;
+                if (r < rows && c < cols) tile[i][tx] = src[r * cols + c];
+            }
+            __syncthreads();
+            for (int i = ty; i < kTile; i += kThreads / kTile) {
+                const int64_t c = c0 + i, r = r0 + tx;
+                if (c < cols && r < rows) dst[c * rows + r] = tile[tx][i];
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // ---- dispatch -------------------------------------------------------------
 
 int mt_for(int64_t m) {
@@ -1447,6 +1474,14 @@ hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset
     const uint64_t groups = std::min<uint64_t>(65536, ((uint64_t)count + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(fill_counter_bf16_kernel, dim3((unsigned)groups), dim3(kThreads), 0, s, dst,
                        (uint64_t)count, (uint64_t)offset, key, table);
+    return hipGetLastError();
+}
+
+hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t rows, int64_t cols, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const unsigned gx = (unsigned)std::min<int64_t>(65535, (cols + kTile - 1) / kTile);
+    const unsigned gy = (unsigned)std::min<int64_t>(65535, (rows + kTile - 1) / kTile);
+    hipLaunchKernelGGL(transpose_bf16_kernel, dim3(gx, gy), dim3(kThreads), 0, s, src, dst, rows, cols);
     return hipGetLastError();
 }
 

@@ -115,6 +115,10 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hi
 size_t probe_sink_bytes();
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
 
+// dst [cols, rows] = src [rows, cols]^T for bf16 bit patterns (weight
+// residency in the row-dot layout).
+hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t rows, int64_t cols, hipStream_t stream);
+
 // Synthetic weights for measurements: dst[i] = table[h(offset + i) >> 48],
 // h(j) = splitmix64(j ^ key), table = 65,536 bf16 bit patterns.
 hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset, uint64_t key,

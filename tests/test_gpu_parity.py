@@ -2,9 +2,12 @@
 
 Every case runs the same seeded inputs through the device and through the
 oracle (the reference's dmc_matmul_bf16 chain, compiler/src/jit.rs:29481-29681)
-and applies tests/parity.py's rule.  Row-dot (RD) cases go through
-dmc_matmul_bf16_gpu_t / dmc_hip_gemv_rd, column-stream (CS) cases through the
-drop-in dmc_matmul_bf16_gpu / _batched / _deferred and dmc_hip_gemv_cs.
+and applies tests/parity.py's rule.  Layouts: "rd" goes through
+dmc_matmul_bf16_gpu_t (row-dot kernels on W [N,K]); "cs" through the drop-in
+dmc_matmul_bf16_gpu (x @ W with W [K,N], which a single slice serves with the
+row-dot kernels on a transposed resident copy); "cs_dev" through
+dmc_hip_gemv_cs on device pointers (the column-stream kernels).  Batched and
+deferred calls run the column-stream kernels too.
 """
 import numpy as np
 import pytest
@@ -45,6 +48,26 @@ def run_cs(hip, x, w):
     return hip.matmul_bf16_gpu(x, np.ascontiguousarray(w.T))
 
 
+def run_cs_dev(hip, x, w):
+    """x @ W' through the column-stream kernels on device pointers (W^T [K,N] in HBM)."""
+    x = np.ascontiguousarray(x, np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    m, k = x.shape
+    n = w.shape[0]
+    wt = np.ascontiguousarray(w.T)
+    with hip.DeviceBuffer.from_numpy(wt if wt.size else np.zeros(1, np.uint16)) as dw, \
+            hip.DeviceBuffer.from_numpy(x if x.size else np.zeros(1, np.float32)) as dx, \
+            hip.DeviceBuffer(max(4, 4 * m * n)) as dy:
+        hip.gemv_cs(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        return dy.download(np.float32, (m, n))
+
+
+RUN = {"rd": run_rd, "cs": run_cs, "cs_dev": run_cs_dev}
+LAYOUTS = list(RUN)
+
+
 def ref(x, w):
     return oracle.matmul_bf16_t(x, w)
 
@@ -68,7 +91,7 @@ def test_denormals_survive_and_inf_times_tiny_is_inf(hip):
     w[2, :] = 0x0001          # smallest bf16 subnormal everywhere
     x2 = x.copy()
     x2[0, :] = 1.0
-    for run in (run_rd, run_cs):
+    for run in RUN.values():
         y = run(hip, x, w)[0]
         assert np.isposinf(y[0]), y
         assert y[1] == np.float32(1e-38), y
@@ -87,18 +110,18 @@ SHAPES = [
 
 
 @pytest.mark.parametrize("m,k,n", SHAPES)
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_shapes(hip, m, k, n, layout):
     x, w = case(m, k, n, seed=1000 + m * 7 + k * 13 + n, edge=True)
-    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    y = RUN[layout](hip, x, w)
     check(y, ref(x, w), what=f"{layout} m={m} k={k} n={n}")
 
 
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_k_zero_writes_positive_zero(hip, layout):
     x = np.zeros((2, 0), np.float32)
     w = np.zeros((5, 0), np.uint16)
-    y = hip.matmul_bf16_gpu_t(x, w) if layout == "rd" else hip.matmul_bf16_gpu(x, w.T.copy())
+    y = RUN[layout](hip, x, w)
     assert y.shape == (2, 5)
     assert np.all(y == 0) and not np.any(np.signbit(y))
 
@@ -116,20 +139,20 @@ def test_m_or_n_zero_leaves_out_untouched(hip):
 
 # ---- the BASELINE configurations ---------------------------------------------------------
 
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_c1_full(hip, layout):
     w, x = W.c1()
-    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    y = RUN[layout](hip, x, w)
     rel = check(y, ref(x, w), what=f"C1 {layout}")
     print(f"C1 {layout} rel={rel:.3e}")
 
 
 @pytest.mark.parametrize("shape", W.C5_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}")
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_c5_numerics(hip, shape, layout):
     n, k = shape
     w, x, rows = W.c5(n, k)
-    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)[0]
+    y = RUN[layout](hip, x, w)[0]
     y_ref = ref(x, w)[0]
     rel = check(y, y_ref, what=f"C5 {shape} {layout}")
     print(f"C5 {shape} {layout} rel={rel:.3e}")
@@ -181,11 +204,11 @@ def test_c2_sampled_rows(hip, which):
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_skinny_m(hip, m, layout):
     """The LM-head skinny batch on a 16,387-row slice of the C4 weight shape."""
     x, w = case(m, 4096, 16387, seed=77 + m, scale=0.02)
-    y = (run_rd if layout == "rd" else run_cs)(hip, x, w)
+    y = RUN[layout](hip, x, w)
     check(y, ref(x, w), what=f"skinny m={m} {layout}")
 
 
@@ -279,20 +302,50 @@ def test_weights_resident_by_content(hip):
 
 
 def test_register_weight_then_call(hip):
+    """A registered weight keeps the caller's layout: the x @ W' entry and the
+    batched x @ W entry (column-stream kernels) reuse it without an upload."""
     hip.release_weights()
     x, w = case(1, 2048, 300, seed=12)
+    assert hip.register_weight(w) != 0
+    assert hip.resident_count() == 1
+    y = hip.matmul_bf16_gpu_t(x, w)
+    assert hip.resident_count() == 1
+    check(y, ref(x, w), what="registered rd")
     wt = np.ascontiguousarray(w.T)
     assert hip.register_weight(wt) != 0
-    assert hip.resident_count() == 1
-    y = hip.matmul_bf16_gpu(x, wt)
-    assert hip.resident_count() == 1
-    check(y, ref(x, w), what="registered")
+    assert hip.resident_count() == 2
+    xb = np.concatenate([x[0], x[0]])
+    y2 = hip.matmul_bf16_gpu_batched(xb, wt, 1, 2048, 300, 2, 2048, 0)
+    assert hip.resident_count() == 2
+    check(y2[:300], ref(x, w)[0], what="registered batched cs")
+    check(y2[300:], ref(x, w)[0], what="registered batched cs, slice 1")
 
 
-@pytest.mark.parametrize("layout", ["rd", "cs"])
+def test_dropin_x_at_w_keeps_one_transposed_copy(hip, monkeypatch):
+    """A single-slice x @ W uploads W once, transposed for the row-dot
+    kernels, and reuses that copy; DMC_HIP_CS_LAYOUT=1 runs the
+    column-stream kernels on the weight as given instead.  Both match."""
+    hip.release_weights()
+    x, w = case(2, 3000, 777, seed=14, edge=True)
+    wt = np.ascontiguousarray(w.T)
+    y1 = hip.matmul_bf16_gpu(x, wt)
+    assert hip.resident_count() == 1 and hip.resident_bytes() == wt.nbytes
+    y2 = hip.matmul_bf16_gpu(x, wt.copy())
+    assert hip.resident_count() == 1
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+    monkeypatch.setenv("DMC_HIP_CS_LAYOUT", "1")
+    y3 = hip.matmul_bf16_gpu(x, wt)
+    assert hip.resident_count() == 2           # the as-given copy
+    y_ref = ref(x, w)
+    check(y1, y_ref, what="x@W transposed copy")
+    check(y3, y_ref, what="x@W column-stream")
+    hip.release_weights()
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
 def test_repeat_calls_bit_identical(hip, layout):
     x, w = case(1, 14336, 1024, seed=13, scale=0.02)
-    run = run_rd if layout == "rd" else run_cs
+    run = RUN[layout]
     a = run(hip, x, w)
     b = run(hip, x, w)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
