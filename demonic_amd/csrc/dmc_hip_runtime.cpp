@@ -304,7 +304,7 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
         if (rc) return rc;
     }
     void *d = nullptr, *raw = nullptr;
-    int rc = weight_alloc(&d, (size_t)bytes);
+    int rc = weight_alloc(&d, (size_t)(bytes + dmc::kWeightSlack));  // slack: see RdProblem::w_slack
     if (rc) return rc;
     if (t_rows > 0 && (rc = weight_alloc(&raw, (size_t)bytes))) {
         (void)hipFree(d);
@@ -438,7 +438,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     hipError_t e;
     if (rd || cs_as_rd) {
         dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
-                         ydst, n, m, k, n};
+                         ydst, n, m, k, n, dmc::kWeightSlack};
         e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
     } else {
         dmc::CsProblem p{static_cast<const uint16_t *>(dw), static_cast<const float *>(c.dx.p),

@@ -131,6 +131,17 @@ __device__ __forceinline__ u32x4 load_w16(__amdgpu_buffer_rsrc_t r, uint32_t byt
     return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kLoadNT);
 }
 
+// The same with a wave-uniform part of the offset in the instruction's scalar
+// offset.  Measured on gfx950: the range check covers the sum of both offsets
+// (per dword), like a single offset.  Keeping a loop's row offset scalar and
+// the lane's offset loop-invariant leaves no per-load vector address
+// arithmetic, whose temporaries the register allocator otherwise places in
+// registers just freed by a load -- and the compiler then waits for that
+// load's whole batch before the next one may issue.
+__device__ __forceinline__ u32x4 load_w16(__amdgpu_buffer_rsrc_t r, uint32_t lane_off, uint32_t uniform_off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, uniform_off, kLoadNT);
+}
+
 __device__ __forceinline__ float widen_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
@@ -197,15 +208,16 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     // x rows [m0, m0 + mrows): activation row m0 + m reads row min(m, mrows - 1).
     const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4);
     uint32_t eoff[KV];
+    bool has[KV];
     u32x4 xa[MT][KV], xb[MT][KV];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
         const int e = ((j * NW + wave) * 64 + lane) * 8;
-        const bool has = e < K;
-        eoff[j] = has ? (uint32_t)e * 2 : kOutOfRange;
+        has[j] = e < K;
+        eoff[j] = has[j] ? (uint32_t)e * 2 : kOutOfRange;
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const uint32_t xo = has ? ((uint32_t)min(m, mrows - 1) * (uint32_t)K + (uint32_t)e) * 4 : kOutOfRange;
+            const uint32_t xo = has[j] ? ((uint32_t)min(m, mrows - 1) * (uint32_t)K + (uint32_t)e) * 4 : kOutOfRange;
             xa[m][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
             xb[m][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16, 0, 0);
         }
@@ -224,7 +236,7 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
         for (int q = 0; q < ROWS; ++q) {
             const uint32_t base = (uint32_t)(r0 + q - rb) * row_bytes;
 #pragma unroll
-            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, base + eoff[j]);
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], base);
         }
     };
     load(ba, rb);
@@ -238,6 +250,14 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
                 xr[m][j][q] = __uint_as_float(xa[m][j][q]);
                 xr[m][j][q + 4] = __uint_as_float(xb[m][j][q]);
             }
+    // A vector past K reads zero weights and zero x; its weights become bf16
+    // -0.0 (0x8000) so that each of its products is -0.0f, the exact additive
+    // identity: it leaves any chain unchanged, a -0.0f (a product that
+    // underflowed) included.  Applied to the weights as they arrive, not to x:
+    // a select on x would make the prologue wait for x.
+    uint32_t pad[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) pad[j] = has[j] ? 0u : 0x80008000u;
 
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
         float acc[MT][ROWS];
@@ -251,7 +271,7 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
             for (int e = 0; e < 8; ++e)
 #pragma unroll
                 for (int q = 0; q < ROWS; ++q) {
-                    const uint32_t d = wv[q][j][e >> 1];
+                    const uint32_t d = wv[q][j][e >> 1] | pad[j];
                     const float w = (e & 1) ? widen_hi(d) : widen_lo(d);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
@@ -279,6 +299,127 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
 #pragma unroll
         for (int w = 1; w < NW; ++w) s += red[w][m][r];
         if (m < mrows) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
+    }
+}
+
+// ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
+//
+// The layout of gemv_rd_stream_kernel (NW waves split k; lane l of wave w
+// owns the 8-element windows p = (j*NW + w)*64 + l of every row, x windows
+// in registers, two register buffers of ROWS rows, unconditional loads), for
+// rows that do not start on a 16-byte boundary: each window is one 128-bit
+// buffer load at the row's own 2-byte-aligned offset.  Measured on gfx950:
+// buffer loads honour such offsets exactly, and the range check is per dword
+// of the load (a dword is returned only when it lies wholly inside the
+// range).  The descriptor starts on the 4-byte boundary at or below the first
+// row; its range ends `tail` (0 or 2) bytes past the last element, rounded up
+// to a dword.  A row's last dword may run 2 bytes past the row: inside the
+// range for every row but the matrix's last, whose element K-1 is lost when
+// it sits at an offset of 2 mod 4 with K odd unless 2 bytes of padding follow
+// the matrix (tail = 2) -- the planner only picks this kernel when one of the
+// two holds.  Without padding the range reaches at most 2 bytes past the last
+// element, in the same aligned dword and so the same page.  Elements
+// at or past K (the next row's bits may be inf or NaN), whole windows past K
+// included, become bf16 -0.0 (0x8000); their x is +0.0 (read past the end of
+// x), so each such product is -0.0f, the exact additive identity, and padding
+// never turns a -0.0f chain into +0.0f.  M == 1.
+template <int NW, int KV, int ROWS>
+__global__ void __launch_bounds__(64 * NW)
+gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                         int K, int64_t ldw, int rpw, int tail) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = (int)blockIdx.x * rpw;
+    const int re = min(N, rb + rpw);
+
+    const uintptr_t base = reinterpret_cast<uintptr_t>(W + (int64_t)rb * ldw) & ~(uintptr_t)3;
+    const uintptr_t end = reinterpret_cast<uintptr_t>(W + (int64_t)(re - 1) * ldw + K);
+    const __amdgpu_buffer_rsrc_t rs =
+        weight_rsrc(reinterpret_cast<const void *>(base), (uint32_t)((end - base + tail + 3) & ~(uintptr_t)3));
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4u);
+
+    uint32_t coff[KV];
+    uint32_t mask[KV][4];
+    u32x4 xa[KV], xb[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int p = (j * NW + wave) * 64 + lane;
+        const int valid = min(max(K - 8 * p, 0), 8);  // elements of window p inside the row
+        coff[j] = valid > 0 ? (uint32_t)p * 16u : kOutOfRange;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            mask[j][d] = (2 * d < valid ? 0x0000ffffu : 0u) | (2 * d + 1 < valid ? 0xffff0000u : 0u);
+        const uint32_t xo = valid > 0 ? (uint32_t)p * 32u : kOutOfRange;
+        xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+        xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
+    }
+    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
+
+    // Row r's first element, in bytes from the descriptor's base.  No branch on
+    // r < re (a branch around a load address makes the compiler wait for every
+    // load in flight): a row past re yields offsets at or past the range's end,
+    // which read zeros or the last row's tail, and its sum is never stored.
+    auto row_off = [&](int r) -> uint32_t {
+        return (uint32_t)(reinterpret_cast<uintptr_t>(W + (int64_t)r * ldw) - base);
+    };
+
+    __shared__ float red[NW][kMaxRpw];
+    u32x4 ba[ROWS][KV], bb[ROWS][KV];
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int r0) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const uint32_t o = row_off(r0 + q);
+#pragma unroll
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, coff[j], o);
+        }
+    };
+    load(ba, rb);
+    float xr[KV][8];
+#pragma unroll
+    for (int j = 0; j < KV; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xr[j][q] = __uint_as_float(xa[j][q]);
+            xr[j][q + 4] = __uint_as_float(xb[j][q]);
+        }
+
+    // A wave whose windows of the last block all lie past K skips that block's
+    // arithmetic (a wave-uniform branch around arithmetic only; its loads, out
+    // of range, stay unconditional): k = 4097 then costs 1.125x the
+    // arithmetic of k = 4096 instead of 2x.
+    const bool last_block = (((KV - 1) * NW + wave) * 64) * 8 < K;
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            float acc = init;
+#pragma unroll
+            for (int j = 0; j < KV; ++j) {
+                if (j == KV - 1 && !last_block) break;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t v = (wv[q][j][d] & mask[j][d]) | (~mask[j][d] & 0x80008000u);
+                    acc = fmaf(xr[j][2 * d], widen_lo(v), acc);
+                    acc = fmaf(xr[j][2 * d + 1], widen_hi(v), acc);
+                }
+            }
+            const float s = wave_sum_dpp(acc);
+            if (lane == 0 && r0 + q < re) red[wave][r0 - rb + q] = s;
+        }
+    };
+    for (int r0 = rb; r0 < re; r0 += 2 * ROWS) {
+        load(bb, r0 + ROWS);
+        sum_rows(ba, r0);
+        if (r0 + ROWS >= re) break;
+        load(ba, r0 + 2 * ROWS);
+        sum_rows(bb, r0 + ROWS);
+    }
+    __syncthreads();
+    const int nr = re - rb;
+    for (int t = threadIdx.x; t < nr; t += 64 * NW) {
+        float s = red[0][t];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w][t];
+        Y[rb + t] = s;
     }
 }
 
@@ -841,7 +982,7 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     u32x4 ba[U], bb[U];
     auto load = [&](u32x4 (&b)[U], int r) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) b[u] = load_w16(rsw, (uint32_t)(r - r0 + u) * row_bytes + loff);
+        for (int u = 0; u < U; ++u) b[u] = load_w16(rsw, loff, (uint32_t)(r - r0 + u) * row_bytes);
     };
     auto sum_rows = [&](const u32x4 (&b)[U], int r) {
         if (r + U <= r1) {
@@ -1078,6 +1219,41 @@ hipError_t rs_rows(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hi
     return hipErrorInvalidValue;
 }
 
+template <int NW, int KV>
+hipError_t rd_unaligned_go(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    // one row per step for KV = 2 and KV > 4: the compiler keeps the other
+    // buffer's loads in flight there (two rows of KV = 2 made it drain them)
+    constexpr int ROWS = (KV <= 4 && KV != 2) ? 2 : 1;
+    if (pl.rows != ROWS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_rd_unaligned_kernel<NW, KV, ROWS>), dim3((unsigned)pl.grid_x), dim3(64 * NW), 0, s, p.w,
+                       p.x, p.y, (int)p.n, (int)p.k, p.ldw, pl.rpw, p.w_slack >= 2 ? 2 : 0);
+    return hipGetLastError();
+}
+
+hipError_t rd_unaligned_dispatch(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+    if (pl.mt != 1) return hipErrorInvalidValue;
+    if (pl.waves == 8) {
+        switch (pl.kvec) {
+        case 1: return rd_unaligned_go<8, 1>(p, pl, s);
+        case 2: return rd_unaligned_go<8, 2>(p, pl, s);
+        case 3: return rd_unaligned_go<8, 3>(p, pl, s);
+        case 4: return rd_unaligned_go<8, 4>(p, pl, s);
+        case 5: return rd_unaligned_go<8, 5>(p, pl, s);
+        case 6: return rd_unaligned_go<8, 6>(p, pl, s);
+        case 7: return rd_unaligned_go<8, 7>(p, pl, s);
+        case 8: return rd_unaligned_go<8, 8>(p, pl, s);
+        }
+        return hipErrorInvalidValue;
+    }
+    if (pl.kvec != 1) return hipErrorInvalidValue;
+    switch (pl.waves) {
+    case 1: return rd_unaligned_go<1, 1>(p, pl, s);
+    case 2: return rd_unaligned_go<2, 1>(p, pl, s);
+    case 4: return rd_unaligned_go<4, 1>(p, pl, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t rs_dispatch(const RdGroupArgs &ga, const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     if (pl.waves == 8) {
         switch (pl.kvec) {
@@ -1264,6 +1440,39 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) return sp;
     }
 
+    // Streaming over misaligned rows (odd K, offset views) with unaligned
+    // 128-bit loads: M == 1, x 16-byte aligned, and the matrix's last element
+    // readable (padding after it, or not at 2 mod 4 with K odd; see the kernel).
+    const uintptr_t last_elem = reinterpret_cast<uintptr_t>(p.w + ((p.n - 1) * p.ldw + p.k - 1));
+    const bool last_ok = p.w_slack >= 2 || !((last_elem & 3) == 2 && (p.k & 1) == 1);
+    if (pl.vec < 8 && p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) && last_ok &&
+        env_int("DMC_HIP_RD_UNALIGNED", 1) != 0) {
+        const int nw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
+        const int kv = (int)((p.k + nw * 512 - 1) / (nw * 512));
+        const int rpw_default = kv >= 2 ? 8 : 4;
+        const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
+        int rpw = rpw_default;
+        while (rpw > 2 && (p.n + rpw - 1) / rpw < min_blocks) rpw >>= 1;
+        // Only when the last block of windows is at least half full: measured
+        // on MI355X against the general kernel, k = 4095 67% vs 57% of peak,
+        // 11007 64% vs 60%, 14335 64% vs 56%, but k = 4097 (one element in its
+        // last block) 53% vs 61%.
+        const int64_t block = (int64_t)nw * 512;
+        if (p.k - (kv - 1) * block >= block / 2 && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
+            (p.n + rpw - 1) / rpw <= INT32_MAX) {
+            RdPlan sp{};
+            sp.vec = pl.vec;
+            sp.rows = (kv <= 4 && kv != 2) ? 2 : 1;
+            sp.mt = 1;
+            sp.waves = nw;
+            sp.kvec = kv;
+            sp.rpw = rpw;
+            sp.grid_x = (p.n + rpw - 1) / rpw;
+            sp.grid_y = 1;
+            return sp;
+        }
+    }
+
     // General kernel.
     pl.mt = mt_for(p.m);
     // Rows per workgroup: 4 keeps >= 4 workgroups per CU at the decode
@@ -1403,6 +1612,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
 #undef DMC_RDM
         return hipErrorInvalidValue;
     }
+    if (pl.kvec > 0 && pl.vec < 8) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0) {
         RdGroup g{};
         g.w[0] = p.w;

@@ -27,7 +27,11 @@ struct RdProblem {
     float *y;           // [m, ldy]
     int64_t ldy;        // elements between output rows (>= n)
     int64_t m, k, n;
+    int64_t w_slack = 0;  // bytes readable past the last weight element (allocation padding)
 };
+
+// Padding the library allocates after every resident weight.
+constexpr int64_t kWeightSlack = 16;
 
 struct CsProblem {
     const uint16_t *w;  // slice z: w + z*rs, [k, n] row-major

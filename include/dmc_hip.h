@@ -138,10 +138,12 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
 
 /* Launch plan a GEMV would use on this device (or on a 256-CU gfx950 when no
  * device is present), for tests and reports.  out8 receives
- * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes, waves, rows_per_group}:
- * for the row-dot layout kvec-streaming plans report waves = 1..8 and
- * rows_per_group = weight rows per workgroup; `slices` is then the number of
- * 8-element k vectors per lane (0 for the general kernel). */
+ * {vec, rows_or_rw, mt, grid_x, slices, workspace_bytes, waves, rows_per_group}.
+ * Row-dot layout: `vec` is the weight rows' alignment in bf16 elements (8 =
+ * 16 bytes); `slices` > 0 is a streaming plan with that many 8-element k
+ * windows per lane (with vec < 8, the variant that reads misaligned rows with
+ * unaligned 128-bit loads), 0 the general kernel, -1 / -6 the MFMA layouts; waves and
+ * rows_per_group (weight rows per workgroup) describe the workgroup. */
 int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k,
                      int64_t n, int64_t batch, int64_t rs, int64_t *out8);
 

@@ -137,9 +137,42 @@ def test_rowdot_mfma_layouts(monkeypatch):
 
 
 def test_rowdot_falls_back_to_general_kernel():
-    for k, w in [(32776, 256), (4097, 256), (4096, 258), (0, 256)]:
-        p = d.plan("rd", 1, k, 1000, x_addr=256, w_addr=w)
-        assert p.slices == 0 and p.waves == 4, (k, w, p)
+    # k beyond the register budget, k == 0, several activation rows on
+    # misaligned weights, x not 16-byte aligned
+    for m, k, x, w in [(1, 32776, 256, 256), (1, 0, 256, 256), (2, 4097, 256, 256), (1, 4097, 260, 256),
+                       (1, 32770, 256, 258)]:
+        p = d.plan("rd", m, k, 1000, x_addr=x, w_addr=w)
+        assert p.slices == 0 and p.waves == 4, (m, k, x, w, p)
+
+
+@pytest.mark.parametrize("k,w,waves,kvec,rows", [(6145, 256, 8, 2, 1), (4096, 258, 8, 1, 2), (11007, 256, 8, 3, 2),
+                                                 (1023, 256, 2, 1, 2), (257, 256, 1, 1, 2), (16384, 262, 8, 4, 2),
+                                                 (32767, 256, 8, 8, 1), (4095, 256, 8, 1, 2)])
+def test_rowdot_misaligned_rows_stream_unaligned(k, w, waves, kvec, rows):
+    """Rows that do not start on 16-byte boundaries (odd k, an offset
+    weight) at m = 1: the streaming layout with unaligned 128-bit loads,
+    reported as a streaming plan (slices > 0) with vec < 8.  With n odd the
+    matrix's last element ends on a dword boundary, so no padding is needed."""
+    p = d.plan("rd", 1, k, 11007, x_addr=256, w_addr=w)
+    assert p.vec < 8 and (p.waves, p.slices, p.rows_or_rw, p.mt) == (waves, kvec, rows, 1), p
+    assert p.grid_x * p.rows_per_group >= 11007
+
+
+def test_rowdot_unaligned_needs_a_readable_last_element():
+    """Odd k and n even put the matrix's last element at 2 mod 4: its 128-bit
+    window would need 2 bytes past the caller's allocation, so a caller's
+    weight gets the general kernel (the drop-in's resident copies carry
+    padding and keep the unaligned kernel)."""
+    assert d.plan("rd", 1, 4095, 11008, x_addr=256, w_addr=256).slices == 0
+    assert d.plan("rd", 1, 4095, 11007, x_addr=256, w_addr=256).slices == 1
+    assert d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=258).slices == 1   # k even: never straddles
+
+
+def test_rowdot_unaligned_needs_a_well_filled_last_block():
+    """k = 4097 puts one element in a second block of windows: the general
+    kernel measured faster there."""
+    assert d.plan("rd", 1, 4097, 11007, x_addr=256, w_addr=256).slices == 0
+    assert d.plan("rd", 1, 7, 1001, x_addr=256, w_addr=256).slices == 0
 
 
 def test_column_stream_plans_split_k_and_size_workspace():

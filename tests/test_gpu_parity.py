@@ -117,6 +117,42 @@ def test_shapes(hip, m, k, n, layout):
     check(y, ref(x, w), what=f"{layout} m={m} k={k} n={n}")
 
 
+@pytest.mark.parametrize("offset,k,n", [(2, 4096, 300), (6, 4104, 257), (14, 2048, 33), (10, 777, 1000),
+                                        (4, 16384, 70), (2, 11007, 129)])
+def test_misaligned_weight_view(hip, offset, k, n):
+    """W [n,k] starting `offset` bytes into its device region, which ends
+    right after the last row: rows on 2-byte boundaries, windows re-aligned
+    in registers, the last window's second chunk past the region's end."""
+    x, w = case(1, k, n, seed=offset * 31 + k + n, edge=True)
+    with hip.DeviceBuffer(offset + w.nbytes) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * n) as dy:
+        dw.upload(w, offset=offset)
+        hip.gemv_rd(dx.addr, dw.addr + offset, dy, 1, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (1, n))
+    check(y, ref(x, w), what=f"view +{offset} k={k} n={n}")
+
+
+@pytest.mark.parametrize("k", [1, 7, 1000, 1001, 4096, 14336])
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_underflowing_products_keep_their_zero_sign(hip, k, layout):
+    """Row 0: every product is negative and underflows, so the reference chain
+    (fmaf from +0.0, jit.rs:29655) ends at -0.0 -- and so does every other
+    summation order, as long as the device's padding (lanes past K, windows
+    past K, masked tails) adds only -0.0.  Row 1: the same products with the
+    opposite sign end at +0.0.  (A zero made of underflowing products of both
+    signs takes the sign of the last one in k order: that case is
+    order-dependent and not asserted.)"""
+    x = np.full((1, k), np.float32(-1e-38), np.float32)
+    w = np.full((2, k), 0x0001, np.uint16)     # smallest bf16 subnormal: |x*w| ~ 9e-79
+    w[1, :] = 0x8001                           # row 1: positive products
+    y_ref = ref(x, w)
+    assert y_ref[0, 0] == 0 and np.signbit(y_ref[0, 0])
+    assert y_ref[0, 1] == 0 and not np.signbit(y_ref[0, 1])
+    y = RUN[layout](hip, x, w)
+    check(y, y_ref, what=f"underflow signs k={k} {layout}")
+
+
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_k_zero_writes_positive_zero(hip, layout):
     x = np.zeros((2, 0), np.float32)
