@@ -444,11 +444,13 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
 //   w = +-inf or NaN: multiplies hi only -- the mid and lo MFMAs see 0 there,
 //     because inf * (mid == 0) would be NaN where the reference has inf.
 //
-// Workgroup: R (1, 2 or kMfmaTiles) tiles of 16 weight rows; its NW waves
-// split k into contiguous ranges of 64-element pairs.  In a pair, lane (i, g) of the A operand reads
-// 32 contiguous bytes of row i at k0 + 16g, so the four lane groups of a row
-// read its 128-byte line in one step; the B operand uses the same k mapping.
-constexpr int kMfmaTiles = 4;
+// Zeros: the MFMA rounds a nonzero sum smaller than half the least f32
+// subnormal to +0 whatever its sign, where the reference's fmaf gives the
+// signed zero (every product underflowing negative ends at -0).  So an output
+// that comes out exactly zero is settled by the reference's own rule: +0 when
+// its activation row or its weight row holds only zeros (every product is an
+// exact zero and the chain never leaves +0), otherwise the chain itself,
+// fmaf over ascending k from +0 (rare: underflow or exact cancellation).
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -481,14 +483,13 @@ __device__ __forceinline__ bool wave_has_inf_nan(uint32_t mx) {
 
 // The three bf16 terms of one f32.
 __device__ __forceinline__ void split3(float v, uint32_t &h, uint32_t &m, uint32_t &l) {
+    // Selects, not branches: every lane of the rows16 layout splits 16 values per line.
     const uint32_t u = __float_as_uint(v);
     const bool fin = (u & 0x7f800000u) != 0x7f800000u;
-    h = u >> 16;
-    if (!fin) {
-        if (u & 0x007fffffu) h |= 0x0040u;          // NaN: stay NaN after truncation
-    } else if ((h & 0x7fffu) == 0 && (u & 0x7fffffffu) != 0) {
-        h |= 1u;                                     // |x| < 2^-133: keep hi nonzero
-    }
+    const uint32_t t = u >> 16;
+    const uint32_t nan_q = !fin && (u & 0x007fffffu) ? 0x0040u : 0u;                 // NaN: stay NaN after truncation
+    const uint32_t keep = fin && (t & 0x7fffu) == 0 && (u & 0x7fffffffu) != 0 ? 1u : 0u;  // |x| < 2^-133: hi nonzero
+    h = t | nan_q | keep;
     const float r1 = fin ? v - __uint_as_float(h << 16) : 0.0f;
     m = __float_as_uint(r1) >> 16;
     const float r2 = r1 - __uint_as_float(m << 16);
@@ -507,94 +508,84 @@ __device__ __forceinline__ void split8(const float *v, u32x4 &hi, u32x4 &mid, u3
     }
 }
 
-template <int NW, int R>
-__global__ void __launch_bounds__(64 * NW)
-gemv_rd_mfma_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
-                    int K, int M) {
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int i16 = lane & 15;
-    const int g = lane >> 4;
-    const int row0 = blockIdx.x * (R * 16);
-    const int nrows = min(R * 16, N - row0);
-    const int m0 = blockIdx.y * 16;
-    const int npairs = K / 64;
-    const int per = (npairs + NW - 1) / NW;
-    const int p0 = min(npairs, wave * per);
-    const int p1 = min(npairs, p0 + per);
-
-    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
-    uint32_t roff[R];
+// The reference chain for one output: fmaf over ascending k from +0 (K a
+// multiple of 8, rows 16-byte aligned).
+__device__ float reference_chain(const uint16_t *__restrict__ w, const float *__restrict__ x, int K) {
+    float acc = 0.0f;
+    for (int k = 0; k < K; k += 8) {
+        const u32x4 wv = *reinterpret_cast<const u32x4 *>(w + k);
+        const float4 xa = *reinterpret_cast<const float4 *>(x + k);
+        const float4 xb = *reinterpret_cast<const float4 *>(x + k + 4);
+        const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
 #pragma unroll
-    for (int t = 0; t < R; ++t) roff[t] = (uint32_t)min(t * 16 + i16, nrows - 1) * (uint32_t)K * 2u;
-    const bool mlive = m0 + i16 < M;
-    const float *xr = X + (int64_t)min(m0 + i16, M - 1) * K;
-
-    const float z = p0 < p1 ? 0.0f : -0.0f;
-    f32x4 acc[R];
-#pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = f32x4{z, z, z, z};
-
-    for (int p = p0; p < p1; ++p) {
-        const int kb = p * 64 + g * 16;
-        float xv[16];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const float4 v = mlive ? *reinterpret_cast<const float4 *>(xr + kb + 4 * q) : float4{0, 0, 0, 0};
-            xv[4 * q] = v.x; xv[4 * q + 1] = v.y; xv[4 * q + 2] = v.z; xv[4 * q + 3] = v.w;
-        }
-        u32x4 wa[R], wb[R];
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-            wa[t] = load_w16(rs, roff[t] + (uint32_t)kb * 2u);
-            wb[t] = load_w16(rs, roff[t] + (uint32_t)kb * 2u + 16u);
-        }
-        u32x4 hA, mA, lA, hB, mB, lB;
-        split8(xv, hA, mA, lA);
-        split8(xv + 8, hB, mB, lB);
-        uint32_t mx = 0;
-#pragma unroll
-        for (int t = 0; t < R; ++t)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) mx = max_mag(max_mag(mx, wa[t][q]), wb[t][q]);
-        const bool any_special = wave_has_inf_nan(mx);
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-            acc[t] = mfma_bf16(wa[t], hA, acc[t]);
-            acc[t] = mfma_bf16(wb[t], hB, acc[t]);
-            u32x4 wa2 = wa[t], wb2 = wb[t];
-            if (any_special) {
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    wa2[q] &= ~inf_nan_mask(wa2[q]);
-                    wb2[q] &= ~inf_nan_mask(wb2[q]);
-                }
-            }
-            acc[t] = mfma_bf16(wa2, mA, acc[t]);
-            acc[t] = mfma_bf16(wb2, mB, acc[t]);
-            acc[t] = mfma_bf16(wa2, lA, acc[t]);
-            acc[t] = mfma_bf16(wb2, lB, acc[t]);
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t bits = e & 1 ? wv[e >> 1] & 0xffff0000u : wv[e >> 1] << 16;
+            acc = fmaf(xv[e], __uint_as_float(bits), acc);
         }
     }
+    return acc;
+}
 
-    // acc[t] of lane l holds weight rows row0 + 16t + 4(l/16) + r, activation row m0 + l%16.
-    __shared__ f32x4 red[NW][R][64];
+// Wave-uniform: does the row hold an element other than +-0?  (bytes: 16 * n16)
+__device__ bool wave_row_nonzero(const void *row, int n16, uint32_t mask) {
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(row);
+    uint32_t acc = 0;
+    for (int c = threadIdx.x & 63; c < n16; c += 64) {
+        const u32x4 v = p[c];
+        acc |= (v[0] | v[1] | v[2] | v[3]) & mask;
+    }
+    return __builtin_amdgcn_ballot_w64(acc != 0) != 0;
+}
+
+// One wave's outputs after the zero rule above.  Lane l holds s[t][r] for
+// weight row base[t] + 4(l/16) + r of W and activation row m of X; `live`
+// marks the ones it stores.  All 64 lanes call this; the rows are walked
+// wave-uniformly.  Rare path: entered only when some output is exactly zero.
+template <int T>
+__device__ void settle_zeros(f32x4 (&s)[T], const bool (&live)[T][4], const int (&base)[T], const uint16_t *W,
+                             const float *X, int K, int m) {
+    const int g = (threadIdx.x & 63) >> 4;
+    bool zero[T][4];
+    bool any = false;
 #pragma unroll
-    for (int t = 0; t < R; ++t) red[wave][t][lane] = acc[t];
-    __syncthreads();
-    for (int e = threadIdx.x; e < R * 64; e += 64 * NW) {
-        const int t = e >> 6, l = e & 63;
-        f32x4 s = red[0][t][l];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w][t][l];
-        const int m = m0 + (l & 15);
-        if (m >= M) continue;
+    for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = t * 16 + (l >> 4) * 4 + r;
-            if (row < nrows) Y[(int64_t)m * N + row0 + row] = s[r];
+            zero[t][r] = live[t][r] && s[t][r] == 0.0f;
+            any |= zero[t][r];
+        }
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;
+    // Is this lane's activation row nonzero?  Lanes j = 0..15 hold every row
+    // the wave has.
+    bool xnz = false;
+    for (int j = 0; j < 16; ++j) {
+        const int mj = __builtin_amdgcn_readlane(m, j);
+        if (__builtin_amdgcn_ballot_w64(any && m == mj) != 0) {
+            const bool nz = wave_row_nonzero(X + (int64_t)mj * K, K / 4, 0x7fffffffu);
+            if (m == mj) xnz = nz;
         }
     }
+    // Zero outputs become +0, or the chain's value where both rows are nonzero.
+    bool chain[T][4];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            chain[t][r] = false;
+            if (zero[t][r]) s[t][r] = 0.0f;
+            for (int gq = 0; gq < 4; ++gq) {
+                const bool ask = zero[t][r] && xnz && g == gq;
+                if (__builtin_amdgcn_ballot_w64(ask) == 0) continue;
+                const int row = base[t] + 4 * gq + r;
+                const bool nz = wave_row_nonzero(W + (int64_t)row * K, K / 8, 0x7fff7fffu);
+                if (ask) chain[t][r] = nz;
+            }
+        }
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (chain[t][r]) s[t][r] = reference_chain(W + (int64_t)(base[t] + 4 * g + r) * K, X + (int64_t)m * K, K);
 }
 
 // Fourth MFMA layout ("wide"): what bounds the MFMA kernels on MI355X is the
@@ -720,15 +711,208 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
         step(c + 1, ra, rb);
     }
 
-    const int m = m0 + i16;
-    if (m < M) {
+    const int base[2] = {wave * 32, wave * 32 + 16};
+    bool live[2][4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = (wave * 2 + t) * 16 + g * 4 + r;
-                if (row < nrows) Y[(int64_t)m * N + row0 + row] = acc[t][r];
+        for (int r = 0; r < 4; ++r) live[t][r] = m0 + i16 < M && base[t] + g * 4 + r < nrows;
+    settle_zeros(acc, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (live[t][r]) Y[(int64_t)(m0 + i16) * N + row0 + base[t] + g * 4 + r] = acc[t][r];
+}
+
+// Fifth MFMA layout ("rows16"), for a few activation rows: 16 weight rows per
+// workgroup, read whole.  The rows advance in windows of 8 lines (1 KiB per
+// row); wave w owns line w of every window, 64 k elements = two MFMA k-blocks.
+// On MI355X the read pattern decides the rate: 16 rows x 1 KiB per window
+// streams ~10% faster than the wide layout's 256 rows x 128 bytes, and a load
+// instruction must cover whole lines (8 rows x 128 bytes here) -- one in the
+// MFMA operand layout (16 rows x 64 bytes) streams ~15% slower still.  So each
+// wave loads its 16 rows x 128 bytes as whole lines and passes them through a
+// private LDS tile into the operand layout (one wave's LDS operations run in
+// program order: no barrier).
+//
+// x: splitting f32 into three bf16 terms is the costly vector work here, and
+// the B operand has 16 columns however few activation rows there are.  With
+// MC = 4 or 8 activation rows per workgroup, lane l loads and splits the
+// 64 MC / 64 values x[m0 + l/(64/MC)][64L + MC(l%(64/MC)), +MC) and writes the
+// three terms to a private LDS tile; B columns MC..15 read a row of zeros.
+// With MC = 16 each lane loads its B operand directly (lanes past M load from
+// outside the buffer: zeros, no traffic) and splits 16 values.  The waves' partial sums meet once, at the
+// end, in LDS in wave order.  Loads run one line ahead (two register sets);
+// lines past the last load from outside the buffers.
+constexpr int kRows16Pitch = 144;
+
+template <int MC>
+__global__ void __launch_bounds__(512)
+gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
+                           int N, int K, int M) {
+    static_assert(MC == 4 || MC == 8 || MC == 16, "activation rows per workgroup");
+    constexpr bool kCompact = MC < 16;
+    constexpr int kLanesPerRow = 64 / MC;  // compact x: lanes per activation row
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int i16 = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * 16;
+    const int nrows = min(16, N - row0);
+    const int m0 = blockIdx.y * MC;
+    const int mrows = min(MC, M - m0);
+    const int nlines = K >> 6;
+
+    __shared__ __attribute__((aligned(16))) uint8_t wt[8][16 * kRows16Pitch];  // 8 x 2.25 KiB
+    // MC = 4, 8: per wave, three planes of MC x rows (64 bf16 each) and a zero row.
+    constexpr int kXRows = kCompact ? MC + 1 : 1;
+    __shared__ __attribute__((aligned(16))) uint8_t xt[8][3][kXRows][kRows16Pitch];
+    __shared__ f32x4 red[8][64];                                                 // 8 KiB
+    uint8_t *const tile = wt[wave];
+
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m0 * K, (uint32_t)((int64_t)mrows * K * 4));
+    // Whole-line staging: load j (0, 1) covers rows 8j + lane/8, bytes 16*(lane%8) of the line.
+    const int srow = lane >> 3, scol = (lane & 7) * 16;
+    const uint32_t woff0 = srow < nrows ? (uint32_t)srow * (uint32_t)K * 2u + scol : kOutOfRange;
+    const uint32_t woff1 = srow + 8 < nrows ? (uint32_t)(srow + 8) * (uint32_t)K * 2u + scol : kOutOfRange;
+    // x offsets.  MC = 16: lane (j, g) takes x[m0 + j][64L + 32b + 8g, +8) for k-block b.
+    // MC = 4, 8: lane l takes x[m0 + l/(64/MC)][64L + MC(l%(64/MC)), +MC).
+    const int xm = kCompact ? lane / kLanesPerRow : i16;
+    const int xq = lane % kLanesPerRow;
+    const uint32_t xoff =
+        xm < mrows ? ((uint32_t)xm * (uint32_t)K + (kCompact ? (uint32_t)(MC * xq) : 8u * g)) * 4u : kOutOfRange;
+    if (kCompact) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+            if (lane < kRows16Pitch / 16)
+                *reinterpret_cast<u32x4 *>(&xt[wave][p][MC][lane * 16]) = u32x4{0, 0, 0, 0};
+    }
+
+    struct Line {
+        u32x4 w0, w1;          // weight rows srow, srow + 8
+        u32x4 x0, x1, x2, x3;  // MC = 16: x for k-block 0 (x0, x1) and 1 (x2, x3); MC = 4: x0; MC = 8: x0, x1
+    };
+    // Line L's loads; lines past the end read zeros from outside the buffers.
+    auto load = [&](Line &r, int L) {
+        const bool live = L < nlines;
+        const uint32_t lw = (uint32_t)L * 128u, lx = (uint32_t)L * 256u;
+        r.w0 = load_w16(rs, live ? woff0 : kOutOfRange, lw);
+        r.w1 = load_w16(rs, live ? woff1 : kOutOfRange, lw);
+        const uint32_t xo = live ? xoff : kOutOfRange;
+        r.x0 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, lx, 0);
+        if (MC == 8) r.x1 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, lx, 0);
+        if (MC == 16) {
+            r.x1 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, lx, 0);
+            r.x2 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 128u, lx, 0);
+            r.x3 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 144u, lx, 0);
+        }
+    };
+
+    // A wave that owns no line adds -0, the identity that keeps a -0 sum.
+    const float z = wave < nlines ? 0.0f : -0.0f;
+    f32x4 acc = f32x4{z, z, z, z};
+    auto compute = [&](const Line &r) {
+        *reinterpret_cast<u32x4 *>(tile + srow * kRows16Pitch + scol) = r.w0;
+        *reinterpret_cast<u32x4 *>(tile + (srow + 8) * kRows16Pitch + scol) = r.w1;
+        u32x4 h0, md0, lo0, h1, md1, lo1;
+        if (MC == 4) {
+            uint32_t hq[2], mq[2], lq[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                uint32_t ha, ma, la, hb, mb, lb;
+                split3(__uint_as_float(r.x0[2 * q]), ha, ma, la);
+                split3(__uint_as_float(r.x0[2 * q + 1]), hb, mb, lb);
+                hq[q] = ha | (hb << 16);
+                mq[q] = ma | (mb << 16);
+                lq[q] = la | (lb << 16);
             }
+            const int xc = xq * 8;
+            *reinterpret_cast<uint2 *>(&xt[wave][0][xm][xc]) = uint2{hq[0], hq[1]};
+            *reinterpret_cast<uint2 *>(&xt[wave][1][xm][xc]) = uint2{mq[0], mq[1]};
+            *reinterpret_cast<uint2 *>(&xt[wave][2][xm][xc]) = uint2{lq[0], lq[1]};
+        } else if (MC == 8) {
+            float xv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xv[e] = __uint_as_float(r.x0[e]);
+                xv[4 + e] = __uint_as_float(r.x1[e]);
+            }
+            u32x4 hq, mq, lq;
+            split8(xv, hq, mq, lq);
+            const int xc = xq * 16;
+            *reinterpret_cast<u32x4 *>(&xt[wave][0][xm][xc]) = hq;
+            *reinterpret_cast<u32x4 *>(&xt[wave][1][xm][xc]) = mq;
+            *reinterpret_cast<u32x4 *>(&xt[wave][2][xm][xc]) = lq;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const u32x4 a0 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + g * 16);
+        const u32x4 a1 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + 64 + g * 16);
+        if (kCompact) {
+            const int jr = i16 < MC ? i16 : MC;
+            h0 = *reinterpret_cast<const u32x4 *>(&xt[wave][0][jr][g * 16]);
+            md0 = *reinterpret_cast<const u32x4 *>(&xt[wave][1][jr][g * 16]);
+            lo0 = *reinterpret_cast<const u32x4 *>(&xt[wave][2][jr][g * 16]);
+            h1 = *reinterpret_cast<const u32x4 *>(&xt[wave][0][jr][64 + g * 16]);
+            md1 = *reinterpret_cast<const u32x4 *>(&xt[wave][1][jr][64 + g * 16]);
+            lo1 = *reinterpret_cast<const u32x4 *>(&xt[wave][2][jr][64 + g * 16]);
+        } else {
+            float xv[16];
+            const u32x4 xs[4] = {r.x0, r.x1, r.x2, r.x3};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[4 * q + e] = __uint_as_float(xs[q][e]);
+            split8(xv, h0, md0, lo0);
+            split8(xv + 8, h1, md1, lo1);
+        }
+        __builtin_amdgcn_wave_barrier();
+        uint32_t mx = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) mx = max_mag(max_mag(mx, a0[v]), a1[v]);
+        const bool any_special = wave_has_inf_nan(mx);
+        u32x4 a0m = a0, a1m = a1;
+        if (any_special) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                a0m[v] &= ~inf_nan_mask(a0m[v]);
+                a1m[v] &= ~inf_nan_mask(a1m[v]);
+            }
+        }
+        acc = mfma_bf16(a0, h0, acc);
+        acc = mfma_bf16(a0m, md0, acc);
+        acc = mfma_bf16(a0m, lo0, acc);
+        acc = mfma_bf16(a1, h1, acc);
+        acc = mfma_bf16(a1m, md1, acc);
+        acc = mfma_bf16(a1m, lo1, acc);
+    };
+
+    Line la, lb;
+    load(la, wave);
+    for (int L = wave; L < nlines; L += 16) {
+        load(lb, L + 8);
+        compute(la);
+        if (L + 8 >= nlines) break;
+        load(la, L + 16);
+        compute(lb);
+    }
+
+    // acc of lane l holds weight rows 4(l/16) + r, activation row m0 + l%16.
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        f32x4 s[1] = {red[0][lane]};
+#pragma unroll
+        for (int w = 1; w < 8; ++w) s[0] += red[w][lane];
+        const int base[1] = {0};
+        bool live[1][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) live[0][r] = i16 < mrows && g * 4 + r < nrows;
+        settle_zeros(s, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (live[0][r]) Y[(int64_t)(m0 + i16) * N + row0 + g * 4 + r] = s[0][r];
     }
 }
 
@@ -1398,13 +1582,16 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
-    // MFMA kernel for skinny M >= 2: packed rows, k a multiple of 64.  Tiles per
-    // workgroup shrink (4 -> 2 -> 1) until the grid has >= 2 workgroups per
-    // CU; 8 waves split k when it is long.
+    // MFMA kernels for skinny M >= 2: packed rows, k a multiple of 64.  The
+    // layout, by measurement on MI355X: rows16 with compact x for M <= 4 (C4
+    // 155-167 us against 170-214 for the wide layout); for larger M the wide
+    // layout where its 256-row workgroups give >= 1.5 per CU (C4), rows16
+    // elsewhere.  (A third layout, 16-row tiles with k split over the waves,
+    // measured 1.2-2.7x slower than rows16 on every shape and was removed.)
     const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 2);
     if (mfma_min_m > 0 && p.m >= mfma_min_m && p.k >= 64 && p.k % 64 == 0 && p.k <= INT32_MAX / 2 &&
         aligned(p.w, 16) && aligned(p.x, 16) && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n &&
-        (int64_t)kMfmaTiles * 16 * p.k * 2 <= INT32_MAX && (p.m + 15) / 16 <= 65535) {
+        (int64_t)16 * 4 * p.k <= INT32_MAX && (p.m + 15) / 16 <= 65535) {  // rows16: 16 x rows of f32
         RdPlan mp{};
         mp.mfma = true;
         mp.vec = 8;
@@ -1412,25 +1599,19 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.mt = 16;
         mp.kvec = 0;
         const int64_t gy = (p.m + 15) / 16;
-        // The wide layout when its 256-row workgroups still give >= 1.5 per
-        // CU; otherwise the k-split layout, whose workgroups shrink to fill
-        // the device.
         const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus &&
                                (int64_t)kWideRows * p.k * 2 <= INT32_MAX;
-        mp.mkind = env_int("DMC_HIP_RD_MFMA_KIND", wide_fits ? 6 : 1) == 1 ? 1 : 6;
-        if ((int64_t)kWideRows * p.k * 2 > INT32_MAX) mp.mkind = 1;  // 256-row buffer range
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 4 && wide_fits ? 6 : 7);
+        mp.mkind = kind == 6 && (int64_t)kWideRows * p.k * 2 <= INT32_MAX ? 6 : 7;  // 256-row buffer range
+        mp.waves = 8;
         if (mp.mkind == 6) {
-            mp.waves = 8;
             mp.rpw = kWideRows;
         } else {
-            mp.waves = env_int("DMC_HIP_RD_MFMA_WAVES", p.k >= 8192 ? 8 : 4) == 8 ? 8 : 4;
-            int tiles = env_int("DMC_HIP_RD_MFMA_TILES", kMfmaTiles);
-            if (tiles != 1 && tiles != 2 && tiles != 4) tiles = kMfmaTiles;
-            while (tiles > 1 && ((p.n + tiles * 16 - 1) / (tiles * 16)) * gy < 2 * cus) tiles >>= 1;
-            mp.rpw = tiles * 16;
+            mp.rpw = 16;
+            mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
         }
         mp.grid_x = (p.n + mp.rpw - 1) / mp.rpw;
-        mp.grid_y = (p.m + 15) / 16;
+        mp.grid_y = (p.m + mp.mt - 1) / mp.mt;
         return mp;
     }
 
@@ -1602,14 +1783,18 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
                                (int)p.m);
             return hipGetLastError();
         }
-#define DMC_RDM(NW, R)                                                                                        \
-    if (pl.waves == NW && pl.rpw == R * 16) {                                                                 \
-        hipLaunchKernelGGL((gemv_rd_mfma_kernel<NW, R>), grid, dim3(64 * NW), 0, s, p.w, p.x, p.y, (int)p.n, \
-                           (int)p.k, (int)p.m);                                                               \
-        return hipGetLastError();                                                                             \
-    }
-        DMC_RDM(4, 4) DMC_RDM(4, 2) DMC_RDM(4, 1) DMC_RDM(8, 4) DMC_RDM(8, 2) DMC_RDM(8, 1)
-#undef DMC_RDM
+        if (pl.mkind == 7) {
+            if (pl.mt == 4)
+                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<4>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
+                                   (int)p.k, (int)p.m);
+            else if (pl.mt == 8)
+                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<8>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
+                                   (int)p.k, (int)p.m);
+            else
+                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<16>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
+                                   (int)p.k, (int)p.m);
+            return hipGetLastError();
+        }
         return hipErrorInvalidValue;
     }
     if (pl.kvec > 0 && pl.vec < 8) return rd_unaligned_dispatch(p, pl, s);

@@ -56,8 +56,8 @@ struct CsProblem {
 //     `rpw` weight rows and 16 activation rows per workgroup.
 struct RdPlan {
     bool mfma;  // skinny-M MFMA kernel
-    int mkind;  // MFMA layout: 1 = the workgroup's waves split k over R 16-row tiles;
-                // 6 = 256 rows per workgroup, weights and x staged through LDS
+    int mkind;  // MFMA layout: 6 = 256 rows per workgroup, weights and x staged through LDS;
+                // 7 = 16 rows per workgroup read whole, waves own lines of each window
     int vec;    // bf16 elements per lane per weight load (8 = 128-bit loads)
     int rows;   // weight rows per step (streaming) / per workgroup (general)
     int mt;     // activation rows per workgroup (skinny-M tile)

@@ -99,8 +99,13 @@ def test_rowdot_plans_at_decode_shapes():
     # M = 1: the streaming kernel
     p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
     assert p.mt == 1 and p.slices >= 1, p
-    # M >= 2 with k % 64 == 0: an MFMA kernel (slices == -kind), 16 activation rows per tile
-    for m in (2, 3, 4, 5, 16, 17):
+    # M >= 2 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
+    # (16 weight rows per workgroup, 4 activation rows); larger M on the LM head:
+    # the wide layout, 16 activation rows per tile
+    for m in (2, 3, 4):
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
+    for m in (5, 16, 17):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
     # k not a multiple of 64: back to the streaming kernel, activation rows held in
@@ -121,14 +126,14 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
 
 
 def test_rowdot_mfma_layouts(monkeypatch):
-    # small N: the k-split layout, tiles shrinking to fill the device
-    p = d.plan("rd", 8, 4096, 16387, x_addr=256, w_addr=256)
-    assert p.slices == -1 and p.grid_x >= 512, p
-    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "1")
+    # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
+    for m, mt in [(2, 4), (4, 4), (5, 8), (8, 8), (9, 16), (16, 16), (20, 16)]:
+        p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, mt, 16, 8, 1025), (m, p)
+    # either layout can be forced
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
-    assert (p.slices, p.rows_per_group, p.grid_x) == (-1, 64, 2004), p
-    small = d.plan("rd", 16, 14336, 4096, x_addr=256, w_addr=256)
-    assert small.slices == -1 and small.waves == 8 and small.grid_x * 16 >= 4096
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-7, 16, 16, 8016), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "6")
     p = d.plan("rd", 16, 4096, 1000, x_addr=256, w_addr=256)
     assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p

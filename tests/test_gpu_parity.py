@@ -99,6 +99,25 @@ def test_denormals_survive_and_inf_times_tiny_is_inf(hip):
         assert y2[2] == np.float32(k) * W.bf16_to_f32(np.array([1], np.uint16))[0], y2
 
 
+@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("m,k", [(2, 64), (3, 320), (4, 4096), (8, 1024), (16, 64)])
+def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind, monkeypatch):
+    """As the M = 1 case above, through each MFMA layout: weight row 0's
+    products all underflow negative (reference -0.0), row 1's positive (+0.0),
+    row 2 is exact zeros against negative x (products -0.0, reference +0.0).
+    K = 64 leaves seven of rows16's eight waves without a line: they add -0.0."""
+    x = np.full((m, k), np.float32(-1e-38), np.float32)
+    w = np.zeros((3, k), np.uint16)
+    w[0, :] = 0x0001
+    w[1, :] = 0x8001
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    assert hip.plan("rd", m, k, 3, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
+    y_ref = ref(x, w)
+    assert np.all(np.signbit(y_ref[:, 0])) and not np.any(np.signbit(y_ref[:, 1:]))
+    y = run_rd(hip, x, w)
+    check(y, y_ref, what=f"mfma underflow signs m={m} k={k} kind={kind}")
+
+
 # ---- shape and tail coverage ----------------------------------------------------------
 
 SHAPES = [
@@ -563,8 +582,8 @@ def test_c3_layer_schedule(hip):
 
 # ---- skinny M on MFMA: special values through the three-term split ---------------------
 
-@pytest.mark.parametrize("kind", [1, 6])
-@pytest.mark.parametrize("m", [2, 3, 4, 8, 16, 20])
+@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 16, 20])
 def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     """The MFMA path (M >= 2) against the reference chain on data full of
     special values: bf16 subnormal weights, +-inf / NaN weights, +-0 and
@@ -594,9 +613,10 @@ def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     assert np.all(y[:, 12][np.isfinite(y_ref[:, 12])] == 0)
 
 
-@pytest.mark.parametrize("kind", [1, 6])
+@pytest.mark.parametrize("kind", [6, 7])
 @pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000),
-                                   (16, 4096, 40000), (3, 320, 300), (2, 4096, 16387), (2, 64, 70)])
+                                   (16, 4096, 40000), (3, 320, 300), (2, 4096, 16387), (2, 64, 70),
+                                   (4, 14336, 1001), (7, 576, 33), (12, 128, 17)])
 def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
     """MFMA tiles, k split over waves or chunked through LDS, partial tiles
     and chunks: every element within the rigorous forward-error bound of the
