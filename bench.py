@@ -307,6 +307,41 @@ def extended(d, W, reps: int) -> dict:
             f(0)
             record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
             s.free()
+    # C2's shapes at a few activation rows (MFMA kernels)
+    for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
+        n, k = w.shape
+        for m in (2, 4, 8):
+            x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+            s = Rotating(d, w, x, 5, n_out=n)
+            f = lambda i: d.gemv_rd(s.x, s.w[i % 5], s.y, m, k, n)  # noqa: E731
+            f(0)
+            record(f"C2 rd {name} m={m}", batch_us(d, f, 50), n, k, m)
+            s.free()
+    out.update(helpers(d, c2["up"][0]))
+    return out
+
+
+def helpers(d, w) -> dict:
+    """The device bf16 helpers on C2's up/gate weight (bytes = read + write,
+    two source and two destination regions rotated)."""
+    out = {}
+    rows, cols = w.shape
+    srcs = [d.DeviceBuffer.from_numpy(w) for _ in range(2)]
+    dsts = [d.DeviceBuffer(w.nbytes) for _ in range(2)]
+    wides = [d.DeviceBuffer(2 * w.nbytes) for _ in range(2)]
+    cases = [("transpose_2d bf16 [14336,4096]", 2 * w.nbytes,
+              lambda i: d.bf16_transpose_2d(srcs[i % 2], dsts[i % 2], rows, cols)),
+             ("bf16_upconvert 58.7M", 6 * w.size, lambda i: d.bf16_upconvert(srcs[i % 2], wides[i % 2], w.size)),
+             ("f32_to_bf16 58.7M", 6 * w.size, lambda i: d.f32_to_bf16(wides[i % 2], dsts[i % 2], w.size))]
+    for label, nbytes, f in cases:
+        for i in range(3):
+            f(i)
+        us = batch_us(d, f, 20)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
+    for b in srcs + dsts + wides:
+        b.free()
     return out
 
 

@@ -220,6 +220,22 @@ def fill_counter_bf16(dst, count: int, key: int, table, offset: int = 0) -> None
                                                      _addr(table)))
 
 
+def bf16_upconvert(src, dst, n: int) -> None:
+    """Enqueue dst f32[n] = widen(src bf16[n]) (dmc_bf16_upconvert, jit.rs:29760)."""
+    _lib.check(_lib.load().dmc_hip_bf16_upconvert(_addr(src), _addr(dst), n))
+
+
+def f32_to_bf16(src, dst, n: int) -> None:
+    """Enqueue dst bf16[n] = src f32 bits >> 16 (dmc_f32_to_bf16, jit.rs:29783)."""
+    _lib.check(_lib.load().dmc_hip_f32_to_bf16(_addr(src), _addr(dst), n))
+
+
+def bf16_transpose_2d(src, dst, m: int, n: int) -> None:
+    """Enqueue dst [n, m] = src [m, n]^T on bf16 bit patterns
+    (dmc_bf16_transpose_2d, jit.rs:29801)."""
+    _lib.check(_lib.load().dmc_hip_bf16_transpose_2d(_addr(src), _addr(dst), m, n))
+
+
 def synchronize() -> None:
     _lib.check(_lib.load().dmc_hip_synchronize())
 

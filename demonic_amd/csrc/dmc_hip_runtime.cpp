@@ -714,6 +714,43 @@ int32_t dmc_hip_fill_counter_bf16(int64_t dst_dev, int64_t count, int64_t offset
     return DMC_HIP_OK;
 }
 
+int32_t dmc_hip_bf16_upconvert(int64_t src_dev, int64_t dst_dev, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (n < 0 || (n > 0 && (!src_dev || !dst_dev))) return fail(DMC_HIP_EINVAL, "bad upconvert arguments");
+    if (n == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = dmc::launch_bf16_upconvert(reinterpret_cast<const uint16_t *>(src_dev),
+                                              reinterpret_cast<float *>(dst_dev), n, ctx().stream);
+    if (e != hipSuccess) return hip_fail(e, "upconvert launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_f32_to_bf16(int64_t src_dev, int64_t dst_dev, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (n < 0 || (n > 0 && (!src_dev || !dst_dev))) return fail(DMC_HIP_EINVAL, "bad f32-to-bf16 arguments");
+    if (n == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = dmc::launch_f32_to_bf16(reinterpret_cast<const float *>(src_dev),
+                                           reinterpret_cast<uint16_t *>(dst_dev), n, ctx().stream);
+    if (e != hipSuccess) return hip_fail(e, "f32-to-bf16 launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (m < 0 || n < 0 || (m > 0 && n > 0 && (!src_dev || !dst_dev)))
+        return fail(DMC_HIP_EINVAL, "bad transpose arguments");
+    if (m == 0 || n == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = dmc::launch_transpose_bf16(reinterpret_cast<const uint16_t *>(src_dev),
+                                              reinterpret_cast<uint16_t *>(dst_dev), m, n, ctx().stream);
+    if (e != hipSuccess) return hip_fail(e, "transpose launch");
+    return DMC_HIP_OK;
+}
+
 int32_t dmc_hip_capture_begin(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     int rc = ensure_init();

@@ -1319,6 +1319,97 @@ transpose_bf16_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ d
     }
 }
 
+// The same transpose with 16-byte accesses, for rows and cols that are
+// multiples of 8 on 16-byte-aligned bases (every weight shape of the decode
+// workloads).  A 64 x 64 tile: thread t loads source row r0 + t/8 (+32),
+// elements c0 + 8(t%8), +8; after the barrier it gathers destination row
+// c0 + t/4 (a source column), elements r0 + 16(t%4), +16, and stores them as
+// two 16-byte pieces -- four threads per 128-byte line, so a wave stores 16
+// whole lines.  Workgroups stride over the tiles.
+constexpr int kTvPitch = 72;  // halves per tile row: 144 bytes keeps 16-byte rows
+
+__global__ void __launch_bounds__(256)
+transpose_bf16_v8_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict__ dst, int64_t rows, int64_t cols,
+                         int64_t tiles_c, int64_t ntiles) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kTile][kTvPitch];
+    const int t = threadIdx.x;
+    for (int64_t tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
+        const int64_t r0 = (tl / tiles_c) * kTile, c0 = (tl % tiles_c) * kTile;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int lr = t / 8 + 32 * h, lc = 8 * (t % 8);
+            const int64_t r = r0 + lr, c = c0 + lc;
+            u32x4 v = {0, 0, 0, 0};
+            if (r < rows && c < cols) v = *reinterpret_cast<const u32x4 *>(src + r * cols + c);
+            *reinterpret_cast<u32x4 *>(&tile[lr][lc]) = v;
+        }
+        __syncthreads();
+        const int i = t / 4, jq = t % 4;
+        uint32_t o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            o[e] = (uint32_t)tile[16 * jq + 2 * e][i] | ((uint32_t)tile[16 * jq + 2 * e + 1][i] << 16);
+        const int64_t dr = c0 + i;
+        if (dr < cols) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int64_t dc = r0 + 16 * jq + 8 * h;
+                if (dc < rows)
+                    *reinterpret_cast<u32x4 *>(dst + dr * rows + dc) =
+                        u32x4{o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]};
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// dst[i] = bf16 widen of src[i] (bits << 16; NaN payloads, infinities and
+// subnormals kept), and dst[i] = src[i]'s bits >> 16 (truncation, the inverse
+// on bf16-representable values).  VEC = 8: 8 elements per thread per step
+// (16-byte-aligned bases, count a multiple of 8 in the vector part; the
+// remainder runs one element per thread).  Grid-stride.
+template <int VEC>
+__global__ void __launch_bounds__(256)
+bf16_upconvert_kernel(const uint16_t *__restrict__ src, float *__restrict__ dst, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC == 8) {
+        for (; i < n / 8; i += stride) {
+            const u32x4 v = reinterpret_cast<const u32x4 *>(src)[i];
+            u32x4 lo, hi;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                lo[2 * q] = v[q] << 16;
+                lo[2 * q + 1] = v[q] & 0xffff0000u;
+                hi[2 * q] = v[q + 2] << 16;
+                hi[2 * q + 1] = v[q + 2] & 0xffff0000u;
+            }
+            reinterpret_cast<u32x4 *>(dst)[2 * i] = lo;
+            reinterpret_cast<u32x4 *>(dst)[2 * i + 1] = hi;
+        }
+        i = (n / 8) * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    }
+    for (; i < n; i += stride) dst[i] = __uint_as_float((uint32_t)src[i] << 16);
+}
+
+template <int VEC>
+__global__ void __launch_bounds__(256)
+f32_to_bf16_kernel(const float *__restrict__ src, uint16_t *__restrict__ dst, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC == 8) {
+        for (; i < n / 8; i += stride) {
+            const u32x4 a = reinterpret_cast<const u32x4 *>(src)[2 * i];
+            const u32x4 b = reinterpret_cast<const u32x4 *>(src)[2 * i + 1];
+            reinterpret_cast<u32x4 *>(dst)[i] =
+                u32x4{(a[0] >> 16) | (a[1] & 0xffff0000u), (a[2] >> 16) | (a[3] & 0xffff0000u),
+                      (b[0] >> 16) | (b[1] & 0xffff0000u), (b[2] >> 16) | (b[3] & 0xffff0000u)};
+        }
+        i = (n / 8) * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    }
+    for (; i < n; i += stride) dst[i] = (uint16_t)(__float_as_uint(src[i]) >> 16);
+}
+
 // ---- dispatch -------------------------------------------------------------
 
 int mt_for(int64_t m) {
@@ -1872,11 +1963,45 @@ hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset
     return hipGetLastError();
 }
 
+// Workgroups for a grid-stride elementwise or tile pass: enough to fill the
+// device several times over, no more than the work.
+unsigned stride_grid(int64_t work_items) {
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, work_items));
+}
+
 hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t rows, int64_t cols, hipStream_t s) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
+    if (rows % 8 == 0 && cols % 8 == 0 && aligned(src, 16) && aligned(dst, 16)) {
+        const int64_t tiles_c = (cols + kTile - 1) / kTile;
+        const int64_t ntiles = tiles_c * ((rows + kTile - 1) / kTile);
+        hipLaunchKernelGGL(transpose_bf16_v8_kernel, dim3(stride_grid(ntiles)), dim3(256), 0, s, src, dst, rows, cols,
+                           tiles_c, ntiles);
+        return hipGetLastError();
+    }
     const unsigned gx = (unsigned)std::min<int64_t>(65535, (cols + kTile - 1) / kTile);
     const unsigned gy = (unsigned)std::min<int64_t>(65535, (rows + kTile - 1) / kTile);
     hipLaunchKernelGGL(transpose_bf16_kernel, dim3(gx, gy), dim3(kThreads), 0, s, src, dst, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t launch_bf16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (aligned(src, 16) && aligned(dst, 16))
+        hipLaunchKernelGGL(bf16_upconvert_kernel<8>, dim3(stride_grid((n / 8 + 255) / 256)), dim3(256), 0, s, src,
+                           dst, n);
+    else
+        hipLaunchKernelGGL(bf16_upconvert_kernel<1>, dim3(stride_grid((n + 255) / 256)), dim3(256), 0, s, src, dst,
+                           n);
+    return hipGetLastError();
+}
+
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    if (aligned(src, 16) && aligned(dst, 16))
+        hipLaunchKernelGGL(f32_to_bf16_kernel<8>, dim3(stride_grid((n / 8 + 255) / 256)), dim3(256), 0, s, src, dst,
+                           n);
+    else
+        hipLaunchKernelGGL(f32_to_bf16_kernel<1>, dim3(stride_grid((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
     return hipGetLastError();
 }
 

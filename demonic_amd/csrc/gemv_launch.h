@@ -120,8 +120,12 @@ size_t probe_sink_bytes();
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
 
 // dst [cols, rows] = src [rows, cols]^T for bf16 bit patterns (weight
-// residency in the row-dot layout).
+// residency in the row-dot layout, dmc_hip_bf16_transpose_2d).
 hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t rows, int64_t cols, hipStream_t stream);
+
+// dst[i] = widen(src[i]) (bits << 16), and dst[i] = bits(src[i]) >> 16.
+hipError_t launch_bf16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t stream);
+hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);
 
 // Synthetic weights for measurements: dst[i] = table[h(offset + i) >> 48],
 // h(j) = splitmix64(j ^ key), table = 65,536 bf16 bit patterns.

@@ -142,7 +142,8 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
  * Row-dot layout: `vec` is the weight rows' alignment in bf16 elements (8 =
  * 16 bytes); `slices` > 0 is a streaming plan with that many 8-element k
  * windows per lane (with vec < 8, the variant that reads misaligned rows with
- * unaligned 128-bit loads), 0 the general kernel, -1 / -6 the MFMA layouts; waves and
+ * unaligned 128-bit loads), 0 the general kernel, -6 / -7 the MFMA layouts (256 rows
+ * per workgroup / 16 rows per workgroup, mt activation rows); waves and
  * rows_per_group (weight rows per workgroup) describe the workgroup. */
 int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k,
                      int64_t n, int64_t batch, int64_t rs, int64_t *out8);
@@ -163,6 +164,21 @@ int32_t dmc_hip_probe_read(int64_t src_dev, int64_t bytes);
  * host in reasonable time).  No reference counterpart. */
 int32_t dmc_hip_fill_counter_bf16(int64_t dst_dev, int64_t count, int64_t offset, uint64_t key,
                                   int64_t table_dev);
+
+/* Device forms of the reference's bf16 helpers, on device pointers, ordered
+ * on the library stream.  Results are bit-exact:
+ *   dmc_hip_bf16_upconvert: dst f32[n] = widen(src bf16[n]), bits << 16
+ *     (replaces dmc_bf16_upconvert, jit.rs:29760);
+ *   dmc_hip_f32_to_bf16: dst bf16[n] = src f32 bits >> 16, truncation
+ *     (replaces dmc_f32_to_bf16, jit.rs:29783);
+ *   dmc_hip_bf16_transpose_2d: dst [n, m] = src [m, n]^T, bit patterns moved
+ *     unchanged (replaces dmc_bf16_transpose_2d, jit.rs:29801).
+ * The reference allocates and returns the result; here the caller passes it
+ * (for instance a region from dmc_hip_region_alloc), and the ranges must not
+ * overlap.  n == 0 (or m == 0) does nothing. */
+int32_t dmc_hip_bf16_upconvert(int64_t src_dev, int64_t dst_dev, int64_t n);
+int32_t dmc_hip_f32_to_bf16(int64_t src_dev, int64_t dst_dev, int64_t n);
+int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, int64_t n);
 
 /* HIP graphs of the library stream.  Between capture_begin and capture_end,
  * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
