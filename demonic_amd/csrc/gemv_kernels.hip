@@ -747,36 +747,47 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 // lines past the last load from outside the buffers.
 constexpr int kRows16Pitch = 144;
 
-template <int MC>
+template <int MC, int T>
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
                            int N, int K, int M) {
     static_assert(MC == 4 || MC == 8 || MC == 16, "activation rows per workgroup");
+    static_assert(T == 1 || T == 2 || T == 4, "16-row blocks per workgroup");
     constexpr bool kCompact = MC < 16;
     constexpr int kLanesPerRow = 64 / MC;  // compact x: lanes per activation row
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int i16 = lane & 15;
     const int g = lane >> 4;
-    const int row0 = blockIdx.x * 16;
-    const int nrows = min(16, N - row0);
     const int m0 = blockIdx.y * MC;
     const int mrows = min(MC, M - m0);
     const int nlines = K >> 6;
 
-    __shared__ __attribute__((aligned(16))) uint8_t wt[8][16 * kRows16Pitch];  // 8 x 2.25 KiB
-    // MC = 4, 8: per wave, three planes of MC x rows (64 bf16 each) and a zero row.
-    constexpr int kXRows = kCompact ? MC + 1 : 1;
-    __shared__ __attribute__((aligned(16))) uint8_t xt[8][3][kXRows][kRows16Pitch];
-    __shared__ f32x4 red[8][64];                                                 // 8 KiB
-    uint8_t *const tile = wt[wave];
+    // LDS: the waves' weight tiles and x planes while streaming, then the
+    // partial sums (T x 8 KiB) in the same bytes.
+    constexpr int kXRows = kCompact ? MC + 1 : 1;  // MC x rows and a zero row
+    constexpr int kTileBytes = 16 * kRows16Pitch;
+    constexpr int kXBytes = kCompact ? 3 * kXRows * kRows16Pitch : 0;
+    constexpr int kStreamBytes = 8 * (kTileBytes + kXBytes);
+    constexpr int kRedBytes = 8 * T * 64 * 16;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kStreamBytes > kRedBytes ? kStreamBytes : kRedBytes];
+    uint8_t *const tile = lds + wave * kTileBytes;
+    uint8_t *const xt = lds + 8 * kTileBytes + wave * kXBytes;  // [3][kXRows][pitch]
+    f32x4 *const red = reinterpret_cast<f32x4 *>(lds);         // [8][T][64]
 
-    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
+    // Block t of this workgroup: weight rows 16 (blockIdx.x + t gridDim.x) + 0..15.
+    __amdgpu_buffer_rsrc_t rs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int r0 = min(N, (int)(blockIdx.x + t * gridDim.x) * 16);
+        rs[t] = weight_rsrc(W + (int64_t)r0 * K, (uint32_t)((int64_t)min(16, N - r0) * K * 2));
+    }
     const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m0 * K, (uint32_t)((int64_t)mrows * K * 4));
-    // Whole-line staging: load j (0, 1) covers rows 8j + lane/8, bytes 16*(lane%8) of the line.
+    // Whole-line staging: load j (0, 1) covers rows 8j + lane/8, bytes 16*(lane%8) of the line; rows
+    // past a block's end lie outside its buffer resource and read zeros.
     const int srow = lane >> 3, scol = (lane & 7) * 16;
-    const uint32_t woff0 = srow < nrows ? (uint32_t)srow * (uint32_t)K * 2u + scol : kOutOfRange;
-    const uint32_t woff1 = srow + 8 < nrows ? (uint32_t)(srow + 8) * (uint32_t)K * 2u + scol : kOutOfRange;
+    const uint32_t woff0 = (uint32_t)srow * (uint32_t)K * 2u + scol;
+    const uint32_t woff1 = (uint32_t)(srow + 8) * (uint32_t)K * 2u + scol;
     // x offsets.  MC = 16: lane (j, g) takes x[m0 + j][64L + 32b + 8g, +8) for k-block b.
     // MC = 4, 8: lane l takes x[m0 + l/(64/MC)][64L + MC(l%(64/MC)), +MC).
     const int xm = kCompact ? lane / kLanesPerRow : i16;
@@ -787,19 +798,22 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
 #pragma unroll
         for (int p = 0; p < 3; ++p)
             if (lane < kRows16Pitch / 16)
-                *reinterpret_cast<u32x4 *>(&xt[wave][p][MC][lane * 16]) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<u32x4 *>(xt + (p * kXRows + MC) * kRows16Pitch + lane * 16) = u32x4{0, 0, 0, 0};
     }
 
     struct Line {
-        u32x4 w0, w1;          // weight rows srow, srow + 8
+        u32x4 w0[T], w1[T];    // weight rows srow, srow + 8 of each block
         u32x4 x0, x1, x2, x3;  // MC = 16: x for k-block 0 (x0, x1) and 1 (x2, x3); MC = 4: x0; MC = 8: x0, x1
     };
     // Line L's loads; lines past the end read zeros from outside the buffers.
     auto load = [&](Line &r, int L) {
         const bool live = L < nlines;
         const uint32_t lw = (uint32_t)L * 128u, lx = (uint32_t)L * 256u;
-        r.w0 = load_w16(rs, live ? woff0 : kOutOfRange, lw);
-        r.w1 = load_w16(rs, live ? woff1 : kOutOfRange, lw);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            r.w0[t] = load_w16(rs[t], live ? woff0 : kOutOfRange, lw);
+            r.w1[t] = load_w16(rs[t], live ? woff1 : kOutOfRange, lw);
+        }
         const uint32_t xo = live ? xoff : kOutOfRange;
         r.x0 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, lx, 0);
         if (MC == 8) r.x1 = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, lx, 0);
@@ -812,10 +826,11 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
 
     // A wave that owns no line adds -0, the identity that keeps a -0 sum.
     const float z = wave < nlines ? 0.0f : -0.0f;
-    f32x4 acc = f32x4{z, z, z, z};
+    f32x4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{z, z, z, z};
     auto compute = [&](const Line &r) {
-        *reinterpret_cast<u32x4 *>(tile + srow * kRows16Pitch + scol) = r.w0;
-        *reinterpret_cast<u32x4 *>(tile + (srow + 8) * kRows16Pitch + scol) = r.w1;
+        // x: the three bf16 terms in the B operand layout.
         u32x4 h0, md0, lo0, h1, md1, lo1;
         if (MC == 4) {
             uint32_t hq[2], mq[2], lq[2];
@@ -828,10 +843,10 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
                 mq[q] = ma | (mb << 16);
                 lq[q] = la | (lb << 16);
             }
-            const int xc = xq * 8;
-            *reinterpret_cast<uint2 *>(&xt[wave][0][xm][xc]) = uint2{hq[0], hq[1]};
-            *reinterpret_cast<uint2 *>(&xt[wave][1][xm][xc]) = uint2{mq[0], mq[1]};
-            *reinterpret_cast<uint2 *>(&xt[wave][2][xm][xc]) = uint2{lq[0], lq[1]};
+            uint8_t *const xr = xt + xm * kRows16Pitch + xq * 8;
+            *reinterpret_cast<uint2 *>(xr) = uint2{hq[0], hq[1]};
+            *reinterpret_cast<uint2 *>(xr + kXRows * kRows16Pitch) = uint2{mq[0], mq[1]};
+            *reinterpret_cast<uint2 *>(xr + 2 * kXRows * kRows16Pitch) = uint2{lq[0], lq[1]};
         } else if (MC == 8) {
             float xv[8];
 #pragma unroll
@@ -841,22 +856,20 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             }
             u32x4 hq, mq, lq;
             split8(xv, hq, mq, lq);
-            const int xc = xq * 16;
-            *reinterpret_cast<u32x4 *>(&xt[wave][0][xm][xc]) = hq;
-            *reinterpret_cast<u32x4 *>(&xt[wave][1][xm][xc]) = mq;
-            *reinterpret_cast<u32x4 *>(&xt[wave][2][xm][xc]) = lq;
+            uint8_t *const xr = xt + xm * kRows16Pitch + xq * 16;
+            *reinterpret_cast<u32x4 *>(xr) = hq;
+            *reinterpret_cast<u32x4 *>(xr + kXRows * kRows16Pitch) = mq;
+            *reinterpret_cast<u32x4 *>(xr + 2 * kXRows * kRows16Pitch) = lq;
         }
-        __builtin_amdgcn_wave_barrier();
-        const u32x4 a0 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + g * 16);
-        const u32x4 a1 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + 64 + g * 16);
         if (kCompact) {
-            const int jr = i16 < MC ? i16 : MC;
-            h0 = *reinterpret_cast<const u32x4 *>(&xt[wave][0][jr][g * 16]);
-            md0 = *reinterpret_cast<const u32x4 *>(&xt[wave][1][jr][g * 16]);
-            lo0 = *reinterpret_cast<const u32x4 *>(&xt[wave][2][jr][g * 16]);
-            h1 = *reinterpret_cast<const u32x4 *>(&xt[wave][0][jr][64 + g * 16]);
-            md1 = *reinterpret_cast<const u32x4 *>(&xt[wave][1][jr][64 + g * 16]);
-            lo1 = *reinterpret_cast<const u32x4 *>(&xt[wave][2][jr][64 + g * 16]);
+            __builtin_amdgcn_wave_barrier();
+            const uint8_t *const xr = xt + (i16 < MC ? i16 : MC) * kRows16Pitch + g * 16;
+            h0 = *reinterpret_cast<const u32x4 *>(xr);
+            md0 = *reinterpret_cast<const u32x4 *>(xr + kXRows * kRows16Pitch);
+            lo0 = *reinterpret_cast<const u32x4 *>(xr + 2 * kXRows * kRows16Pitch);
+            h1 = *reinterpret_cast<const u32x4 *>(xr + 64);
+            md1 = *reinterpret_cast<const u32x4 *>(xr + kXRows * kRows16Pitch + 64);
+            lo1 = *reinterpret_cast<const u32x4 *>(xr + 2 * kXRows * kRows16Pitch + 64);
         } else {
             float xv[16];
             const u32x4 xs[4] = {r.x0, r.x1, r.x2, r.x3};
@@ -867,25 +880,35 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             split8(xv, h0, md0, lo0);
             split8(xv + 8, h1, md1, lo1);
         }
-        __builtin_amdgcn_wave_barrier();
-        uint32_t mx = 0;
+        // Weights: each block through the wave's tile in turn.
 #pragma unroll
-        for (int v = 0; v < 4; ++v) mx = max_mag(max_mag(mx, a0[v]), a1[v]);
-        const bool any_special = wave_has_inf_nan(mx);
-        u32x4 a0m = a0, a1m = a1;
-        if (any_special) {
+        for (int t = 0; t < T; ++t) {
+            __builtin_amdgcn_wave_barrier();
+            *reinterpret_cast<u32x4 *>(tile + srow * kRows16Pitch + scol) = r.w0[t];
+            *reinterpret_cast<u32x4 *>(tile + (srow + 8) * kRows16Pitch + scol) = r.w1[t];
+            __builtin_amdgcn_wave_barrier();
+            const u32x4 a0 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + g * 16);
+            const u32x4 a1 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + 64 + g * 16);
+            uint32_t mx = 0;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                a0m[v] &= ~inf_nan_mask(a0m[v]);
-                a1m[v] &= ~inf_nan_mask(a1m[v]);
+            for (int v = 0; v < 4; ++v) mx = max_mag(max_mag(mx, a0[v]), a1[v]);
+            const bool any_special = wave_has_inf_nan(mx);
+            u32x4 a0m = a0, a1m = a1;
+            if (any_special) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    a0m[v] &= ~inf_nan_mask(a0m[v]);
+                    a1m[v] &= ~inf_nan_mask(a1m[v]);
+                }
             }
+            acc[t] = mfma_bf16(a0, h0, acc[t]);
+            acc[t] = mfma_bf16(a0m, md0, acc[t]);
+            acc[t] = mfma_bf16(a0m, lo0, acc[t]);
+            acc[t] = mfma_bf16(a1, h1, acc[t]);
+            acc[t] = mfma_bf16(a1m, md1, acc[t]);
+            acc[t] = mfma_bf16(a1m, lo1, acc[t]);
         }
-        acc = mfma_bf16(a0, h0, acc);
-        acc = mfma_bf16(a0m, md0, acc);
-        acc = mfma_bf16(a0m, lo0, acc);
-        acc = mfma_bf16(a1, h1, acc);
-        acc = mfma_bf16(a1m, md1, acc);
-        acc = mfma_bf16(a1m, lo1, acc);
+        __builtin_amdgcn_wave_barrier();
     };
 
     Line la, lb;
@@ -898,21 +921,28 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
         compute(lb);
     }
 
-    // acc of lane l holds weight rows 4(l/16) + r, activation row m0 + l%16.
-    red[wave][lane] = acc;
+    // acc[t] of lane l holds weight rows 4(l/16) + r of block t, activation row m0 + l%16.
+    __syncthreads();  // every wave is done with its tile and x planes
+#pragma unroll
+    for (int t = 0; t < T; ++t) red[(wave * T + t) * 64 + lane] = acc[t];
     __syncthreads();
-    if (wave == 0) {
-        f32x4 s[1] = {red[0][lane]};
+    if (wave < T) {
+        const int t = wave;
+        const int row0 = (int)(blockIdx.x + t * gridDim.x) * 16;
+        if (row0 < N) {
+            const int nrows = min(16, N - row0);
+            f32x4 s[1] = {red[t * 64 + lane]};
 #pragma unroll
-        for (int w = 1; w < 8; ++w) s[0] += red[w][lane];
-        const int base[1] = {0};
-        bool live[1][4];
+            for (int w = 1; w < 8; ++w) s[0] += red[(w * T + t) * 64 + lane];
+            const int base[1] = {0};
+            bool live[1][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) live[0][r] = i16 < mrows && g * 4 + r < nrows;
-        settle_zeros(s, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
+            for (int r = 0; r < 4; ++r) live[0][r] = i16 < mrows && g * 4 + r < nrows;
+            settle_zeros(s, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            if (live[0][r]) Y[(int64_t)(m0 + i16) * N + row0 + g * 4 + r] = s[0][r];
+            for (int r = 0; r < 4; ++r)
+                if (live[0][r]) Y[(int64_t)(m0 + i16) * N + row0 + g * 4 + r] = s[0][r];
+        }
     }
 }
 
@@ -1674,10 +1704,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
     // MFMA kernels for skinny M >= 2: packed rows, k a multiple of 64.  The
-    // layout, by measurement on MI355X: rows16 with compact x for M <= 4 (C4
-    // 155-167 us against 170-214 for the wide layout); for larger M the wide
-    // layout where its 256-row workgroups give >= 1.5 per CU (C4), rows16
-    // elsewhere.  (A third layout, 16-row tiles with k split over the waves,
+    // layout, by measurement on MI355X: rows16 with compact x for M <= 8 (C4
+    // m = 2..4: 155-167 us against 170-214 for the wide layout; m = 8: 165
+    // against 174); for larger M the wide layout where its 256-row workgroups
+    // give >= 1.5 per CU (C4), rows16 elsewhere.  (A third layout, 16-row tiles with k split over the waves,
     // measured 1.2-2.7x slower than rows16 on every shape and was removed.)
     const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 2);
     if (mfma_min_m > 0 && p.m >= mfma_min_m && p.k >= 64 && p.k % 64 == 0 && p.k <= INT32_MAX / 2 &&
@@ -1692,14 +1722,24 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         const int64_t gy = (p.m + 15) / 16;
         const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus &&
                                (int64_t)kWideRows * p.k * 2 <= INT32_MAX;
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 4 && wide_fits ? 6 : 7);
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 8 && wide_fits ? 6 : 7);
         mp.mkind = kind == 6 && (int64_t)kWideRows * p.k * 2 <= INT32_MAX ? 6 : 7;  // 256-row buffer range
         mp.waves = 8;
         if (mp.mkind == 6) {
             mp.rpw = kWideRows;
         } else {
-            mp.rpw = 16;
+            // rows16: T 16-row blocks per workgroup, gridDim.x apart, while
+            // the grid keeps >= 2 workgroups per CU.  Two blocks share each x
+            // split at MC = 8 (C4 m = 8: 165 us against 195 with one block
+            // and 174 on the wide layout); at MC = 4 the split is cheap enough
+            // (equal times), at MC = 16 the registers of more blocks cost
+            // occupancy (205-217 us against 174 on the wide layout).
             mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
+            int tiles = env_int("DMC_HIP_RD_R16_TILES", mp.mt == 8 ? 2 : 1);
+            if (tiles != 1 && tiles != 2 && tiles != 4) tiles = 1;
+            const int64_t blocks16 = (p.n + 15) / 16;
+            while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < 2 * cus) tiles >>= 1;
+            mp.rpw = 16 * tiles;
         }
         mp.grid_x = (p.n + mp.rpw - 1) / mp.rpw;
         mp.grid_y = (p.m + mp.mt - 1) / mp.mt;
@@ -1875,16 +1915,17 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
             return hipGetLastError();
         }
         if (pl.mkind == 7) {
-            if (pl.mt == 4)
-                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<4>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
-                                   (int)p.k, (int)p.m);
-            else if (pl.mt == 8)
-                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<8>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
-                                   (int)p.k, (int)p.m);
-            else
-                hipLaunchKernelGGL(gemv_rd_mfma_rows16_kernel<16>, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n,
-                                   (int)p.k, (int)p.m);
-            return hipGetLastError();
+            const int tiles = pl.rpw / 16;
+#define DMC_R16(MC, T)                                                                                      \
+    if (pl.mt == MC && tiles == T) {                                                                        \
+        hipLaunchKernelGGL((gemv_rd_mfma_rows16_kernel<MC, T>), grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n, \
+                           (int)p.k, (int)p.m);                                                             \
+        return hipGetLastError();                                                                           \
+    }
+            DMC_R16(4, 1) DMC_R16(4, 2) DMC_R16(4, 4) DMC_R16(8, 1) DMC_R16(8, 2) DMC_R16(8, 4)
+            DMC_R16(16, 1) DMC_R16(16, 2) DMC_R16(16, 4)
+#undef DMC_R16
+            return hipErrorInvalidValue;
         }
         return hipErrorInvalidValue;
     }

@@ -105,7 +105,10 @@ def test_rowdot_plans_at_decode_shapes():
     for m in (2, 3, 4):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
-    for m in (5, 16, 17):
+    for m in (5, 8):  # two 16-row blocks per workgroup
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
+    for m in (9, 16, 17):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
     # k not a multiple of 64: back to the streaming kernel, activation rows held in
@@ -127,9 +130,19 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
 
 def test_rowdot_mfma_layouts(monkeypatch):
     # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
-    for m, mt in [(2, 4), (4, 4), (5, 8), (8, 8), (9, 16), (16, 16), (20, 16)]:
+    for m, mt, rpw in [(2, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32), (9, 16, 16), (16, 16, 16), (20, 16, 16)]:
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, mt, 16, 8, 1025), (m, p)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
+            (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
+    # blocks per workgroup shrink while the grid would fall under 2 per CU
+    p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
+    assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
+    monkeypatch.setenv("DMC_HIP_RD_R16_TILES", "4")
+    p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
+    assert p.slices == -6, p  # tiles only shape the rows16 layout
+    p = d.plan("rd", 4, 4096, 128256, x_addr=256, w_addr=256)
+    assert (p.slices, p.rows_per_group, p.grid_x) == (-7, 64, 2004), p
+    monkeypatch.delenv("DMC_HIP_RD_R16_TILES")
     # either layout can be forced
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)

@@ -118,6 +118,29 @@ def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind,
     check(y, y_ref, what=f"mfma underflow signs m={m} k={k} kind={kind}")
 
 
+@pytest.mark.parametrize("tiles", [2, 4])
+@pytest.mark.parametrize("m", [2, 5, 8, 16])
+def test_rows16_blocks_per_workgroup(hip, m, tiles, monkeypatch):
+    """rows16 with 2 or 4 16-row blocks per workgroup, gridDim.x blocks apart:
+    N = 40003 leaves a 3-row block and, at 4 blocks, three empty ones.  Edge
+    data (subnormals, +-0, +-1e-38, inf/NaN weights), an all-zero weight row,
+    rows sampled from every block position and the last rows."""
+    k, n = 1024, 40003
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
+    monkeypatch.setenv("DMC_HIP_RD_R16_TILES", str(tiles))
+    x, w = case(m, k, n, seed=77 + m * 5 + tiles, edge=True)
+    w[n - 2, :] = 0
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert (p.slices, p.rows_per_group) == (-7, 16 * tiles), p
+    y = run_rd(hip, x, w)
+    rng = np.random.default_rng(m)
+    rows = np.unique(np.r_[np.arange(n - 40, n), np.arange(0, 48), rng.integers(0, n, 400),
+                           np.array([16 * p.grid_x, 16 * p.grid_x + 15, 32 * p.grid_x - 1]) % n])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    check(y[:, rows], y_ref, what=f"rows16 m={m} tiles={tiles}")
+    assert np.all(y[:, n - 2][np.isfinite(y_ref[:, list(rows).index(n - 2)])] == 0)
+
+
 # ---- shape and tail coverage ----------------------------------------------------------
 
 SHAPES = [
