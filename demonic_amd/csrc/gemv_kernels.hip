@@ -1137,9 +1137,19 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
 // (Finishing inside the same launch needs device-scope fences, which on a
 // multi-XCD part write back and invalidate the whole L2 per workgroup:
 // measured 5x slower than the second launch.)
+//
+// UN: rows at any 2-byte alignment (odd N, offset views).  Buffer loads take
+// 2-byte-aligned offsets exactly, and the hardware range check is per dword
+// of the load: a dword that runs past the range's end comes back as zeros.
+// A row's last chunk runs into the next row, which is in range except after
+// the workgroup's last row; there the range extends 2 bytes, so the dword
+// holding element N-1 is whole.  Those 2 bytes belong to the next row, which
+// exists because the matrix's last row is left out: the slice pass applies it
+// as the chain's final fma (sum_slices_stream_kernel).  Columns past N read
+// the next row's first elements and are never stored.
 constexpr int kCsCols = 512;
 
-template <int NW, int MT>
+template <int NW, int MT, bool UN>
 __global__ void __launch_bounds__(64 * NW)
 gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restrict__ X, int64_t ls,
                       float *__restrict__ Y, float *__restrict__ P, int64_t z_stride, int64_t p_slice, int N,
@@ -1153,16 +1163,18 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     const bool live = col < N;
 
     const int kb = s * kslice;
-    const int ke = min(K, kb + kslice);
+    const int ke = min(UN ? K - 1 : K, kb + kslice);
     const int per = (ke - kb + NW - 1) / NW;
     const int r0 = min(ke, kb + wave * per);
     const int r1 = min(ke, r0 + per);
 
     const float *xz = X + z * ls;
-    const __amdgpu_buffer_rsrc_t rsw =
-        weight_rsrc(W + z * rs + (int64_t)r0 * N, (uint32_t)((int64_t)(r1 - r0) * N * 2));
+    const uint16_t *const w0 = W + z * rs + (int64_t)r0 * N;
+    const uint32_t delta = UN ? (uint32_t)(reinterpret_cast<uintptr_t>(w0) & 3) : 0;  // 0 or 2
+    const uint32_t range = (uint32_t)((int64_t)(r1 - r0) * N * 2) + (UN ? (delta + 2 + 3) & ~3u : 0);
+    const __amdgpu_buffer_rsrc_t rsw = weight_rsrc(reinterpret_cast<const char *>(w0) - delta, range);
     const uint32_t row_bytes = (uint32_t)N * 2;
-    const uint32_t lane_off = (uint32_t)col * 2;
+    const uint32_t lane_off = delta + (uint32_t)col * 2;
 
     // +0.0f when this lane sums at least one product (or K == 0, which must
     // write +0.0f), -0.0f, the additive identity, otherwise.
@@ -1226,7 +1238,7 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
 
     const int c0 = cb * kCsCols;
     const int ncol = min(kCsCols, N - c0);
-    float *out = slices == 1 ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
+    float *out = slices == 1 && !UN ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
     for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {
         const int m = t / kCsCols, c = t - m * kCsCols;
         if (m >= M || c >= ncol) continue;
@@ -1241,9 +1253,18 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
 // of P[j][i] in ascending j.  A workgroup owns 64 consecutive outputs; its 4
 // waves take slices j = w, w+4, ... (coalesced 256-byte reads), and the four
 // partial sums meet in LDS in wave order.  Every element's order is fixed.
+//
+// With `last` set (the UN streaming kernel left out the matrix's last row):
+// y[i] = fmaf(x[z][m][K-1], w[z][K-1][n], that sum), the chain's final step.
+struct LastRow {
+    const uint16_t *w;  // slice z's row K-1: w + z*rs
+    const float *x;     // x[z][m][K-1]: x + z*ls + m*K
+    int64_t rs, ls, K, N, M;
+};
+
 __global__ void __launch_bounds__(256)
 sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
-                         int64_t count) {
+                         int64_t count, const LastRow last) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
@@ -1260,7 +1281,16 @@ sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slice
     __shared__ float part[4][64];
     part[wave][lane] = s;
     __syncthreads();
-    if (wave == 0 && i < count) Y[i] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+    if (wave == 0 && i < count) {
+        float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
+        if (last.w) {
+            const int64_t z = i / (last.M * last.N), r = i - z * last.M * last.N;
+            const int64_t m = r / last.N, n = r - m * last.N;
+            const float xv = last.x[z * last.ls + m * last.K];
+            v = fmaf(xv, __uint_as_float((uint32_t)last.w[z * last.rs + n] << 16), v);
+        }
+        Y[i] = v;
+    }
 }
 
 // Second CS pass: y[i] = sum over slices in ascending order of P[s][i].
@@ -1611,10 +1641,16 @@ template <int NW, int MT>
 hipError_t css_go(const CsProblem &p, const CsPlan &pl, float *P, int64_t z0, int64_t nz, int64_t m0,
                   int64_t mc, hipStream_t s) {
     const int64_t zs = p.m * p.n;
-    hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.slices, (unsigned)nz),
-                       dim3(64 * NW), 0, s, p.w + z0 * p.rs, p.rs, p.x + z0 * p.ls + m0 * p.k, p.ls,
-                       p.y + z0 * zs + m0 * p.n, P ? P + z0 * zs + m0 * p.n : nullptr, zs, p.batch * zs,
-                       (int)p.n, (int)p.k, (int)mc, (int)pl.kslice, (int)pl.slices);
+    const dim3 grid((unsigned)pl.grid_x, (unsigned)pl.slices, (unsigned)nz);
+    if (pl.unaligned)
+        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, true>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs, p.rs,
+                           p.x + z0 * p.ls + m0 * p.k, p.ls, p.y + z0 * zs + m0 * p.n, P + z0 * zs + m0 * p.n, zs,
+                           p.batch * zs, (int)p.n, (int)p.k, (int)mc, (int)pl.kslice, (int)pl.slices);
+    else
+        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, false>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs,
+                           p.rs, p.x + z0 * p.ls + m0 * p.k, p.ls, p.y + z0 * zs + m0 * p.n,
+                           P ? P + z0 * zs + m0 * p.n : nullptr, zs, p.batch * zs, (int)p.n, (int)p.k, (int)mc,
+                           (int)pl.kslice, (int)pl.slices);
     return hipGetLastError();
 }
 
@@ -1824,13 +1860,16 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
     const int64_t batch = std::max<int64_t>(p.batch, 1);
     const int64_t kmax = std::max<int64_t>(p.k, 1);
 
-    // Streaming kernel: 128-bit column vectors.
-    if (pl.vec == 8 && env_int("DMC_HIP_CS_STREAM", 1) != 0) {
+    // Streaming kernel: 128-bit column vectors; rows at any 2-byte alignment
+    // (UN: the matrix's last row goes to the slice pass) from N = 8 and K = 2.
+    const bool un = pl.vec < 8 && p.n >= 8 && p.k >= 2 && env_int("DMC_HIP_CS_UNALIGNED", 1) != 0;
+    if ((pl.vec == 8 || un) && env_int("DMC_HIP_CS_STREAM", 1) != 0) {
         int nw = env_int("DMC_HIP_CS_WAVES", 4);
         if (nw != 2 && nw != 4 && nw != 8) nw = 4;
         pl.stream = true;
+        pl.unaligned = un;
         pl.waves = nw;
-        pl.rw = 1;
+        pl.rw = 0;
         pl.mt = std::min(mt_for(p.m), 4);
         pl.cb = kCsCols;
         pl.grid_x = (p.n + kCsCols - 1) / kCsCols;
@@ -1839,21 +1878,23 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         const int64_t groups = pl.grid_x * std::min<int64_t>(batch, 32768) * ((p.m + pl.mt - 1) / pl.mt);
         const int64_t target = (int64_t)env_int("DMC_HIP_CS_GROUPS_PER_CU", 4) * cus;
         const int64_t want = std::max<int64_t>(1, (target + groups - 1) / groups);
-        int64_t kslice = (kmax + want - 1) / want;
+        const int64_t krows = un ? kmax - 1 : kmax;  // rows the streaming kernel covers
+        int64_t kslice = (krows + want - 1) / want;
         kslice = std::max<int64_t>(kslice, 8 * nw);
         kslice = (kslice + nw - 1) / nw * nw;
         kslice = std::max<int64_t>(nw, env_int("DMC_HIP_CS_KSLICE", (int)std::min<int64_t>(kslice, INT32_MAX)));
         pl.kslice = kslice;
-        pl.slices = (kmax + kslice - 1) / kslice;
+        pl.slices = (krows + kslice - 1) / kslice;
         // A wave's rows, plus the 16 rows its last loads run past them, must
         // fit a 31-bit buffer offset; the grid's y extent is limited to 65535.
         const int64_t per_wave = (kslice + nw - 1) / nw;
         if (pl.slices <= 65535 && (per_wave + 16) * p.n * 2 <= INT32_MAX) {
-            pl.workspace_bytes = pl.slices > 1 ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
+            pl.workspace_bytes = pl.slices > 1 || un ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
             return pl;
         }
+        const int vec = pl.vec;
         pl = CsPlan{};
-        pl.vec = 8;
+        pl.vec = vec;
     }
 
     // General kernel with a second summation pass.
@@ -1954,7 +1995,7 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
     if (p.m <= 0 || p.n <= 0 || p.batch <= 0) return hipSuccess;
     const int64_t zmax_s = 32768;  // grid.z limit, with margin
     if (pl.stream) {
-        float *P = pl.slices > 1 ? static_cast<float *>(workspace) : nullptr;
+        float *P = pl.slices > 1 || pl.unaligned ? static_cast<float *>(workspace) : nullptr;
         for (int64_t z0 = 0; z0 < p.batch; z0 += zmax_s) {
             const int64_t nz = std::min(zmax_s, p.batch - z0);
             for (int64_t m0 = 0; m0 < p.m; m0 += pl.mt) {
@@ -1963,10 +2004,12 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
                 if (e != hipSuccess) return e;
             }
         }
-        if (pl.slices > 1) {
+        if (pl.slices > 1 || pl.unaligned) {
             const int64_t total = p.m * p.n * p.batch;
+            LastRow last{};
+            if (pl.unaligned) last = LastRow{p.w + (p.k - 1) * p.n, p.x + (p.k - 1), p.rs, p.ls, p.k, p.n, p.m};
             hipLaunchKernelGGL(sum_slices_stream_kernel, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, s, P,
-                               total, (int)pl.slices, p.y, total);
+                               total, (int)pl.slices, p.y, total, last);
             return hipGetLastError();
         }
         return hipSuccess;

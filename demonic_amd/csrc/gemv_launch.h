@@ -68,8 +68,10 @@ struct RdPlan {
 };
 
 // Two column-stream kernels:
-//   streaming (vec == 8): lanes own 8 columns, a workgroup owns 512 columns
-//     and a k slice, `waves` waves split the slice;
+//   streaming (rw == 0): lanes own 8 columns, a workgroup owns 512 columns
+//     and a k slice, `waves` waves split the slice; with `unaligned` (vec < 8:
+//     rows at any 2-byte alignment, N >= 8, K >= 2) the slice pass also
+//     applies the last k row;
 //   general (any N): 4 waves, RW k rows per wave-wide load.
 // Either way, when k is split over several workgroups a second launch sums
 // the slice partials in slice order.
@@ -80,6 +82,7 @@ struct CsPlan {
     int cb;         // output columns per workgroup
     int waves;      // waves per workgroup
     bool stream;    // streaming kernel
+    bool unaligned; // streaming over rows at any 2-byte alignment (the last k row in the slice pass)
     int64_t kslice; // k rows per workgroup (split-K)
     int64_t slices; // number of k slices (1 = no reduction across workgroups)
     int64_t grid_x;

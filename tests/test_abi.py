@@ -205,9 +205,21 @@ def test_column_stream_plans_split_k_and_size_workspace():
     one = d.plan("cs", 1, 32, 4096, x_addr=256, w_addr=256)  # >= 8 k rows per wave
     assert one.slices == 1 and one.workspace_bytes == 0
     assert d.plan("cs", 16, 4096, 4096, x_addr=256, w_addr=256).mt == 4
-    # general kernel for N not a multiple of 8
+    assert p.rows_or_rw == 0 and up.rows_or_rw == 0  # the streaming kernel
+    # N not a multiple of 8: the streaming kernel over misaligned rows, the
+    # last k row left to the slice pass (which needs its workspace even for
+    # one slice); tiny N or K = 1: the general kernel
     odd = d.plan("cs", 1, 4097, 11007, x_addr=256, w_addr=256)
-    assert odd.vec == 1 and odd.waves == 4
+    assert (odd.vec, odd.rows_or_rw, odd.waves) == (1, 0, 4), odd
+    assert odd.rows_per_group * odd.slices >= 4096 > odd.rows_per_group * (odd.slices - 1)
+    assert odd.workspace_bytes == odd.slices * 11007 * 4
+    c5 = d.plan("cs", 1, 11008, 4097, x_addr=256, w_addr=256)
+    assert (c5.vec, c5.rows_or_rw) == (1, 0) and c5.workspace_bytes == c5.slices * 4097 * 4, c5
+    view = d.plan("cs", 1, 4096, 14336, x_addr=256, w_addr=258)  # a view 2 bytes into its region
+    assert (view.vec, view.rows_or_rw) == (1, 0), view
+    for k, n in [(1, 4097), (64, 7)]:
+        g = d.plan("cs", 1, k, n, x_addr=256, w_addr=256)
+        assert g.rows_or_rw > 0, (k, n, g)
     zero_k = d.plan("cs", 1, 0, 512, x_addr=256, w_addr=256)
     assert zero_k.slices == 1
 

@@ -118,6 +118,35 @@ def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind,
     check(y, y_ref, what=f"mfma underflow signs m={m} k={k} kind={kind}")
 
 
+@pytest.mark.parametrize("kind", [6, 7])
+def test_skinny_mfma_zero_outputs_follow_the_reference_chain(hip, kind, monkeypatch):
+    """An MFMA output that comes out exactly zero is settled by the reference's
+    own chain, so even the order-dependent zeros match bit for bit: rows whose
+    underflowing products change sign along k (the chain keeps the sign of the
+    last one, then +-0 products may flip -0 to +0), exact cancellation, and
+    all-zero weight and activation rows."""
+    m, k = 4, 256
+    x = np.full((m, k), np.float32(1e-38), np.float32)
+    x[1] = -x[1]
+    x[3] = 0                                   # an all-zero activation row
+    x[2, ::3] = -x[2, ::3]
+    w = np.full((8, k), 0x0001, np.uint16)     # every product underflows
+    w[1, k - 1] = 0x8001                       # last product flips sign
+    w[2, k - 1] = 0x0000                       # then a +-0 product after the last nonzero one
+    w[3, 1::2] = 0x8001                        # alternating signs
+    w[4] = 0                                   # an all-zero weight row
+    w[5, :] = 0x3F80                           # 1.0 ...
+    w[5, k // 2:] = 0xBF80                     # ... and -1.0: exact cancellation against x = 1e-38
+    w[6, :7] = 0x8001
+    w[7, ::5] = 0x8000                         # -0 weights among positive tiny products
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    assert hip.plan("rd", m, k, 8, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
+    y_ref = ref(x, w)
+    assert np.any(np.signbit(y_ref[y_ref == 0])) and np.any(~np.signbit(y_ref[y_ref == 0]))
+    y = run_rd(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), (y, y_ref)
+
+
 @pytest.mark.parametrize("tiles", [2, 4])
 @pytest.mark.parametrize("m", [2, 5, 8, 16])
 def test_rows16_blocks_per_workgroup(hip, m, tiles, monkeypatch):
@@ -173,6 +202,58 @@ def test_misaligned_weight_view(hip, offset, k, n):
         hip.synchronize()
         y = dy.download(np.float32, (1, n))
     check(y, ref(x, w), what=f"view +{offset} k={k} n={n}")
+
+
+@pytest.mark.parametrize("offset,k,n", [(2, 4096, 300), (6, 777, 1000), (2, 11008, 4097), (0, 4097, 4097),
+                                        (10, 3, 9), (2, 2, 513)])
+def test_column_stream_weight_views_at_any_2_byte_offset(hip, offset, k, n):
+    """dmc_hip_gemv_cs on W [k,n] starting `offset` bytes into a region that
+    ends right after its last row: the streaming kernel over misaligned rows
+    (each row's last chunk runs into the next row; the matrix's last row is
+    applied by the slice pass with 2-byte loads, so nothing past the region is
+    read)."""
+    x, w = case(1, k, n, seed=offset * 7 + k + n, edge=True)
+    wkn = np.ascontiguousarray(w.T)
+    p = hip.plan("cs", 1, k, n, x_addr=x.ctypes.data, w_addr=256 + offset)
+    assert p.rows_or_rw == 0, p
+    with hip.DeviceBuffer(offset + wkn.nbytes) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * n) as dy:
+        dw.upload(wkn, offset=offset)
+        hip.gemv_cs(dx, dw.addr + offset, dy, 1, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (1, n))
+    check(y, ref(x, w), what=f"cs view +{offset} k={k} n={n}")
+
+
+@pytest.mark.parametrize("k", [2, 7, 1000, 4097])
+def test_column_stream_misaligned_rows_keep_zero_signs(hip, k):
+    """The zero-sign rule of the test below through the streaming kernel over
+    odd-N rows: columns whose products all underflow negative end at -0.0,
+    positive ones at +0.0, also with the last k row in the slice pass."""
+    n = 9
+    x = np.full((1, k), np.float32(-1e-38), np.float32)
+    w = np.full((n, k), 0x0001, np.uint16)
+    w[1::2, :] = 0x8001
+    y_ref = ref(x, w)
+    assert np.all(np.signbit(y_ref[0, ::2])) and not np.any(np.signbit(y_ref[0, 1::2]))
+    y = run_cs_dev(hip, x, w)
+    check(y, y_ref, what=f"cs odd-n underflow signs k={k}")
+
+
+def test_column_stream_batched_slices_at_odd_strides(hip):
+    """Batched device calls whose slices start at alternating 2-byte
+    alignments (rs and ls odd), N odd."""
+    k, n, batch = 300, 1001, 3
+    ls, rs = k + 1, k * n + 3
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((batch - 1) * ls + k).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal((batch - 1) * rs + k * n).astype(np.float32))
+    with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * batch * n) as dy:
+        hip.gemv_cs(dx, dw, dy, 1, k, n, batch, ls, rs)
+        hip.synchronize()
+        y = dy.download(np.float32, (batch * n,))
+    check(y, oracle.matmul_bf16_batched(x, w, k, n, batch, ls, rs), what="cs batched odd strides")
 
 
 @pytest.mark.parametrize("k", [1, 7, 1000, 1001, 4096, 14336])
