@@ -200,8 +200,9 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     float *__restrict__ Y = ga.y[gi];
     const int N = ga.n[gi];
     const int64_t ldw = K, ldy = N;
+    // The workgroup's rows: [rb, rb + nr).
     const int rb = ((int)blockIdx.x - ga.gstart[gi]) * rpw;
-    const int re = min(N, rb + rpw);
+    const int nr = min(N, rb + rpw) - rb;
     const int m0 = blockIdx.y * MT;
     const int mrows = min(MT, M - m0);
 
@@ -226,20 +227,22 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     // jit.rs:29655), -0.0f, the additive identity, for a lane that owns none.
     const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
 
-    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * ldw, (uint32_t)((int64_t)(re - rb) * ldw * 2));
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * ldw, (uint32_t)((int64_t)nr * ldw * 2));
     const uint32_t row_bytes = (uint32_t)ldw * 2;
     __shared__ float red[NW][MT][kMaxRpw];
 
+    // Row rb + i sits at i * row_bytes; rows i >= nr fall past the
+    // resource's range (the planner keeps rpw rows below 2^31 bytes).
     u32x4 ba[ROWS][KV], bb[ROWS][KV];
-    auto load = [&](u32x4 (&wv)[ROWS][KV], int r0) {
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
-            const uint32_t base = (uint32_t)(r0 + q - rb) * row_bytes;
+            const uint32_t base = (uint32_t)(i0 + q) * row_bytes;
 #pragma unroll
             for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], base);
         }
     };
-    load(ba, rb);
+    load(ba, 0);
     float xr[MT][KV][8];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
@@ -250,16 +253,23 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
                 xr[m][j][q] = __uint_as_float(xa[m][j][q]);
                 xr[m][j][q + 4] = __uint_as_float(xb[m][j][q]);
             }
-    // A vector past K reads zero weights and zero x; its weights become bf16
-    // -0.0 (0x8000) so that each of its products is -0.0f, the exact additive
+    // A vector past K reads +0 weights (past the resource's range); its x
+    // becomes -0.0f, so each of its products is -0.0f, the exact additive
     // identity: it leaves any chain unchanged, a -0.0f (a product that
-    // underflowed) included.  Applied to the weights as they arrive, not to x:
-    // a select on x would make the prologue wait for x.
-    uint32_t pad[KV];
+    // underflowed) included.  Applied once, after both weight buffers' loads
+    // are in flight (the sign bit needs x to have arrived), so the loop's
+    // widen stays one shift or mask per weight.
+    auto pad_x = [&]() {
 #pragma unroll
-    for (int j = 0; j < KV; ++j) pad[j] = has[j] ? 0u : 0x80008000u;
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int j = 0; j < KV; ++j)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    xr[m][j][e] = __uint_as_float(__float_as_uint(xr[m][j][e]) | (has[j] ? 0u : 0x80000000u));
+    };
 
-    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
         float acc[MT][ROWS];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
@@ -271,7 +281,7 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
             for (int e = 0; e < 8; ++e)
 #pragma unroll
                 for (int q = 0; q < ROWS; ++q) {
-                    const uint32_t d = wv[q][j][e >> 1] | pad[j];
+                    const uint32_t d = wv[q][j][e >> 1];
                     const float w = (e & 1) ? widen_hi(d) : widen_lo(d);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
@@ -281,18 +291,24 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) {
                 const float s = wave_sum_dpp(acc[m][q]);
-                if (lane == 0 && r0 + q < re) red[wave][m][r0 - rb + q] = s;
+                if (lane == 0 && i0 + q < nr) red[wave][m][i0 + q] = s;
             }
     };
-    for (int r0 = rb; r0 < re; r0 += 2 * ROWS) {
-        load(bb, r0 + ROWS);
-        sum_rows(ba, r0);
-        if (r0 + ROWS >= re) break;
-        load(ba, r0 + 2 * ROWS);
-        sum_rows(bb, r0 + ROWS);
+    // Rows [i0, i0 + ROWS) sit in one buffer while the next ROWS rows load
+    // into the other; the first step is peeled so that pad_x follows the
+    // second buffer's loads.
+    load(bb, ROWS);
+    __builtin_amdgcn_sched_barrier(0);  // keep pad_x's wait for x after every load above
+    pad_x();
+    sum_rows(ba, 0);
+    for (int i0 = 0; i0 + ROWS < nr; i0 += 2 * ROWS) {
+        load(ba, i0 + 2 * ROWS);
+        sum_rows(bb, i0 + ROWS);
+        if (i0 + 2 * ROWS >= nr) break;
+        load(bb, i0 + 3 * ROWS);
+        sum_rows(ba, i0 + 2 * ROWS);
     }
     __syncthreads();
-    const int nr = re - rb;
     for (int t = threadIdx.x; t < MT * nr; t += 64 * NW) {
         const int m = t / nr, r = t - m * nr;
         float s = red[0][m][r];
