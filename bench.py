@@ -318,6 +318,43 @@ def extended(d, W, reps: int) -> dict:
             record(f"C2 rd {name} m={m}", batch_us(d, f, 50), n, k, m)
             s.free()
     out.update(helpers(d, c2["up"][0]))
+    out.update(ingress(d, c2["down"][0]))
+    return out
+
+
+def ingress(d, w) -> dict:
+    """Weight ingress: dmc_hip_vault_load_npz reading a C2 weight from an .npz
+    in the page cache into HBM (stored: parallel positioned reads; deflated:
+    one zlib stream), against the reference's CPU loader restated (the oracle's
+    dmc_vault_load_npz: the whole entry read into host memory, CRC checked,
+    data copied out).  GB/s = array bytes / wall time of one call."""
+    import tempfile
+
+    from oracle import npz as onpz
+
+    out = {}
+    with tempfile.TemporaryDirectory(prefix="dmc_ingress_") as td:
+        for label, save in (("stored", np.savez), ("deflated", np.savez_compressed)):
+            path = pathlib.Path(td) / f"{label}.npz"
+            save(path, w=w)
+            path.read_bytes()  # page cache
+            times = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                buf = d.vault_load_npz(path, "w", w.size, 2, 0)
+                times.append(time.perf_counter() - t0)
+                buf.free()
+            t0 = time.perf_counter()
+            host = onpz.vault_load_npz(path, "w", w.size, 2, 0)
+            cpu = time.perf_counter() - t0
+            assert host is not None and len(host) == w.nbytes
+            dev = min(times)
+            rec = {"bytes": w.nbytes, "file_bytes": path.stat().st_size, "us": round(dev * 1e6, 1),
+                   "GB/s": round(w.nbytes / dev / 1e9, 2), "cpu_loader_us": round(cpu * 1e6, 1),
+                   "cpu_loader_GB/s": round(w.nbytes / cpu / 1e9, 2)}
+            out[f"ingress npz {label} W{list(w.shape)}"] = rec
+            log(f"ingress npz {label}: {rec['GB/s']} GB/s into HBM ({rec['us']:.0f} us), "
+                f"CPU loader {rec['cpu_loader_GB/s']} GB/s")
     return out
 
 

@@ -25,7 +25,7 @@ __all__ = [
     "matmul_bf16_gpu", "matmul_bf16_gpu_t", "matmul_bf16_gpu_batched",
     "matmul_bf16_gpu_batched_deferred", "flush", "DeviceBuffer", "gemv_cs", "gemv_rd",
     "synchronize", "probe_read", "gemv_rd_grouped", "fill_counter_bf16", "Graph", "Event", "plan", "register_weight", "release_weights",
-    "resident_count", "resident_bytes", "device_info",
+    "resident_count", "resident_bytes", "device_info", "vault_load_npz", "npz_locate", "f16_upconvert",
 ]
 
 MIN_MACS = 1 << 17  # DMC_HIP_MIN_MACS in include/dmc_hip.h
@@ -149,6 +149,13 @@ class DeviceBuffer:
             _lib.check(-3)
 
     @classmethod
+    def adopt(cls, addr: int, nbytes: int) -> "DeviceBuffer":
+        """Take ownership of a region the library allocated (freed by free())."""
+        buf = cls.__new__(cls)
+        buf.addr, buf.nbytes = int(addr), int(nbytes)
+        return buf
+
+    @classmethod
     def from_numpy(cls, a: np.ndarray) -> "DeviceBuffer":
         a = np.ascontiguousarray(a)
         buf = cls(max(a.nbytes, 1))
@@ -228,6 +235,41 @@ def bf16_upconvert(src, dst, n: int) -> None:
 def f32_to_bf16(src, dst, n: int) -> None:
     """Enqueue dst bf16[n] = src f32 bits >> 16 (dmc_f32_to_bf16, jit.rs:29783)."""
     _lib.check(_lib.load().dmc_hip_f32_to_bf16(_addr(src), _addr(dst), n))
+
+
+def f16_upconvert(src, dst, n: int) -> None:
+    """Enqueue dst f32[n] = the IEEE f16 patterns src[n] widened exactly
+    (f16_bits_to_f32, jit.rs:29231-29257)."""
+    _lib.check(_lib.load().dmc_hip_f16_upconvert(_addr(src), _addr(dst), n))
+
+
+# ---- weight ingress ---------------------------------------------------------------
+
+# vault.load_npz dtypes: (on-disk element bytes, convert) as the JIT lowers
+# them (jit.rs:12671-12681); bf16 stays 2-byte (the Bf16Tensor route).
+NPZ_DTYPES = {"f32": (4, 0), "f64": (8, 0), "i32": (4, 0), "i64": (8, 0), "bf16": (2, 0),
+              "f16": (2, 2), "bool": (1, 0)}
+
+
+def vault_load_npz(path, key: str, numel: int, elem_bytes: int = 2, convert: int = 0) -> DeviceBuffer:
+    """dmc_hip_vault_load_npz: array `key` of the .npz at `path` in a new
+    device region (numel * elem_bytes bytes, numel * 4 when convert widens,
+    plus 16 zero bytes of padding).  Raises HipError where the reference's
+    dmc_vault_load_npz (jit.rs:29836-29926) returns 0."""
+    lib = _lib.load()
+    addr = lib.dmc_hip_vault_load_npz(str(path).encode(), key.encode(), numel, elem_bytes, convert)
+    if not addr:
+        raise HipError(-5, lib.dmc_hip_last_error().decode())
+    out_bytes = numel * (4 if convert else elem_bytes)
+    return DeviceBuffer.adopt(addr, out_bytes + 16)
+
+
+def npz_locate(path, key: str) -> dict:
+    """Where dmc_hip_vault_load_npz finds `key` (no device needed)."""
+    info = (ctypes.c_int64 * 8)()
+    _lib.check(_lib.load().dmc_hip_npz_locate(str(path).encode(), key.encode(), info))
+    names = ("bare", "method", "compressed", "uncompressed", "data_pos", "npy_major", "npy_data_offset", "crc")
+    return dict(zip(names, [int(v) for v in info]))
 
 
 def bf16_transpose_2d(src, dst, m: int, n: int) -> None:

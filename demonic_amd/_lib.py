@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dmc_hip_bf16_upconvert": (i32, [i64, i64, i64]),
     "dmc_hip_f32_to_bf16": (i32, [i64, i64, i64]),
     "dmc_hip_bf16_transpose_2d": (i32, [i64, i64, i64, i64]),
+    "dmc_hip_f16_upconvert": (i32, [i64, i64, i64]),
+    "dmc_hip_vault_load_npz": (i64, [cstr, cstr, i64, i64, i64]),
+    "dmc_hip_npz_locate": (i32, [cstr, cstr, ctypes.POINTER(i64)]),
     "dmc_hip_plan": (i32, [i32, i64, i64, i64, i64, i64, i64, i64, ctypes.POINTER(i64)]),
     "dmc_hip_capture_begin": (i32, []),
     "dmc_hip_capture_end": (i64, []),

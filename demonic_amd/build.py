@@ -54,13 +54,13 @@ def build_lib() -> pathlib.Path:
     LIB_DIR.mkdir(exist_ok=True)
     cc = hipcc()
     objs = []
-    for src, device in (("gemv_kernels.hip", True), ("dmc_hip_runtime.cpp", False)):
+    for src, device in (("gemv_kernels.hip", True), ("dmc_hip_runtime.cpp", False), ("npz_ingress.cpp", False)):
         obj = OBJ / (src.rsplit(".", 1)[0] + ".o")
         lang = ["-x", "hip"] + DEVICE if device else ["-D__HIP_PLATFORM_AMD__"]
         _run([cc, *COMMON, *lang, "-c", str(CSRC / src), "-o", str(obj)])
         objs.append(str(obj))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", str(tmp)])
+    _run([cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", str(tmp), "-lz", "-pthread"])
     os.replace(tmp, LIB)  # atomic: a concurrent loader never sees a half-written file
     return LIB
 

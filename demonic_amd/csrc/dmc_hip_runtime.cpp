@@ -16,10 +16,14 @@
 //     or fatal (the void drop-in entries), never silently recomputed.
 #include "../../include/dmc_hip.h"
 #include "gemv_launch.h"
+#include "npz_ingress.h"
 
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cstdarg>
 #include <cstdio>
@@ -27,6 +31,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
@@ -139,6 +144,8 @@ struct Ctx {
     std::vector<Pending> pending;
     void *dummy = nullptr;  // non-null device address for zero-byte weights
     void *sink = nullptr;   // probe output words
+    std::vector<void *> ingress;        // pinned chunks for .npz ingress, kIngressChunk bytes each
+    std::vector<hipEvent_t> ingress_ev; // one per chunk: its last copy to the device
     bool timing = false;
     Stats st;
 };
@@ -478,6 +485,209 @@ void run_host_or_die(const char *entry, bool rd, int64_t l, int64_t r, int64_t o
     if (rc) fatal(entry);
 }
 
+
+// ---- weight ingress from .npz (jit.rs:29836-29944) ----------------------------
+//
+// The entry's uncompressed bytes stream through pinned chunks; the part that
+// is array data goes to the device with asynchronous copies on the library
+// stream while the next chunks are read.  A stored entry of at least
+// kIngressParallelMin bytes is read by several threads (positioned reads,
+// one CRC-32 per chunk, combined in order); a deflated one by one thread
+// through zlib.  The whole entry is read, so its CRC-32 is checked as the
+// reference's reader checks it.
+
+constexpr size_t kIngressChunk = (size_t)8 << 20;
+constexpr uint64_t kIngressParallelMin = (uint64_t)64 << 20;
+
+struct FdCloser {
+    int fd;
+    ~FdCloser() {
+        if (fd >= 0) close(fd);
+    }
+};
+
+// Pinned chunks [0, count) of the ingress pool, allocated on first use.
+int ingress_pool(size_t count) {
+    Ctx &c = ctx();
+    while (c.ingress.size() < count) {
+        void *p = nullptr;
+        HIP_TRY(hipHostMalloc(&p, kIngressChunk, hipHostMallocDefault), "hipHostMalloc(ingress)");
+        hipEvent_t ev = nullptr;
+        hipError_t e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) {
+            (void)hipHostFree(p);
+            return hip_fail(e, "hipEventCreate(ingress)");
+        }
+        c.ingress.push_back(p);
+        c.ingress_ev.push_back(ev);
+    }
+    return DMC_HIP_OK;
+}
+
+// Bytes [pos, pos + n) of the entry sit in pinned chunk `buf`; the part inside
+// the array's bytes [doff, doff + take) is copied to dst + (offset - doff),
+// then the chunk's event is recorded so its next user can wait for the copy.
+hipError_t deliver(const uint8_t *buf, uint64_t pos, size_t n, uint64_t doff, uint64_t take, uint8_t *dst,
+                   hipEvent_t ev, hipStream_t s) {
+    const uint64_t lo = std::max(pos, doff), hi = std::min<uint64_t>(pos + n, doff + take);
+    if (lo < hi) {
+        hipError_t e = hipMemcpyAsync(dst + (lo - doff), buf + (lo - pos), (size_t)(hi - lo), hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipEventRecord(ev, s);
+}
+
+int64_t vault_load_npz_locked(const char *path, const char *key, int64_t numel, int64_t elem_bytes,
+                              int64_t convert) {
+    if (!path || !key) return fail(DMC_HIP_EINVAL, "vault.load_npz: null path or key"), 0;
+    if (numel < 0 || elem_bytes < 1 || elem_bytes > 8 || convert < 0 || convert > 2 ||
+        (convert != 0 && elem_bytes != 2) || numel > (INT64_MAX - 256) / 8)
+        return fail(DMC_HIP_EINVAL, "vault.load_npz: bad numel/elem_bytes/convert (%lld, %lld, %lld)",
+                    (long long)numel, (long long)elem_bytes, (long long)convert), 0;
+    if (ensure_init()) return 0;
+    Ctx &c = ctx();
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(DMC_HIP_EIO, "vault.load_npz: cannot open `%s`: %s", path, strerror(errno)), 0;
+    FdCloser closer{fd};
+    dmc::NpzEntry ent;
+    std::string err;
+    if (dmc::npz_find_entry(fd, key, ent, err))
+        return fail(DMC_HIP_EIO, "vault.load_npz: %s in `%s`", err.c_str(), path), 0;
+
+    const bool parallel = ent.method == 0 && ent.usize >= kIngressParallelMin;
+    const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+    const size_t workers = parallel ? std::min<size_t>(16, hw) : 0;
+    if (ingress_pool(2 + 2 * workers)) return 0;
+    for (hipEvent_t ev : c.ingress_ev) {  // every chunk starts out free
+        hipError_t e = hipEventRecord(ev, c.stream);
+        if (e != hipSuccess) return hip_fail(e, "hipEventRecord"), 0;
+    }
+
+    // The first chunk: the .npy header.
+    dmc::NpzStream zs(fd, ent);
+    uint8_t *head = static_cast<uint8_t *>(c.ingress[0]);
+    const int64_t hn = zs.read(head, kIngressChunk, err);
+    if (hn < 0) return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: %s", key, path, err.c_str()), 0;
+    int major = 0;
+    const int64_t doff_s = dmc::npy_data_offset(head, (size_t)hn, &major);
+    if (doff_s == -1) return fail(DMC_HIP_EIO, "vault.load_npz: entry `%s` is not a valid .npy file", key), 0;
+    if (doff_s < 0) return fail(DMC_HIP_EIO, "vault.load_npz: entry `%s` ends inside its .npy header", key), 0;
+    const uint64_t doff = (uint64_t)doff_s;
+    const uint64_t src_bytes = (uint64_t)numel * (uint64_t)elem_bytes;
+    const uint64_t out_bytes = convert ? (uint64_t)numel * 4 : src_bytes;
+    const uint64_t avail = ent.usize > doff ? ent.usize - doff : 0;
+    const uint64_t take = std::min(avail, src_bytes);
+    if (take < src_bytes)  // the reference reports the short entry and loads what it holds
+        fprintf(stderr, "vault.load_npz: entry `%s` data is %llu bytes but expected %llu\n", key,
+                (unsigned long long)avail, (unsigned long long)src_bytes);
+
+    void *region = nullptr, *raw = nullptr;
+    hipError_t he = hipMalloc(&region, (size_t)out_bytes + dmc::kWeightSlack);
+    if (he != hipSuccess) return hip_fail(he, "hipMalloc(region)"), 0;
+    // On failure after this point: drain the stream, free, return 0 (the
+    // message is already set).
+    auto give_up = [&]() -> int64_t {
+        (void)hipStreamSynchronize(c.stream);
+        if (raw) (void)hipFree(raw);
+        (void)hipFree(region);
+        return 0;
+    };
+    if (convert && take) {
+        he = hipMalloc(&raw, (size_t)take);
+        if (he != hipSuccess) return hip_fail(he, "hipMalloc(ingress staging)"), give_up();
+    }
+    uint8_t *dst = static_cast<uint8_t *>(convert ? raw : region);
+
+    he = deliver(head, 0, (size_t)hn, doff, take, dst, c.ingress_ev[0], c.stream);
+    if (he != hipSuccess) return hip_fail(he, "ingress copy"), give_up();
+    uint32_t crc = zs.crc();
+    uint64_t produced = (uint64_t)hn;
+    if (!parallel) {
+        // One reader: chunks alternate between two pinned buffers.
+        for (int b = 1;; b ^= 1) {
+            he = hipEventSynchronize(c.ingress_ev[b]);
+            if (he != hipSuccess) return hip_fail(he, "hipEventSynchronize"), give_up();
+            uint8_t *buf = static_cast<uint8_t *>(c.ingress[b]);
+            const int64_t got = zs.read(buf, kIngressChunk, err);
+            if (got < 0)
+                return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: %s", key, path, err.c_str()),
+                       give_up();
+            if (got == 0) break;
+            he = deliver(buf, produced, (size_t)got, doff, take, dst, c.ingress_ev[b], c.stream);
+            if (he != hipSuccess) return hip_fail(he, "ingress copy"), give_up();
+            produced += (uint64_t)got;
+        }
+        crc = zs.crc();
+    } else {
+        // Chunk i >= 1 of the stored entry goes to worker (i - 1) % workers,
+        // which alternates between its two pinned buffers.
+        const uint64_t nchunks = (ent.usize + kIngressChunk - 1) / kIngressChunk;
+        std::vector<uint32_t> crcs(nchunks, 0);
+        std::atomic<bool> bad{false};
+        std::string werr;
+        std::mutex werr_mu;
+        auto work = [&](size_t w) {
+            for (uint64_t i = 1 + w, round = 0; i < nchunks && !bad.load(); i += workers, ++round) {
+                const size_t slot = 2 + 2 * w + (round & 1);
+                uint8_t *buf = static_cast<uint8_t *>(c.ingress[slot]);
+                const uint64_t pos = i * kIngressChunk;
+                const size_t n = (size_t)std::min<uint64_t>(kIngressChunk, ent.usize - pos);
+                hipError_t e = hipEventSynchronize(c.ingress_ev[slot]);
+                std::string why;
+                if (e != hipSuccess) why = std::string("hipEventSynchronize: ") + hipGetErrorString(e);
+                else if (!dmc::pread_exact(fd, buf, n, ent.data_pos + pos)) why = "read failed";
+                if (why.empty()) {
+                    crcs[i] = dmc::npz_crc32(0, buf, n);
+                    e = deliver(buf, pos, n, doff, take, dst, c.ingress_ev[slot], c.stream);
+                    if (e != hipSuccess) why = std::string("ingress copy: ") + hipGetErrorString(e);
+                }
+                if (!why.empty()) {
+                    std::lock_guard<std::mutex> g(werr_mu);
+                    if (!bad.exchange(true)) werr = why;
+                    return;
+                }
+            }
+        };
+        std::vector<std::thread> pool;
+        for (size_t w = 0; w < workers; ++w) pool.emplace_back(work, w);
+        for (auto &t : pool) t.join();
+        if (bad.load())
+            return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: %s", key, path, werr.c_str()),
+                   give_up();
+        for (uint64_t i = 1; i < nchunks; ++i) {
+            const uint64_t n = std::min<uint64_t>(kIngressChunk, ent.usize - i * kIngressChunk);
+            crc = dmc::npz_crc32_combine(crc, crcs[i], n);
+            produced += n;
+        }
+    }
+    if (produced != ent.usize)
+        return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: %llu bytes, the archive says %llu",
+                    key, path, (unsigned long long)produced, (unsigned long long)ent.usize),
+               give_up();
+    if (crc != ent.crc)
+        return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: invalid checksum", key, path),
+               give_up();
+
+    // Widen on the device (npz_fill, jit.rs:29931-29941: take/2 elements), and
+    // zero what the entry did not hold plus the padding.
+    uint64_t filled = take;
+    if (convert) {
+        const int64_t elems = (int64_t)(take / 2);
+        he = convert == 1 ? dmc::launch_bf16_upconvert(static_cast<const uint16_t *>(raw), static_cast<float *>(region),
+                                                        elems, c.stream)
+                          : dmc::launch_f16_upconvert(static_cast<const uint16_t *>(raw), static_cast<float *>(region),
+                                                       elems, c.stream);
+        if (he != hipSuccess) return hip_fail(he, "ingress widen launch"), give_up();
+        filled = (uint64_t)elems * 4;
+    }
+    he = hipMemsetAsync(static_cast<uint8_t *>(region) + filled, 0,
+                        (size_t)(out_bytes - filled) + dmc::kWeightSlack, c.stream);
+    if (he != hipSuccess) return hip_fail(he, "ingress zero fill"), give_up();
+    he = hipStreamSynchronize(c.stream);
+    if (he != hipSuccess) return hip_fail(he, "hipStreamSynchronize"), give_up();
+    if (raw) (void)hipFree(raw);
+    return reinterpret_cast<int64_t>(region);
+}
 }  // namespace
 
 // ---- drop-in surface ----------------------------------------------------------
@@ -873,6 +1083,44 @@ int32_t dmc_hip_device_cus(void) {
 const char *dmc_hip_device_arch(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     return ensure_init() == DMC_HIP_OK ? ctx().arch.c_str() : "";
+}
+
+int64_t dmc_hip_vault_load_npz(const char *path, const char *key, int64_t numel, int64_t elem_bytes,
+                               int64_t convert) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return vault_load_npz_locked(path, key, numel, elem_bytes, convert);
+}
+
+int32_t dmc_hip_npz_locate(const char *path, const char *key, int64_t *info) {
+    if (!path || !key || !info) return fail(DMC_HIP_EINVAL, "npz_locate: null argument");
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return fail(DMC_HIP_EIO, "vault.load_npz: cannot open `%s`: %s", path, strerror(errno));
+    FdCloser closer{fd};
+    dmc::NpzEntry ent;
+    std::string err;
+    if (dmc::npz_find_entry(fd, key, ent, err)) return fail(DMC_HIP_EIO, "vault.load_npz: %s in `%s`", err.c_str(), path);
+    std::vector<uint8_t> head(4096);
+    dmc::NpzStream zs(fd, ent);
+    const int64_t hn = zs.read(head.data(), head.size(), err);
+    if (hn < 0) return fail(DMC_HIP_EIO, "vault.load_npz: read error for `%s` in `%s`: %s", key, path, err.c_str());
+    int major = -1;
+    const int64_t doff = dmc::npy_data_offset(head.data(), (size_t)hn, &major);
+    const int64_t v[8] = {ent.bare ? 1 : 0, ent.method, (int64_t)ent.csize, (int64_t)ent.usize, (int64_t)ent.data_pos,
+                          doff == -1 ? -1 : major, doff, (int64_t)ent.crc};
+    memcpy(info, v, sizeof v);
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_f16_upconvert(int64_t src_dev, int64_t dst_dev, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (n < 0 || (n > 0 && (!src_dev || !dst_dev))) return fail(DMC_HIP_EINVAL, "bad f16 upconvert arguments");
+    if (n == 0) return DMC_HIP_OK;
+    int rc = ensure_init();
+    if (rc) return rc;
+    hipError_t e = dmc::launch_f16_upconvert(reinterpret_cast<const uint16_t *>(src_dev),
+                                             reinterpret_cast<float *>(dst_dev), n, ctx().stream);
+    if (e != hipSuccess) return hip_fail(e, "f16 upconvert launch");
+    return DMC_HIP_OK;
 }
 
 }  // extern "C"

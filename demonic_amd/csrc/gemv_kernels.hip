@@ -1439,12 +1439,35 @@ transpose_bf16_v8_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict_
     }
 }
 
-// dst[i] = bf16 widen of src[i] (bits << 16; NaN payloads, infinities and
-// subnormals kept), and dst[i] = src[i]'s bits >> 16 (truncation, the inverse
-// on bf16-representable values).  VEC = 8: 8 elements per thread per step
-// (16-byte-aligned bases, count a multiple of 8 in the vector part; the
-// remainder runs one element per thread).  Grid-stride.
-template <int VEC>
+// IEEE binary16 bits (in the low 16 bits of h) to binary32 bits, exactly, by
+// integer steps: the f16_bits_to_f32 of compiler/src/jit.rs:29231-29257
+// (subnormals normalized, NaN payloads and the signalling bit kept, which a
+// hardware conversion may quiet).
+__device__ __forceinline__ uint32_t f16_bits_to_f32_bits(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+    if (exp == 0) {
+        if (mant == 0) return sign;
+        const int s = __clz((int)mant) - 21;  // shifts that bring the leading 1 to bit 10
+        return sign | ((uint32_t)(113 - s) << 23) | (((mant << s) & 0x3ffu) << 13);
+    }
+    if (exp == 0x1f) return sign | 0x7f800000u | (mant << 13);
+    return sign | ((exp + 112u) << 23) | (mant << 13);
+}
+
+// dst[i] = widen of the 16-bit pattern src[i] to f32: bf16 (F16 = false,
+// bits << 16; NaN payloads, infinities and subnormals kept) or IEEE f16
+// (F16 = true); and dst[i] = src[i]'s bits >> 16 (truncation, the inverse of
+// the bf16 widen on bf16-representable values).  VEC = 8: 8 elements per
+// thread per step (16-byte-aligned bases, count a multiple of 8 in the vector
+// part; the remainder runs one element per thread).  Grid-stride.
+template <bool F16>
+__device__ __forceinline__ uint32_t widen16(uint32_t h) {
+    if constexpr (F16) return f16_bits_to_f32_bits(h);
+    return h << 16;
+}
+
+template <int VEC, bool F16>
 __global__ void __launch_bounds__(256)
 bf16_upconvert_kernel(const uint16_t *__restrict__ src, float *__restrict__ dst, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -1455,17 +1478,17 @@ bf16_upconvert_kernel(const uint16_t *__restrict__ src, float *__restrict__ dst,
             u32x4 lo, hi;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                lo[2 * q] = v[q] << 16;
-                lo[2 * q + 1] = v[q] & 0xffff0000u;
-                hi[2 * q] = v[q + 2] << 16;
-                hi[2 * q + 1] = v[q + 2] & 0xffff0000u;
+                lo[2 * q] = widen16<F16>(v[q] & 0xffffu);
+                lo[2 * q + 1] = F16 ? widen16<F16>(v[q] >> 16) : v[q] & 0xffff0000u;
+                hi[2 * q] = widen16<F16>(v[q + 2] & 0xffffu);
+                hi[2 * q + 1] = F16 ? widen16<F16>(v[q + 2] >> 16) : v[q + 2] & 0xffff0000u;
             }
             reinterpret_cast<u32x4 *>(dst)[2 * i] = lo;
             reinterpret_cast<u32x4 *>(dst)[2 * i + 1] = hi;
         }
         i = (n / 8) * 8 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     }
-    for (; i < n; i += stride) dst[i] = __uint_as_float((uint32_t)src[i] << 16);
+    for (; i < n; i += stride) dst[i] = __uint_as_float(widen16<F16>((uint32_t)src[i]));
 }
 
 template <int VEC>
@@ -2084,15 +2107,24 @@ hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t row
     return hipGetLastError();
 }
 
-hipError_t launch_bf16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t s) {
+template <bool F16>
+hipError_t launch_widen16(const uint16_t *src, float *dst, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     if (aligned(src, 16) && aligned(dst, 16))
-        hipLaunchKernelGGL(bf16_upconvert_kernel<8>, dim3(stride_grid((n / 8 + 255) / 256)), dim3(256), 0, s, src,
-                           dst, n);
+        hipLaunchKernelGGL((bf16_upconvert_kernel<8, F16>), dim3(stride_grid((n / 8 + 255) / 256)), dim3(256), 0, s,
+                           src, dst, n);
     else
-        hipLaunchKernelGGL(bf16_upconvert_kernel<1>, dim3(stride_grid((n + 255) / 256)), dim3(256), 0, s, src, dst,
-                           n);
+        hipLaunchKernelGGL((bf16_upconvert_kernel<1, F16>), dim3(stride_grid((n + 255) / 256)), dim3(256), 0, s, src,
+                           dst, n);
     return hipGetLastError();
+}
+
+hipError_t launch_bf16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t s) {
+    return launch_widen16<false>(src, dst, n, s);
+}
+
+hipError_t launch_f16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t s) {
+    return launch_widen16<true>(src, dst, n, s);
 }
 
 hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t s) {

@@ -128,6 +128,8 @@ hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t row
 
 // dst[i] = widen(src[i]) (bits << 16), and dst[i] = bits(src[i]) >> 16.
 hipError_t launch_bf16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t stream);
+// dst[i] = the f32 value of the IEEE binary16 pattern src[i], exactly (NaN payloads kept).
+hipError_t launch_f16_upconvert(const uint16_t *src, float *dst, int64_t n, hipStream_t stream);
 hipError_t launch_f32_to_bf16(const float *src, uint16_t *dst, int64_t n, hipStream_t stream);
 
 // Synthetic weights for measurements: dst[i] = table[h(offset + i) >> 48],

@@ -41,6 +41,7 @@ extern "C" {
 #define DMC_HIP_EINVAL (-2)  /* bad argument (negative size, null pointer) */
 #define DMC_HIP_ENOMEM (-3)  /* device or pinned allocation failed          */
 #define DMC_HIP_EDEVICE (-4) /* a HIP runtime call failed                   */
+#define DMC_HIP_EIO (-5)     /* file missing or unreadable, not a valid .npz */
 
 /* ---- drop-in operator surface (compiler/src/gpu.rs) --------------------- */
 
@@ -198,6 +199,42 @@ int32_t dmc_hip_capture_begin(void);
 int64_t dmc_hip_capture_end(void);
 int32_t dmc_hip_graph_launch(int64_t exec);
 int32_t dmc_hip_graph_destroy(int64_t exec);
+
+/* ---- weight ingress (the loader behind vault.load_npz) ------------------ */
+
+/* Device form of dmc_vault_load_npz (jit.rs:29836-29944), the loader the JIT
+ * emits for `vault.load_npz[T, shape](path, key=...)` (jit.rs:12639-12728):
+ * array `key` of the NumPy .npz archive at `path` goes straight into a new
+ * device region (free it with dmc_hip_region_free) instead of a host Vault
+ * buffer.  The reference's rules: the entry is "{key}.npy", else "{key}";
+ * the .npy header is skipped (major version 1: 2-byte length at byte 8,
+ * otherwise 4-byte) and not checked against the request; numel * elem_bytes
+ * bytes of data follow; convert 0 copies them raw (bf16 weights stay 2-byte,
+ * the Bf16Tensor route of jit.rs:12673-12676), 1 widens bf16 and 2 widens
+ * f16 to f32 (npz_fill, jit.rs:29928-29941; region of numel * 4 bytes,
+ * elem_bytes must be 2).  An entry shorter than the request loads what it
+ * holds, reports the short count on stderr as the reference does, and the
+ * rest of the region is zero.  Stored and deflated entries, ZIP64 archives;
+ * the entry's CRC-32 is checked.  16 zero bytes follow the data (the padding
+ * of resident weights).  Returns the region's device address, or 0 with the
+ * reason in dmc_hip_last_error() (the reference prints it and returns 0). */
+int64_t dmc_hip_vault_load_npz(const char *path, const char *key, int64_t numel, int64_t elem_bytes,
+                               int64_t convert);
+
+/* Where dmc_hip_vault_load_npz finds `key` in `path`, touching no device:
+ * info[0] 1 if the entry is "{key}" rather than "{key}.npy"; [1] compression
+ * method (0 stored, 8 deflate); [2] compressed and [3] uncompressed bytes;
+ * [4] file offset of the entry's data; [5] .npy major version (-1: not a
+ * .npy); [6] offset of the array data in the entry (-1 not a .npy, -2 a
+ * header cut short); [7] CRC-32 from the central directory.  Returns
+ * DMC_HIP_OK or DMC_HIP_EIO / DMC_HIP_EINVAL. */
+int32_t dmc_hip_npz_locate(const char *path, const char *key, int64_t *info);
+
+/* Enqueue dst f32[n] = the IEEE binary16 patterns src[n] widened exactly:
+ * f16_bits_to_f32 (jit.rs:29231-29257), the conversion npz_fill applies for
+ * convert == 2 (jit.rs:29937), by integer steps so NaN payloads and the
+ * signalling bit survive. */
+int32_t dmc_hip_f16_upconvert(int64_t src_dev, int64_t dst_dev, int64_t n);
 
 /* HIP events on the library stream, for timing device work. */
 int64_t dmc_hip_event_create(void);
