@@ -318,6 +318,122 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     }
 }
 
+// ---- RD streaming, two 8-wave halves sharing x through LDS (M = 1, long rows) ----
+//
+// gemv_rd_stream_kernel's layout with one 16-wave workgroup per CU in place
+// of two 8-wave ones: each half walks its own rpw/2 consecutive rows exactly
+// as an 8-wave workgroup does (k split over its 8 waves, two register
+// buffers, unconditional loads), but x is read from L2 once per workgroup,
+// into LDS, and every lane takes its windows from there.  At K = 14336 this
+// halves x's L2 traffic (each 8-wave workgroup otherwise streams all 56 KiB
+// of x at kernel start, 28 MiB per launch).
+constexpr int kXldsMaxK = 16384;  // x in LDS: 64 KiB; KV <= 4 windows per lane
+
+template <int KV, int ROWS>
+__global__ void __launch_bounds__(1024)
+gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
+                           int N, int K, int rpw) {
+    static_assert(KV <= 4, "x windows must lie inside the LDS copy");
+    constexpr int NW = 8;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave = wid & (NW - 1), half = wid / NW;
+    const int hrows = rpw / 2;
+    const int rb = (int)blockIdx.x * rpw + half * hrows;  // this half's rows: [rb, rb + nr)
+    const int nr = max(0, min(N, rb + hrows) - rb);
+    __shared__ __attribute__((aligned(16))) float xs[kXldsMaxK];
+    __shared__ float red[2][NW][kMaxRpw / 2];
+
+    // x into registers as 16-byte pieces t, t + 1024, ... (pieces past K read
+    // as zeros from past the resource's range).
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4);
+    u32x4 xp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + i * 1024u) * 16u, 0, 0);
+
+    uint32_t eoff[KV];
+    bool has[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int e = ((j * NW + wave) * 64 + lane) * 8;
+        has[j] = e < K;
+        eoff[j] = has[j] ? (uint32_t)e * 2 : kOutOfRange;
+    }
+    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * K, (uint32_t)((int64_t)nr * K * 2));
+    const uint32_t row_bytes = (uint32_t)K * 2;
+    u32x4 ba[ROWS][KV], bb[ROWS][KV];
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const uint32_t base = (uint32_t)(i0 + q) * row_bytes;
+#pragma unroll
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], base);
+        }
+    };
+    load(ba, 0);
+    load(bb, ROWS);
+    __builtin_amdgcn_sched_barrier(0);  // both weight buffers in flight before the wait for x
+#pragma unroll
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&xs[(threadIdx.x + i * 1024) * 4]) = xp[i];
+    __syncthreads();
+    // The lane's windows; a window past K (zeros in LDS) gets x = -0.0f, so
+    // its products with the +0 weights read past the range are -0.0f, the
+    // exact additive identity.
+    float xr[KV][8];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int e = ((j * NW + wave) * 64 + lane) * 8;
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[e]);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[e + 4]);
+        const uint32_t sgn = has[j] ? 0u : 0x80000000u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xr[j][q] = __uint_as_float(a[q] | sgn);
+            xr[j][q + 4] = __uint_as_float(b[q] | sgn);
+        }
+    }
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
+        float acc[ROWS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) acc[q] = init;
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int q = 0; q < ROWS; ++q) {
+                    const uint32_t d = wv[q][j][e >> 1];
+                    acc[q] = fmaf(xr[j][e], (e & 1) ? widen_hi(d) : widen_lo(d), acc[q]);
+                }
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const float s = wave_sum_dpp(acc[q]);
+            if (lane == 0 && i0 + q < nr) red[half][wave][i0 + q] = s;
+        }
+    };
+    sum_rows(ba, 0);
+    for (int i0 = 0; i0 + ROWS < nr; i0 += 2 * ROWS) {
+        load(ba, i0 + 2 * ROWS);
+        sum_rows(bb, i0 + ROWS);
+        if (i0 + 2 * ROWS >= nr) break;
+        load(bb, i0 + 3 * ROWS);
+        sum_rows(ba, i0 + 2 * ROWS);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 2 * hrows; t += 1024) {
+        const int h = t / hrows, r = t - h * hrows;
+        const int row = (int)blockIdx.x * rpw + h * hrows + r;
+        if (row < N) {
+            float s = red[h][0][r];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) s += red[h][w][r];
+            Y[row] = s;
+        }
+    }
+}
+
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
 //
 // The layout of gemv_rd_stream_kernel (NW waves split k; lane l of wave w
@@ -1824,7 +1940,18 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     // Streaming kernel: packed 128-bit rows and k within the register budget.
     if (pl.vec == 8 && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n) {
         RdPlan sp{};
-        if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) return sp;
+        if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) {
+            // Long rows at M = 1 (2 to 4 windows per lane): 16-wave workgroups
+            // of 16 rows whose two halves share one LDS copy of x, while they
+            // still give every CU a workgroup.
+            if (p.m == 1 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 && sp.rows == 2 &&
+                p.k <= kXldsMaxK && (p.n + 15) / 16 >= cus && env_int("DMC_HIP_RD_XLDS", 1) != 0) {
+                sp.waves = 16;
+                sp.rpw = 16;
+                sp.grid_x = (p.n + 15) / 16;
+            }
+            return sp;
+        }
     }
 
     // Streaming over misaligned rows (odd K, offset views) with unaligned
@@ -2010,6 +2137,17 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
         return hipErrorInvalidValue;
     }
     if (pl.kvec > 0 && pl.vec < 8) return rd_unaligned_dispatch(p, pl, s);
+    if (pl.kvec > 0 && pl.waves == 16) {
+        if (pl.rows != 2 || pl.rpw != 16 || p.m != 1 || p.k > kXldsMaxK) return hipErrorInvalidValue;
+#define DMC_XLDS(KV)                                                                                          \
+    case KV:                                                                                                  \
+        hipLaunchKernelGGL((gemv_rd_stream_xlds_kernel<KV, 2>), dim3((unsigned)pl.grid_x), dim3(1024), 0, s, p.w, \
+                           p.x, p.y, (int)p.n, (int)p.k, pl.rpw);                                             \
+        return hipGetLastError();
+        switch (pl.kvec) { DMC_XLDS(2) DMC_XLDS(3) DMC_XLDS(4) }
+#undef DMC_XLDS
+        return hipErrorInvalidValue;
+    }
     if (pl.kvec > 0) {
         RdGroup g{};
         g.w[0] = p.w;

@@ -85,15 +85,23 @@ def test_rowdot_vector_width_follows_alignment(k, align, vec):
     assert p.vec == vec, p
 
 
-def test_rowdot_plans_at_decode_shapes():
+def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # streaming kernel: 8 waves split k = 4096 one 8-element vector per lane,
     # 4 weight rows per workgroup, 2 per step
     up = d.plan("rd", 1, 4096, 14336, x_addr=256, w_addr=256)
     assert (up.vec, up.waves, up.slices, up.rows_per_group, up.rows_or_rw, up.mt, up.grid_x) == \
         (8, 8, 1, 4, 2, 1, 3584)
-    # long rows: ceil(14336 / 4096) vectors per lane, 8 rows per workgroup
+    # long rows: ceil(14336 / 4096) vectors per lane; 16-wave workgroups of 16
+    # rows whose two 8-wave halves share one LDS copy of x (one per CU) ...
+    down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
+    assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (16, 4, 16, 256)
+    # ... or, switched off, 8-wave workgroups of 8 rows, each with x in registers
+    monkeypatch.setenv("DMC_HIP_RD_XLDS", "0")
     down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
     assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (8, 4, 8, 512)
+    monkeypatch.delenv("DMC_HIP_RD_XLDS")
+    # fewer rows than one 16-row workgroup per CU: the 8-wave layout
+    assert d.plan("rd", 1, 14336, 1024, x_addr=256, w_addr=256).waves == 8
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
     # M = 1: the streaming kernel

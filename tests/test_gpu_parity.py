@@ -735,3 +735,34 @@ def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
     for r in range(m):
         check_bound(y[r, rows], y_ref[r], x[r], wf, what=f"mfma m={m} k={k} n={n} row {r}")
     check(y[:, rows], y_ref, what=f"mfma m={m} k={k} n={n}")
+
+
+# ---- row-dot streaming with x shared through LDS (16-wave workgroups, M = 1) ----------
+
+XLDS_SHAPES = [(4096, 14336), (4109, 4104), (4100, 8192), (4096, 16384), (5000, 12288)]
+
+
+@pytest.mark.parametrize("n,k", XLDS_SHAPES)
+def test_shared_x_workgroups(hip, n, k, monkeypatch):
+    """Long rows at M = 1 on 16-wave workgroups whose halves share one LDS
+    copy of x: a partial last workgroup (its second half empty at n = 4100),
+    a last window holding one element (k = 4104), the largest K it takes."""
+    monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
+    assert hip.plan("rd", 1, k, n).waves == 16
+    x, w = case(1, k, n, seed=7000 + n + k, edge=True)
+    check(run_rd(hip, x, w), ref(x, w), what=f"xlds n={n} k={k}")
+
+
+@pytest.mark.parametrize("k", [4104, 14336])
+def test_shared_x_zero_signs(hip, k, monkeypatch):
+    """The zero-sign rule of test_underflowing_products_keep_their_zero_sign on
+    the shared-x layout: even rows end at -0.0, odd rows at +0.0."""
+    monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
+    n = 4112
+    assert hip.plan("rd", 1, k, n).waves == 16
+    x = np.full((1, k), np.float32(-1e-38), np.float32)
+    w = np.full((n, k), 0x0001, np.uint16)
+    w[1::2, :] = 0x8001
+    y_ref = ref(x, w)
+    assert np.all(np.signbit(y_ref[0, 0::2])) and not np.any(np.signbit(y_ref[0, 1::2]))
+    check(run_rd(hip, x, w), y_ref, what=f"xlds zero signs k={k}")
