@@ -12,7 +12,7 @@ same bytes (MI355X's Infinity Cache is 256 MB).
 value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
               of the K timed steps over their host wall time.
 roofline      algorithmic bytes per launch / average launch duration of the
-              row-dot streaming kernel, from HIP events on the library stream
+              row-dot streaming kernels, from HIP events on the library stream
               around the timed region (2K back-to-back launches).  Each
               duration includes the fixed cost of a dispatch, which
               `dispatch_floor_us` measures alone with empty launches (rocprof
@@ -214,7 +214,8 @@ def main(argv=None) -> int:
     roofline = {
         "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_from_profile(),
-        "kernel": "gemv_rd_stream_kernel (row-dot streaming GEMV)",
+        "kernel": "row-dot streaming GEMVs: gemv_rd_stream_kernel (up/gate), "
+                  "gemv_rd_stream_xlds_kernel (down, x shared through LDS)",
         "bytes_per_launch": {"up": b_up, "down": b_down},
         "avg_launch_us": round(launch_us, 3),
         "us_per_launch": {nm: round(u, 3) for nm, u in us.items()},
