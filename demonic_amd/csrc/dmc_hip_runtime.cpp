@@ -894,7 +894,9 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
             g.y[i] = reinterpret_cast<float *>(y_devs[b + i]);
             g.n[i] = ns[b + i];
         }
-        const dmc::RdPlan gp = dmc::plan_rd_group(g, c.cus);
+        // A group of one is a single GEMV: the single-problem plan (the
+        // shared-x and MFMA layouts included).
+        const dmc::RdPlan gp = g.count > 1 ? dmc::plan_rd_group(g, c.cus) : dmc::RdPlan{};
         if (gp.kvec > 0) {
             hipError_t e = dmc::launch_rd_group(g, gp, c.stream);
             if (e != hipSuccess) return hip_fail(e, "grouped kernel launch");
