@@ -10,7 +10,13 @@ through them, so >= 1 GiB of other weights streams between two reads of the
 same bytes (MI355X's Infinity Cache is 256 MB).
 
 value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
-              of the K timed steps over their host wall time.
+              of the K timed steps over their host wall time.  The K steps
+              (2K launches on resident inputs) are captured once into a HIP
+              graph on the library stream and the timed region is one replay
+              of it: the host stays out of the device timeline.  (Launched one
+              Python call at a time, the same kernels run 0.3-0.5 us longer
+              each on some boxes, with no gaps between them, as the host's
+              pacing leaks into the dispatches; `eager` reports that figure.)
 roofline      algorithmic bytes per launch / average launch duration of the
               row-dot streaming kernels, from HIP events on the library stream
               around the timed region (2K back-to-back launches).  Each
@@ -18,7 +24,7 @@ roofline      algorithmic bytes per launch / average launch duration of the
               `dispatch_floor_us` measures alone with empty launches (rocprof
               counts it inside a kernel's duration too).  Peak: MI355X's
               8 TB/s HBM3E.  `us_per_launch` times each shape in its own
-              back-to-back batch.
+              back-to-back batch (also a graph replay, as every batch below).
 read_ceiling  the same weights streamed by a read-only probe with the same
               128-bit nontemporal loads, timed the same way.
 cpu_baseline  the oracle's restatement of the reference CPU kernel
@@ -31,6 +37,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import gc
 import json
 import os
 import pathlib
@@ -123,16 +130,32 @@ class Rotating:
             b.free()
 
 
-def batch_us(d, fn, reps: int) -> float:
-    """Average duration of `reps` back-to-back launches, HIP events on the
-    library stream around the whole batch."""
+def batch_us(d, fn, reps: int, graph: bool = True) -> float:
+    """Average duration of `reps` back-to-back launches of fn(0), fn(1), ...,
+    HIP events on the library stream around the batch.  graph=True: the batch
+    is captured once into a HIP graph (after one untimed call that lets the
+    library size its buffers) and the replay is timed; graph=False: one host
+    call per launch."""
+    fn(0)
+    d.synchronize()
+    g = None
+    if graph:
+        with d.Graph() as g:
+            for i in range(reps):
+                fn(i)
+        g.launch()
     e0, e1 = d.Event(), d.Event()
     d.synchronize()
     e0.record()
-    for i in range(reps):
-        fn(i)
+    if g is not None:
+        g.launch()
+    else:
+        for i in range(reps):
+            fn(i)
     e1.record()
     e1.synchronize()
+    if g is not None:
+        g.destroy()
     return e0.elapsed_ms(e1) * 1e3 / reps
 
 
@@ -181,19 +204,37 @@ def main(argv=None) -> int:
             launch(name, i)
     d.synchronize()
 
-    # timed region: K steps, each the two GEMVs, inputs resident
-    e0, e1 = d.Event(), d.Event()
-    t0 = time.perf_counter()
-    e0.record()
-    for i in range(a.steps):
-        for name in order:
-            launch(name, i)
-    e1.record()
+    def steps():
+        for i in range(a.steps):
+            for name in order:
+                launch(name, i)
+
+    def timed(run):
+        e0, e1 = d.Event(), d.Event()
+        d.synchronize()
+        t0 = time.perf_counter()
+        e0.record()
+        run()
+        e1.record()
+        d.synchronize()
+        return time.perf_counter() - t0, e0.elapsed_ms(e1)
+
+    # timed region: K steps, each the two GEMVs, inputs resident, replayed
+    # from a HIP graph captured once (after one untimed replay)
+    with d.Graph() as graph:
+        steps()
+    graph.launch()
     d.synchronize()
-    wall = time.perf_counter() - t0
-    ev_ms = e0.elapsed_ms(e1)
+    wall, ev_ms = timed(graph.launch)
+    graph.destroy()
     bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
     value = bytes_step * a.steps / wall / 1e9
+    # the same K steps launched one call at a time (garbage collector paused)
+    gc.disable()
+    try:
+        eager_wall, eager_ev_ms = timed(steps)
+    finally:
+        gc.enable()
 
     # per-shape launch durations, the read ceiling and the dispatch floor
     us = {nm: batch_us(d, lambda i, nm=nm: launch(nm, i), a.steps) for nm in order}
@@ -228,6 +269,10 @@ def main(argv=None) -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall / a.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16w-f32acc",
+        "submission": "one HIP graph replay of the K timed steps (2K kernel launches)",
+        "eager": {"value": round(bytes_step * a.steps / eager_wall / 1e9, 1),
+                  "avg_launch_us": round(eager_ev_ms * 1e3 / (a.steps * len(order)), 3),
+                  "note": "the same K steps launched one Python call at a time"},
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) f32 activations (PCG64 seed 0)",
         "config": {"workload": "C2 Llama-3-8B FFN decode GEMVs, row-dot layout: up/gate W[14336,4096] "
                                "and down W[4096,14336], m=1, weights resident, cold cache "
@@ -470,8 +515,8 @@ def c3(d, W, tokens: int = 10) -> dict:
             fn()
         g.launch()
         d.synchronize()
-        ms_graph = batch_us(d, lambda i: g.launch(), tokens) / 1e3
-        ms_eager = batch_us(d, lambda i: fn(), tokens) / 1e3
+        ms_graph = batch_us(d, lambda i: g.launch(), tokens, graph=False) / 1e3
+        ms_eager = batch_us(d, lambda i: fn(), tokens, graph=False) / 1e3
         g.destroy()
         gbs = b_token / (ms_graph * 1e-3) / 1e9
         out[label] = {"launches_per_token": launches * W.LLAMA3_8B_LAYERS, "ms_per_token_graph": round(ms_graph, 4),
