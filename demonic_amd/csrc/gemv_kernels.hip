@@ -1942,10 +1942,15 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         RdPlan sp{};
         if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) {
             // Long rows at M = 1 (2 to 4 windows per lane): 16-wave workgroups
-            // of 16 rows whose two halves share one LDS copy of x, while they
-            // still give every CU a workgroup.
+            // of 16 rows whose two halves share one LDS copy of x.  One fills
+            // a CU, so only when they come in whole rounds of one per CU (or
+            // enough rounds that a partial last one costs little): C5's
+            // N = 4097 would leave a 257th workgroup to start after the others
+            // (17.3 us against 15.7 on 8-wave workgroups).
+            const int64_t g16 = (p.n + 15) / 16;
             if (p.m == 1 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 && sp.rows == 2 &&
-                p.k <= kXldsMaxK && (p.n + 15) / 16 >= cus && env_int("DMC_HIP_RD_XLDS", 1) != 0) {
+                p.k <= kXldsMaxK && g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus) &&
+                env_int("DMC_HIP_RD_XLDS", 1) != 0) {
                 sp.waves = 16;
                 sp.rpw = 16;
                 sp.grid_x = (p.n + 15) / 16;

@@ -100,8 +100,12 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
     assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (8, 4, 8, 512)
     monkeypatch.delenv("DMC_HIP_RD_XLDS")
-    # fewer rows than one 16-row workgroup per CU: the 8-wave layout
+    # fewer rows than one 16-row workgroup per CU, or a partial last round of
+    # them (one 16-wave workgroup fills a CU): the 8-wave layout
     assert d.plan("rd", 1, 14336, 1024, x_addr=256, w_addr=256).waves == 8
+    assert d.plan("rd", 1, 11008, 4097, x_addr=256, w_addr=256).waves == 8
+    assert d.plan("rd", 1, 8192, 8192, x_addr=256, w_addr=256).waves == 16      # two whole rounds
+    assert d.plan("rd", 1, 8192, 28672, x_addr=256, w_addr=256).waves == 16     # seven
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
     # M = 1: the streaming kernel

@@ -739,14 +739,15 @@ def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
 
 # ---- row-dot streaming with x shared through LDS (16-wave workgroups, M = 1) ----------
 
-XLDS_SHAPES = [(4096, 14336), (4109, 4104), (4100, 8192), (4096, 16384), (5000, 12288)]
+XLDS_SHAPES = [(4096, 14336), (4096, 4104), (8192, 8192), (4096, 16384), (16380, 12288)]
 
 
 @pytest.mark.parametrize("n,k", XLDS_SHAPES)
 def test_shared_x_workgroups(hip, n, k, monkeypatch):
     """Long rows at M = 1 on 16-wave workgroups whose halves share one LDS
-    copy of x: a partial last workgroup (its second half empty at n = 4100),
-    a last window holding one element (k = 4104), the largest K it takes."""
+    copy of x: a last window holding one element (k = 4104), the largest K it
+    takes, two rounds (n = 8192), and a partial last workgroup whose second
+    half holds 4 rows (n = 16380, four rounds)."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
     assert hip.plan("rd", 1, k, n).waves == 16
     x, w = case(1, k, n, seed=7000 + n + k, edge=True)
@@ -758,7 +759,7 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     """The zero-sign rule of test_underflowing_products_keep_their_zero_sign on
     the shared-x layout: even rows end at -0.0, odd rows at +0.0."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
-    n = 4112
+    n = 4096
     assert hip.plan("rd", 1, k, n).waves == 16
     x = np.full((1, k), np.float32(-1e-38), np.float32)
     w = np.full((n, k), 0x0001, np.uint16)
