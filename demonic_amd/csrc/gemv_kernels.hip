@@ -341,16 +341,23 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
     const int hrows = rpw / 2;
     const int rb = (int)blockIdx.x * rpw + half * hrows;  // this half's rows: [rb, rb + nr)
     const int nr = max(0, min(N, rb + hrows) - rb);
+    // x in LDS as two planes: window w's first 4 elements at lo[4w], its last
+    // 4 at hi[4w], so a wave reading one half of 64 consecutive windows (and
+    // writing them) touches 1 KiB of consecutive bytes: no bank conflicts
+    // (windows read whole at a 32-byte stride conflicted on 29% of the LDS
+    // cycles, rocprof SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE).
     __shared__ __attribute__((aligned(16))) float xs[kXldsMaxK];
+    constexpr int kHi = kXldsMaxK / 2;
     __shared__ float red[2][NW][kMaxRpw / 2];
 
-    // x into registers as 16-byte pieces t, t + 1024, ... (pieces past K read
-    // as zeros from past the resource's range).
+    // x into registers: thread t takes windows t and t + 1024, each whole
+    // (two 16-byte loads; windows past K read as zeros from past the
+    // resource's range).
     const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4);
     u32x4 xp[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + i * 1024u) * 16u, 0, 0);
+        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + (i >> 1) * 1024u) * 32u + (i & 1) * 16u, 0, 0);
 
     uint32_t eoff[KV];
     bool has[KV];
@@ -376,7 +383,8 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);  // both weight buffers in flight before the wait for x
 #pragma unroll
-    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4 *>(&xs[(threadIdx.x + i * 1024) * 4]) = xp[i];
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<u32x4 *>(&xs[(i & 1) * kHi + (threadIdx.x + (i >> 1) * 1024u) * 4u]) = xp[i];
     __syncthreads();
     // The lane's windows; a window past K (zeros in LDS) gets x = -0.0f, so
     // its products with the +0 weights read past the range are -0.0f, the
@@ -384,9 +392,9 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
     float xr[KV][8];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
-        const int e = ((j * NW + wave) * 64 + lane) * 8;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[e]);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[e + 4]);
+        const int w = (j * NW + wave) * 64 + lane;
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
         const uint32_t sgn = has[j] ? 0u : 0x80000000u;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
