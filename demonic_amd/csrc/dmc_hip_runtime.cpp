@@ -446,7 +446,9 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if (rd || cs_as_rd) {
         dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
                          ydst, n, m, k, n, dmc::kWeightSlack};
-        e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+        const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
+        if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
+        e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
     } else {
         dmc::CsProblem p{static_cast<const uint16_t *>(dw), static_cast<const float *>(c.dx.p),
                          ydst, m, k, n, batch, ls, rs};
@@ -852,7 +854,9 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
     Ctx &c = ctx();
     dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_dev), k, reinterpret_cast<const float *>(x_dev),
                      k, reinterpret_cast<float *>(y_dev), n, m, k, n};
-    hipError_t e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+    const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
+    if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
+    hipError_t e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DMC_HIP_OK;
 }
@@ -905,7 +909,9 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
         for (int i = 0; i < g.count; ++i) {  // outside the streaming kernel's range: one launch each
             if (g.n[i] == 0) continue;
             dmc::RdProblem p{g.w[i], k, g.x[i], k, g.y[i], g.n[i], m, k, g.n[i]};
-            hipError_t e = dmc::launch_rd(p, dmc::plan_rd(p, c.cus), c.stream);
+            const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
+            if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
+            hipError_t e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
             if (e != hipSuccess) return hip_fail(e, "kernel launch");
         }
     }
@@ -1024,8 +1030,8 @@ int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t 
         dmc::RdProblem p{reinterpret_cast<const uint16_t *>(w_addr), k, reinterpret_cast<const float *>(x_addr),
                          k, nullptr, n, m, k, n};
         const dmc::RdPlan pl = dmc::plan_rd(p, cus);
-        const int64_t v[8] = {pl.vec, pl.rows, pl.mt, pl.grid_x, pl.mfma ? -pl.mkind : pl.kvec, 0, pl.waves,
-                              pl.rpw};
+        const int64_t v[8] = {pl.vec, pl.rows, pl.mt, pl.grid_x, pl.mfma ? -pl.mkind : pl.kvec,
+                              (int64_t)pl.workspace_bytes, pl.waves, pl.rpw};
         memcpy(out8, v, sizeof v);
     } else {
         dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_addr), reinterpret_cast<const float *>(x_addr),

@@ -865,6 +865,201 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
             if (live[t][r]) Y[(int64_t)(m0 + i16) * N + row0 + base[t] + g * 4 + r] = acc[t][r];
 }
 
+// Sixth MFMA layout ("gemm"), for prefill-sized M (> 16): the wide layout
+// with MB tiles of 16 activation rows per workgroup instead of one.  Every
+// weight tile a wave stages in LDS meets all 16 * MB activation rows, so W
+// streams from HBM once per 16 * MB rows (the 16-row layouts stream it once
+// per 16).  x arrives already split: split_x_planes_kernel writes its three
+// bf16 terms once per call as planes [3][M][K], and each chunk's operands are
+// copied into LDS (no per-workgroup split).  When 256-row by 16*MB-row tiles
+// would leave the device short of workgroups, k is split over `slices`
+// workgroups (grid z), each covering kc chunks of 64, whose partial sums go
+// to P[slice][m][n] for gemm_sum_slices_kernel.  Numerics, special values and
+// the zero rule are the wide layout's, tile by tile; with slices the zero
+// rule runs after the sum.
+template <int MB>
+__global__ void __launch_bounds__(512)
+gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, const uint16_t *__restrict__ XS,
+                         float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc) {
+    static_assert(MB >= 1 && MB <= 4, "x staging covers at most 512 threads");
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i16 = lane & 15;
+    const int g = lane >> 4;
+    const int row0 = blockIdx.x * kWideRows;
+    const int nrows = min(kWideRows, N - row0);
+    const int m0 = blockIdx.y * 16 * MB;
+    const int c0 = blockIdx.z * kc;                      // this slice's chunks: [c0, c1)
+    const int c1 = min(K / 64, c0 + kc);
+    const int nchunks = max(0, c1 - c0);
+
+    __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 36 KiB
+    __shared__ u32x4 xpl[2][MB][2][3][64];                                       // MB x 12 KiB
+    uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
+
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
+    // Staging: load j (0..3) covers the wave's rows 8j + lane/8, bytes 16*(lane%8) of the chunk.
+    const int scol = (lane & 7) * 16;
+    const int slr = lane >> 3;
+    uint32_t soff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        soff[j] = (uint32_t)min(wave * 32 + slr + 8 * j, nrows - 1) * (uint32_t)K * 2u + scol;
+    // x items: threads 0 .. 128*MB-1 = (tile xt = tid/128, k-block b = tid/64 % 2,
+    // operand lane): the lane's 8 elements of each of the three planes.
+    const bool xthread = tid < 128 * MB;
+    const int xt = tid >> 7;
+    const int xb = (tid >> 6) & 1;
+    const int xm = m0 + xt * 16 + (lane & 15);
+    const bool xlive = xthread && xm < M;
+    const int64_t plane = (int64_t)M * K;
+    const uint16_t *xp = XS + (int64_t)min(xm, M - 1) * K + xb * 32 + (lane >> 4) * 8;
+
+    struct Regs {
+        u32x4 w[4];
+        u32x4 x[3];
+    };
+    auto load = [&](int c, Regs &r) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + (uint32_t)(c0 + c) * 128u);
+#pragma unroll
+        for (int q = 0; q < 3; ++q)
+            r.x[q] = xlive ? *reinterpret_cast<const u32x4 *>(xp + q * plane + (int64_t)(c0 + c) * 64)
+                           : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto store = [&](const Regs &r, int xbuf) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
+        if (xthread) {
+#pragma unroll
+            for (int q = 0; q < 3; ++q) xpl[xbuf][xt][xb][q][lane] = r.x[q];
+        }
+    };
+
+    f32x4 acc[MB][2];
+#pragma unroll
+    for (int mt = 0; mt < MB; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    auto compute = [&](int xbuf) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            u32x4 a[2], a2[2];
+            uint32_t mx = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
+            }
+            const bool any_special = wave_has_inf_nan(mx);
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                a2[t] = a[t];
+                if (any_special) {
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) a2[t][v] &= ~inf_nan_mask(a2[t][v]);
+                }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MB; ++mt) {
+                const u32x4 hi = xpl[xbuf][mt][b][0][lane], md = xpl[xbuf][mt][b][1][lane],
+                            lo = xpl[xbuf][mt][b][2][lane];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    acc[mt][t] = mfma_bf16(a[t], hi, acc[mt][t]);
+                    acc[mt][t] = mfma_bf16(a2[t], md, acc[mt][t]);
+                    acc[mt][t] = mfma_bf16(a2[t], lo, acc[mt][t]);
+                }
+            }
+        }
+    };
+
+    // Chunk c is in LDS (x planes in buffer c&1); chunk c+1 waits in one
+    // register set and chunk c+2 loads into the other.
+    Regs ra, rb;
+    if (nchunks > 0) load(0, ra);
+    if (nchunks > 1) load(1, rb);
+    if (nchunks > 0) store(ra, 0);
+    __syncthreads();
+    auto step = [&](int c, Regs &rnext, Regs &rfree) {
+        if (c + 2 < nchunks) load(c + 2, rfree);
+        compute(c & 1);
+        if (c + 1 < nchunks) store(rnext, (c + 1) & 1);
+        __syncthreads();
+    };
+    for (int c = 0; c < nchunks; c += 2) {
+        step(c, rb, ra);
+        if (c + 1 >= nchunks) break;
+        step(c + 1, ra, rb);
+    }
+
+    const int base[2] = {wave * 32, wave * 32 + 16};
+#pragma unroll
+    for (int mt = 0; mt < MB; ++mt) {
+        const int m = m0 + mt * 16 + i16;
+        bool live[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) live[t][r] = m < M && base[t] + g * 4 + r < nrows;
+        if (P) {  // a k slice: the partial sums, for gemm_sum_slices_kernel
+            float *ps = P + (int64_t)blockIdx.z * M * N + (int64_t)m * N + row0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (live[t][r]) ps[base[t] + g * 4 + r] = acc[mt][t][r];
+            continue;
+        }
+        settle_zeros(acc[mt], live, base, W + (int64_t)row0 * K, X + (int64_t)(m0 + mt * 16) * K, K, i16);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (live[t][r]) Y[(int64_t)m * N + row0 + base[t] + g * 4 + r] = acc[mt][t][r];
+    }
+}
+
+// x [M,K] f32 -> its three bf16 terms as planes XS[q][M][K] (split3 of each
+// element), for the gemm layout.  count = M*K, a multiple of 8; 16-byte
+// aligned.  Grid-stride.
+__global__ void __launch_bounds__(256)
+split_x_planes_kernel(const float *__restrict__ X, uint16_t *__restrict__ XS, int64_t count) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count / 8; i += (int64_t)gridDim.x * 256) {
+        const float4 a = reinterpret_cast<const float4 *>(X)[2 * i];
+        const float4 b = reinterpret_cast<const float4 *>(X)[2 * i + 1];
+        const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        u32x4 hi, md, lo;
+        split8(v, hi, md, lo);
+        reinterpret_cast<u32x4 *>(XS)[i] = hi;
+        reinterpret_cast<u32x4 *>(XS + count)[i] = md;
+        reinterpret_cast<u32x4 *>(XS + 2 * count)[i] = lo;
+    }
+}
+
+// y[m][n] = P[0][m][n] + P[1][m][n] + ... in slice order, then the zero rule
+// of settle_zeros for one output: an exact zero is +0 when the activation row
+// or the weight row holds only +-0, else the reference chain's value.
+__global__ void __launch_bounds__(256)
+gemm_sum_slices_kernel(const float *__restrict__ P, int slices, float *__restrict__ Y, const uint16_t *__restrict__ W,
+                       const float *__restrict__ X, int M, int N, int K) {
+    const int64_t count = (int64_t)M * N;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+        float s = P[i];
+        for (int j = 1; j < slices; ++j) s += P[j * count + i];
+        if (s == 0.0f) {
+            const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
+            const uint32_t *xr = reinterpret_cast<const uint32_t *>(X + (int64_t)m * K);
+            const uint32_t *wr = reinterpret_cast<const uint32_t *>(W + (int64_t)n * K);
+            uint32_t xo = 0, wo = 0;
+            for (int k = 0; k < K; ++k) xo |= xr[k] & 0x7fffffffu;
+            for (int k = 0; k < K / 2; ++k) wo |= wr[k] & 0x7fff7fffu;
+            s = (xo && wo) ? reference_chain(W + (int64_t)n * K, X + (int64_t)m * K, K) : 0.0f;
+        }
+        Y[i] = s;
+    }
+}
+
 // Fifth MFMA layout ("rows16"), for a few activation rows: 16 weight rows per
 // workgroup, read whole.  The rows advance in windows of 8 lines (1 KiB per
 // row); wave w owns line w of every window, 64 k elements = two MFMA k-blocks.
@@ -1930,10 +2125,30 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         const int64_t gy = (p.m + 15) / 16;
         const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus &&
                                (int64_t)kWideRows * p.k * 2 <= INT32_MAX;
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 8 && wide_fits ? 6 : 7);
-        mp.mkind = kind == 6 && (int64_t)kWideRows * p.k * 2 <= INT32_MAX ? 6 : 7;  // 256-row buffer range
+        // Above 16 activation rows, the gemm layout (16 * MB rows per
+        // workgroup: W streams once per 32 or 64 rows instead of per 16); from
+        // 9 rows too where the wide layout does not fill the device (C2 up and
+        // down at m = 12 and 16: 34-38 us against 41-44 on rows16; at m = 8
+        // rows16 wins, 27-31 against 31-33).
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 16 ? 8 : p.m > 8 ? (wide_fits ? 6 : 8) : 7);
+        const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
+        mp.mkind = (kind == 6 || kind == 8) && rows256_fit ? kind : 7;
         mp.waves = 8;
-        if (mp.mkind == 6) {
+        if (mp.mkind == 8) {
+            mp.rpw = kWideRows;
+            mp.mt = p.m <= 32 ? 32 : 64;
+            // Split k until the grid holds ~2 workgroups per CU (one 512-thread
+            // gemm workgroup of ~84 KiB LDS fills a CU): kchunks chunks of 64 per slice.
+            const int64_t tiles = ((p.n + kWideRows - 1) / kWideRows) * ((p.m + mp.mt - 1) / mp.mt);
+            const int64_t nchunks = p.k / 64;
+            int64_t want = std::max<int64_t>(1, (2 * cus + tiles - 1) / tiles);
+            want = std::min<int64_t>({want, nchunks, (int64_t)env_int("DMC_HIP_GEMM_MAX_SLICES", 64)});
+            want = std::max<int64_t>(want, 1);
+            mp.kchunks = (int)((nchunks + want - 1) / want);
+            mp.kslices = (int)((nchunks + mp.kchunks - 1) / mp.kchunks);
+            const size_t planes = ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
+            mp.workspace_bytes = planes + (mp.kslices > 1 ? (size_t)mp.kslices * p.m * p.n * 4 : 0);
+        } else if (mp.mkind == 6) {
             mp.rpw = kWideRows;
         } else {
             // rows16: T 16-row blocks per workgroup, gridDim.x apart, while
@@ -2134,13 +2349,37 @@ hipError_t launch_rd_group(const RdGroup &g, const RdPlan &pl, hipStream_t s) {
     return rs_dispatch(ga, g, pl, s);
 }
 
-hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, hipStream_t s) {
+unsigned stride_grid(int64_t work_items);
+
+hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipStream_t s) {
     if (p.m <= 0 || p.n <= 0) return hipSuccess;
     if (pl.mfma) {
         const dim3 grid((unsigned)pl.grid_x, (unsigned)pl.grid_y);
         if (pl.mkind == 6) {
             hipLaunchKernelGGL(gemv_rd_mfma_wide_kernel, grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n, (int)p.k,
                                (int)p.m);
+            return hipGetLastError();
+        }
+        if (pl.mkind == 8) {
+            if (!workspace || (pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 || pl.kslices > 65535 ||
+                (int64_t)pl.kslices * pl.kchunks < p.k / 64)
+                return hipErrorInvalidValue;
+            uint16_t *xs = static_cast<uint16_t *>(workspace);
+            const size_t planes = ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
+            float *part = pl.kslices > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + planes) : nullptr;
+            const int64_t count = p.m * p.k;
+            hipLaunchKernelGGL(split_x_planes_kernel, dim3(stride_grid((count / 8 + 255) / 256)), dim3(256), 0, s,
+                               p.x, xs, count);
+            const dim3 g3((unsigned)pl.grid_x, (unsigned)pl.grid_y, (unsigned)pl.kslices);
+            if (pl.mt == 32)
+                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<2>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
+                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
+            else
+                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<4>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
+                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
+            if (pl.kslices > 1)
+                hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,
+                                   s, part, pl.kslices, p.y, p.w, p.x, (int)p.m, (int)p.n, (int)p.k);
             return hipGetLastError();
         }
         if (pl.mkind == 7) {

@@ -65,6 +65,10 @@ struct RdPlan {
     int kvec;   // 8-element vectors of k per lane (streaming), 0 = general kernel
     int rpw;    // weight rows per workgroup
     int64_t grid_x, grid_y;
+    // gemm layout (mkind 8): k split over `kslices` workgroups of `kchunks`
+    // 64-element chunks each; workspace for x's bf16 planes and the partials
+    int kslices = 1, kchunks = 0;
+    size_t workspace_bytes = 0;
 };
 
 // Two column-stream kernels:
@@ -109,9 +113,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus);
 RdPlan plan_rd_group(const RdGroup &g, int num_cus);
 CsPlan plan_cs(const CsProblem &p, int num_cus);
 
-// Enqueue on `stream`.  `workspace` must hold plan.workspace_bytes when
-// plan.slices > 1.  Returns hipSuccess or the launch error.
-hipError_t launch_rd(const RdProblem &p, const RdPlan &plan, hipStream_t stream);
+// Enqueue on `stream`.  `workspace` must hold plan.workspace_bytes (row-dot:
+// the gemm layout's x planes and partial sums; column-stream: the partial sums
+// when plan.slices > 1).  Returns hipSuccess or the launch error.
+hipError_t launch_rd(const RdProblem &p, const RdPlan &plan, void *workspace, hipStream_t stream);
 hipError_t launch_rd_group(const RdGroup &g, const RdPlan &plan, hipStream_t stream);
 
 hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hipStream_t stream);

@@ -189,8 +189,9 @@ int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, i
 
 /* HIP graphs of the library stream.  Between capture_begin and capture_end,
  * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
- * split-K workspace is already large enough, i.e. after one uncaptured call of
- * the same shape) are recorded instead of run; capture_end returns an
+ * workspace -- column-stream split-K partials, or x's bf16 planes and partial
+ * sums for row-dot with m > 8 -- is already large enough, i.e. after one
+ * uncaptured call of the same shape) are recorded instead of run; capture_end returns an
  * executable graph (0 on error: an entry that allocates or waits was called
  * while capturing) that graph_launch replays on the library stream.  The
  * MI355X form of the reference's pipelined command buffers (gpu.rs:206-219,

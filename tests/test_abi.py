@@ -120,9 +120,13 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     for m in (5, 8):  # two 16-row blocks per workgroup
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
-    for m in (9, 16, 17):
+    for m in (9, 16):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
+    # prefill-sized M: the gemm layout, 32 or 64 activation rows per workgroup
+    for m, mt in ((17, 32), (32, 32), (33, 64), (512, 64)):
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 501), p
     # k not a multiple of 64: back to the streaming kernel, activation rows held in
     # registers (MT * vectors-per-lane <= 8)
     assert d.plan("rd", 16, 4104, 1000, x_addr=256, w_addr=256).slices > 0
@@ -142,13 +146,26 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
 
 def test_rowdot_mfma_layouts(monkeypatch):
     # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
-    for m, mt, rpw in [(2, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32), (9, 16, 16), (16, 16, 16), (20, 16, 16)]:
+    for m, mt, rpw in [(2, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32)]:
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
+    # from 9 activation rows where the wide layout does not fit, and above 16
+    # whatever N, the gemm layout (32 activation rows per workgroup up to 32)
+    for m in (9, 16, 20):
+        p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 256, 8, 65), (m, p)
     # blocks per workgroup shrink while the grid would fall under 2 per CU
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
+    # the gemm layout splits k until the grid holds 2 workgroups per CU: C2 up
+    # at m = 64 has 56 tiles of 256 x 64, so 10 slices of 7 chunks; its
+    # workspace holds x's three bf16 planes and the 10 partial sums
+    p = d.plan("rd", 64, 4096, 14336, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.grid_x) == (-8, 64, 56), p
+    assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 10 * 64 * 14336 * 4, p
+    p = d.plan("rd", 512, 4096, 128256, x_addr=256, w_addr=256)   # 4008 tiles: no split
+    assert p.workspace_bytes == 3 * 512 * 4096 * 2, p
     monkeypatch.setenv("DMC_HIP_RD_R16_TILES", "4")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
     assert p.slices == -6, p  # tiles only shape the rows16 layout
@@ -162,6 +179,9 @@ def test_rowdot_mfma_layouts(monkeypatch):
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "6")
     p = d.plan("rd", 16, 4096, 1000, x_addr=256, w_addr=256)
     assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")
+    p = d.plan("rd", 4, 4096, 1000, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-8, 32, 256, 4), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "0")  # disabled: the FMA kernels
     assert d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256).slices > 0
 

@@ -99,7 +99,7 @@ def test_denormals_survive_and_inf_times_tiny_is_inf(hip):
         assert y2[2] == np.float32(k) * W.bf16_to_f32(np.array([1], np.uint16))[0], y2
 
 
-@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("kind", [6, 7, 8])
 @pytest.mark.parametrize("m,k", [(2, 64), (3, 320), (4, 4096), (8, 1024), (16, 64)])
 def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind, monkeypatch):
     """As the M = 1 case above, through each MFMA layout: weight row 0's
@@ -118,7 +118,7 @@ def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind,
     check(y, y_ref, what=f"mfma underflow signs m={m} k={k} kind={kind}")
 
 
-@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("kind", [6, 7, 8])
 def test_skinny_mfma_zero_outputs_follow_the_reference_chain(hip, kind, monkeypatch):
     """An MFMA output that comes out exactly zero is settled by the reference's
     own chain, so even the order-dependent zeros match bit for bit: rows whose
@@ -686,7 +686,7 @@ def test_c3_layer_schedule(hip):
 
 # ---- skinny M on MFMA: special values through the three-term split ---------------------
 
-@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("kind", [6, 7, 8])
 @pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 16, 20])
 def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     """The MFMA path (M >= 2) against the reference chain on data full of
@@ -717,7 +717,7 @@ def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     assert np.all(y[:, 12][np.isfinite(y_ref[:, 12])] == 0)
 
 
-@pytest.mark.parametrize("kind", [6, 7])
+@pytest.mark.parametrize("kind", [6, 7, 8])
 @pytest.mark.parametrize("m,k,n", [(4, 4096, 16387), (16, 14336, 4096), (8, 64, 70), (5, 11008, 1000),
                                    (16, 4096, 40000), (3, 320, 300), (2, 4096, 16387), (2, 64, 70),
                                    (4, 14336, 1001), (7, 576, 33), (12, 128, 17)])
@@ -767,3 +767,26 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     y_ref = ref(x, w)
     assert np.all(np.signbit(y_ref[0, 0::2])) and not np.any(np.signbit(y_ref[0, 1::2]))
     check(run_rd(hip, x, w), y_ref, what=f"xlds zero signs k={k}")
+
+
+# ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
+
+@pytest.mark.parametrize("m,k,n", [(17, 4096, 1000), (32, 64, 300), (33, 576, 257), (64, 4096, 513),
+                                   (65, 1024, 700), (100, 14336, 260), (128, 4096, 4096), (200, 128, 17)])
+def test_prefill_gemm_within_bound(hip, m, k, n):
+    """M > 16 runs the gemm layout by default: 32 or 64 activation rows per
+    workgroup, partial activation tiles (m = 17, 33, 65, 100, 200), partial
+    256-row weight blocks, K from one chunk to 224; edge data (subnormals,
+    +-0, +-1e-38, inf/NaN weights).  Every element within the rigorous bound,
+    non-finite classes and exact zeros as the reference."""
+    x, w = case(m, k, n, seed=9000 + m + k + n, edge=True)
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert (p.slices, p.mt) == (-8, 32 if m <= 32 else 64), p
+    y = run_rd(hip, x, w)
+    rows = np.unique(np.r_[0, n - 1, np.random.default_rng(m).integers(0, n, 160)])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    check(y[:, rows], y_ref, what=f"gemm m={m} k={k} n={n}")
+    wf = W.bf16_to_f32(w[rows])
+    fin = np.all(np.isfinite(wf), axis=1)
+    for r in range(0, m, 7):
+        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm m={m} k={k} n={n} row {r}")
