@@ -790,3 +790,24 @@ def test_prefill_gemm_within_bound(hip, m, k, n):
     fin = np.all(np.isfinite(wf), axis=1)
     for r in range(0, m, 7):
         check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm m={m} k={k} n={n} row {r}")
+
+
+@pytest.mark.parametrize("m,k,n", [(17, 4096, 1000), (64, 576, 513), (100, 1024, 260)])
+def test_prefill_gemm_unsplit(hip, m, k, n, monkeypatch):
+    """The gemm layout with k in one slice (DMC_HIP_GEMM_MAX_SLICES=1: what it
+    runs when the tiles alone fill the device, as on the LM head), where the
+    zero rule runs inside the kernel: edge data, an all-zero weight row, and
+    rows whose underflowing products end at -0.0 and +0.0."""
+    monkeypatch.setenv("DMC_HIP_GEMM_MAX_SLICES", "1")
+    x, w = case(m, k, n, seed=9500 + m + k + n, edge=True)
+    w[3] = 0
+    w[5] = 0x0001
+    w[6] = 0x8001
+    x[1] = np.float32(-1e-38)
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert p.slices == -8 and p.workspace_bytes == 3 * m * k * 2, p
+    y = run_rd(hip, x, w)
+    y_ref = ref(x, w)
+    check(y, y_ref, what=f"gemm unsplit m={m} k={k} n={n}")
+    assert np.signbit(y_ref[1, 5]) and np.signbit(y[1, 5]) and y[1, 5] == 0
+    assert not np.signbit(y[1, 6]) and y[1, 6] == 0
