@@ -2137,11 +2137,13 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         if (mp.mkind == 8) {
             mp.rpw = kWideRows;
             mp.mt = p.m <= 32 ? 32 : 64;
-            // Split k until the grid holds ~2 workgroups per CU (one 512-thread
-            // gemm workgroup of ~84 KiB LDS fills a CU): kchunks chunks of 64 per slice.
+            // Split k until the grid holds up to 2 workgroups per CU, whole
+            // rounds only (one 512-thread gemm workgroup of ~84 KiB LDS fills
+            // a CU, so a 2.2-round grid runs 3 rounds): kchunks chunks of 64
+            // per slice.
             const int64_t tiles = ((p.n + kWideRows - 1) / kWideRows) * ((p.m + mp.mt - 1) / mp.mt);
             const int64_t nchunks = p.k / 64;
-            int64_t want = std::max<int64_t>(1, (2 * cus + tiles - 1) / tiles);
+            int64_t want = std::max<int64_t>(1, 2 * cus / tiles);
             want = std::min<int64_t>({want, nchunks, (int64_t)env_int("DMC_HIP_GEMM_MAX_SLICES", 64)});
             want = std::max<int64_t>(want, 1);
             mp.kchunks = (int)((nchunks + want - 1) / want);

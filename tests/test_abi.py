@@ -158,12 +158,12 @@ def test_rowdot_mfma_layouts(monkeypatch):
     # blocks per workgroup shrink while the grid would fall under 2 per CU
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
-    # the gemm layout splits k until the grid holds 2 workgroups per CU: C2 up
-    # at m = 64 has 56 tiles of 256 x 64, so 10 slices of 7 chunks; its
-    # workspace holds x's three bf16 planes and the 10 partial sums
+    # the gemm layout splits k while the grid stays within 2 workgroups per CU:
+    # C2 up at m = 64 has 56 tiles of 256 x 64, so at most 9 slices: 8 of 8
+    # chunks; its workspace holds x's three bf16 planes and the 8 partial sums
     p = d.plan("rd", 64, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.grid_x) == (-8, 64, 56), p
-    assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 10 * 64 * 14336 * 4, p
+    assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 8 * 64 * 14336 * 4, p
     p = d.plan("rd", 512, 4096, 128256, x_addr=256, w_addr=256)   # 4008 tiles: no split
     assert p.workspace_bytes == 3 * 512 * 4096 * 2, p
     monkeypatch.setenv("DMC_HIP_RD_R16_TILES", "4")
