@@ -363,6 +363,19 @@ def extended(d, W, reps: int) -> dict:
             f(0)
             record(f"C2 rd {name} m={m}", batch_us(d, f, 50), n, k, m)
             s.free()
+    # prefill-sized M on C2's shapes (the gemm layout): TFLOP/s of x.W products
+    for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
+        n, k = w.shape
+        for m in (64, 512):
+            x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+            s = Rotating(d, w, x, 3, n_out=n)
+            f = lambda i: d.gemv_rd(s.x, s.w[i % 3], s.y, m, k, n)  # noqa: E731
+            us = batch_us(d, f, 10)
+            tfs = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            out[f"C2 rd {name} prefill m={m}"] = {"us": round(us, 3), "TFLOP/s": round(tfs, 1),
+                                                  "GB/s": round(b_alg(n, k, m) / (us * 1e-6) / 1e9, 1)}
+            log(f"C2 rd {name} prefill m={m}: {us:.1f} us  {tfs:.1f} TFLOP/s")
+            s.free()
     out.update(helpers(d, c2["up"][0]))
     out.update(ingress(d, c2["down"][0]))
     return out
