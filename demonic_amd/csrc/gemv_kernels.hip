@@ -2136,11 +2136,13 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.waves = 8;
         if (mp.mkind == 8) {
             mp.rpw = kWideRows;
-            mp.mt = p.m <= 32 ? 32 : 64;
-            // Split k until the grid holds up to 2 workgroups per CU, whole
-            // rounds only (one 512-thread gemm workgroup of ~84 KiB LDS fills
-            // a CU, so a 2.2-round grid runs 3 rounds): kchunks chunks of 64
-            // per slice.
+            // 32 activation rows per workgroup (60 KiB of LDS: two workgroups
+            // per CU) up to m = 128, 64 above (C2 shapes, m = 64: 58-63 us
+            // against 67-71; m = 512: 300 against 340-388).
+            mp.mt = env_int("DMC_HIP_GEMM_MT", p.m <= 128 ? 32 : 64) == 32 ? 32 : 64;
+            // Split k while the grid holds up to 2 workgroups per CU, whole
+            // rounds only (a 2.2-round grid runs 3 rounds): kchunks chunks of
+            // 64 per slice.
             const int64_t tiles = ((p.n + kWideRows - 1) / kWideRows) * ((p.m + mp.mt - 1) / mp.mt);
             const int64_t nchunks = p.k / 64;
             int64_t want = std::max<int64_t>(1, 2 * cus / tiles);
