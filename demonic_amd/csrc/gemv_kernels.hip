@@ -2136,10 +2136,13 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.waves = 8;
         if (mp.mkind == 8) {
             mp.rpw = kWideRows;
-            // 32 activation rows per workgroup (60 KiB of LDS: two workgroups
-            // per CU) up to m = 128, 64 above (C2 shapes, m = 64: 58-63 us
-            // against 67-71; m = 512: 300 against 340-388).
-            mp.mt = env_int("DMC_HIP_GEMM_MT", p.m <= 128 ? 32 : 64) == 32 ? 32 : 64;
+            // 16 activation rows per workgroup up to m = 16 (no half-empty
+            // MFMA tiles: C1 at m = 12 / 16, 20.0 / 21.3 us against 20.5 /
+            // 22.5 with 32-row tiles, C2 within 0.5 us), 32 (60 KiB of LDS:
+            // two workgroups per CU) up to m = 128, 64 above (C2 shapes, m =
+            // 64: 58-63 us against 67-71; m = 512: 300 against 340-388).
+            const int gmt = env_int("DMC_HIP_GEMM_MT", p.m <= 16 ? 16 : p.m <= 128 ? 32 : 64);
+            mp.mt = gmt == 16 ? 16 : gmt == 32 ? 32 : 64;
             // Split k while the grid holds up to 2 workgroups per CU, whole
             // rounds only (a 2.2-round grid runs 3 rounds): kchunks chunks of
             // 64 per slice.
@@ -2365,7 +2368,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             return hipGetLastError();
         }
         if (pl.mkind == 8) {
-            if (!workspace || (pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 || pl.kslices > 65535 ||
+            if (!workspace || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 || pl.kslices > 65535 ||
                 (int64_t)pl.kslices * pl.kchunks < p.k / 64)
                 return hipErrorInvalidValue;
             uint16_t *xs = static_cast<uint16_t *>(workspace);
@@ -2375,7 +2378,10 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             hipLaunchKernelGGL(split_x_planes_kernel, dim3(stride_grid((count / 8 + 255) / 256)), dim3(256), 0, s,
                                p.x, xs, count);
             const dim3 g3((unsigned)pl.grid_x, (unsigned)pl.grid_y, (unsigned)pl.kslices);
-            if (pl.mt == 32)
+            if (pl.mt == 16)
+                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<1>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
+                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
+            else if (pl.mt == 32)
                 hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<2>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
                                    (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
             else

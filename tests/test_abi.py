@@ -151,10 +151,10 @@ def test_rowdot_mfma_layouts(monkeypatch):
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
     # from 9 activation rows where the wide layout does not fit, and above 16
-    # whatever N, the gemm layout (32 activation rows per workgroup up to 32)
-    for m in (9, 16, 20):
+    # whatever N, the gemm layout (16 activation rows per workgroup up to 16, 32 up to 128)
+    for m, mt in ((9, 16), (16, 16), (20, 32)):
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 256, 8, 65), (m, p)
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 65), (m, p)
     # blocks per workgroup shrink while the grid would fall under 2 per CU
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
@@ -181,7 +181,11 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")
     p = d.plan("rd", 4, 4096, 1000, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-8, 16, 256, 4), p
+    monkeypatch.setenv("DMC_HIP_GEMM_MT", "32")
+    p = d.plan("rd", 4, 4096, 1000, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-8, 32, 256, 4), p
+    monkeypatch.delenv("DMC_HIP_GEMM_MT")
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "0")  # disabled: the FMA kernels
     assert d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256).slices > 0
 

@@ -771,18 +771,20 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
 
 # ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
 
-@pytest.mark.parametrize("m,k,n", [(17, 4096, 1000), (32, 64, 300), (33, 576, 257), (64, 4096, 513),
+@pytest.mark.parametrize("m,k,n", [(9, 512, 300), (16, 4096, 1000), (13, 64, 17),
+                                   (17, 4096, 1000), (32, 64, 300), (33, 576, 257), (64, 4096, 513),
                                    (65, 1024, 700), (100, 14336, 260), (128, 4096, 4096), (200, 128, 17),
                                    (130, 1024, 600)])
 def test_prefill_gemm_within_bound(hip, m, k, n):
-    """M > 16 runs the gemm layout by default: 32 or 64 activation rows per
-    workgroup, partial activation tiles (m = 17, 33, 65, 100, 130, 200), partial
+    """M > 16 runs the gemm layout by default, and M = 9..16 where the wide
+    layout does not fill the device: 16, 32 or 64 activation rows per
+    workgroup, partial activation tiles (m = 9, 13, 17, 33, 65, 100, 130, 200), partial
     256-row weight blocks, K from one chunk to 224; edge data (subnormals,
     +-0, +-1e-38, inf/NaN weights).  Every element within the rigorous bound,
     non-finite classes and exact zeros as the reference."""
     x, w = case(m, k, n, seed=9000 + m + k + n, edge=True)
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
-    assert (p.slices, p.mt) == (-8, 32 if m <= 128 else 64), p
+    assert (p.slices, p.mt) == (-8, 16 if m <= 16 else 32 if m <= 128 else 64), p
     y = run_rd(hip, x, w)
     rows = np.unique(np.r_[0, n - 1, np.random.default_rng(m).integers(0, n, 160)])
     y_ref = oracle.matmul_bf16_t(x, w[rows])
