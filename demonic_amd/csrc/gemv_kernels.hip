@@ -873,24 +873,39 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 // bf16 terms once per call as planes [3][M][K], and each chunk's operands are
 // copied into LDS (no per-workgroup split).  When 256-row by 16*MB-row tiles
 // would leave the device short of workgroups, k is split over `slices`
-// workgroups (grid z), each covering kc chunks of 64, whose partial sums go
-// to P[slice][m][n] for gemm_sum_slices_kernel.  Numerics, special values and
+// workgroups, each covering kc chunks of 64, whose partial sums go to
+// P[slice][m][n] for gemm_sum_slices_kernel.  Numerics, special values and
 // the zero rule are the wide layout's, tile by tile; with slices the zero
 // rule runs after the sum.
 template <int MB>
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, const uint16_t *__restrict__ XS,
-                         float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc) {
+                         float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy) {
     static_assert(MB >= 1 && MB <= 4, "x staging covers at most 512 threads");
+    constexpr int D = 2;  // register sets of the chunk ring (3 and 4 measured no faster)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i16 = lane & 15;
     const int g = lane >> 4;
-    const int row0 = blockIdx.x * kWideRows;
+    // The tile from the linear workgroup id (a 1-D grid of gx * gy * slices).
+    // Workgroup L runs on XCD L % 8 (the dispatcher deals workgroups to the 8
+    // XCDs in turn) and takes the L / 8-th tile of that XCD's contiguous
+    // share, activation tiles fastest, so the workgroups an XCD runs together
+    // share weight blocks through its L2 (C2 shapes: 2-3% faster than weight
+    // blocks fastest).
+    uint32_t lin = blockIdx.x;
+    {
+        const uint32_t x = lin & 7u, q = gridDim.x >> 3, r = gridDim.x & 7u;
+        lin = x * q + min(x, r) + (lin >> 3);
+    }
+    const int by = (int)(lin % (uint32_t)gy);
+    const int bx = (int)(lin / (uint32_t)gy % (uint32_t)gx);
+    const int bz = (int)(lin / (uint32_t)gy / (uint32_t)gx);
+    const int row0 = bx * kWideRows;
     const int nrows = min(kWideRows, N - row0);
-    const int m0 = blockIdx.y * 16 * MB;
-    const int c0 = blockIdx.z * kc;                      // this slice's chunks: [c0, c1)
+    const int m0 = by * 16 * MB;
+    const int c0 = bz * kc;                              // this slice's chunks: [c0, c1)
     const int c1 = min(K / 64, c0 + kc);
     const int nchunks = max(0, c1 - c0);
 
@@ -907,26 +922,26 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     for (int j = 0; j < 4; ++j)
         soff[j] = (uint32_t)min(wave * 32 + slr + 8 * j, nrows - 1) * (uint32_t)K * 2u + scol;
     // x items: threads 0 .. 128*MB-1 = (tile xt = tid/128, k-block b = tid/64 % 2,
-    // operand lane): the lane's 8 elements of each of the three planes.
+    // operand lane): the lane's 8 elements of each of the three planes, by
+    // unconditional buffer loads (rows past M load from past the range: zeros).
     const bool xthread = tid < 128 * MB;
     const int xt = tid >> 7;
     const int xb = (tid >> 6) & 1;
     const int xm = m0 + xt * 16 + (lane & 15);
-    const bool xlive = xthread && xm < M;
-    const int64_t plane = (int64_t)M * K;
-    const uint16_t *xp = XS + (int64_t)min(xm, M - 1) * K + xb * 32 + (lane >> 4) * 8;
+    const uint32_t plane_bytes = (uint32_t)M * (uint32_t)K * 2u;
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(XS, 3u * plane_bytes);
+    const uint32_t xoff = xthread && xm < M ? ((uint32_t)xm * (uint32_t)K + xb * 32 + (lane >> 4) * 8) * 2u : kOutOfRange;
 
     struct Regs {
         u32x4 w[4];
         u32x4 x[3];
     };
     auto load = [&](int c, Regs &r) {
+        const uint32_t cb = (uint32_t)(c0 + c) * 128u;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + (uint32_t)(c0 + c) * 128u);
+        for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + cb);
 #pragma unroll
-        for (int q = 0; q < 3; ++q)
-            r.x[q] = xlive ? *reinterpret_cast<const u32x4 *>(xp + q * plane + (int64_t)(c0 + c) * 64)
-                           : u32x4{0u, 0u, 0u, 0u};
+        for (int q = 0; q < 3; ++q) r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, q * plane_bytes + cb, 0);
     };
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
@@ -974,23 +989,25 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
         }
     };
 
-    // Chunk c is in LDS (x planes in buffer c&1); chunk c+1 waits in one
-    // register set and chunk c+2 loads into the other.
-    Regs ra, rb;
-    if (nchunks > 0) load(0, ra);
-    if (nchunks > 1) load(1, rb);
-    if (nchunks > 0) store(ra, 0);
+    // A ring of D register sets: at step c chunk c is in LDS (x planes in
+    // buffer c&1), chunks c+1 .. c+D-1 are in flight to their sets, and the
+    // set chunk c arrived in (already in LDS) takes chunk c+D.
+    Regs r[D];
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+        if (u < nchunks) load(u, r[u]);
+    if (nchunks > 0) store(r[0], 0);
     __syncthreads();
-    auto step = [&](int c, Regs &rnext, Regs &rfree) {
-        if (c + 2 < nchunks) load(c + 2, rfree);
-        compute(c & 1);
-        if (c + 1 < nchunks) store(rnext, (c + 1) & 1);
-        __syncthreads();
-    };
-    for (int c = 0; c < nchunks; c += 2) {
-        step(c, rb, ra);
-        if (c + 1 >= nchunks) break;
-        step(c + 1, ra, rb);
+    for (int cb = 0; cb < nchunks; cb += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int c = cb + u;
+            if (c >= nchunks) break;
+            if (c + D < nchunks) load(c + D, r[u]);
+            compute(c & 1);
+            if (c + 1 < nchunks) store(r[(u + 1) % D], (c + 1) & 1);
+            __syncthreads();
+        }
     }
 
     const int base[2] = {wave * 32, wave * 32 + 16};
@@ -1001,22 +1018,22 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) live[t][r] = m < M && base[t] + g * 4 + r < nrows;
+            for (int rr = 0; rr < 4; ++rr) live[t][rr] = m < M && base[t] + g * 4 + rr < nrows;
         if (P) {  // a k slice: the partial sums, for gemm_sum_slices_kernel
-            float *ps = P + (int64_t)blockIdx.z * M * N + (int64_t)m * N + row0;
+            float *ps = P + (int64_t)bz * M * N + (int64_t)m * N + row0;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (live[t][r]) ps[base[t] + g * 4 + r] = acc[mt][t][r];
+                for (int rr = 0; rr < 4; ++rr)
+                    if (live[t][rr]) ps[base[t] + g * 4 + rr] = acc[mt][t][rr];
             continue;
         }
         settle_zeros(acc[mt], live, base, W + (int64_t)row0 * K, X + (int64_t)(m0 + mt * 16) * K, K, i16);
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (live[t][r]) Y[(int64_t)m * N + row0 + base[t] + g * 4 + r] = acc[mt][t][r];
+            for (int rr = 0; rr < 4; ++rr)
+                if (live[t][rr]) Y[(int64_t)m * N + row0 + base[t] + g * 4 + rr] = acc[mt][t][rr];
     }
 }
 
@@ -2132,7 +2149,8 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // rows16 wins, 27-31 against 31-33).
         const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 16 ? 8 : p.m > 8 ? (wide_fits ? 6 : 8) : 7);
         const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
-        mp.mkind = (kind == 6 || kind == 8) && rows256_fit ? kind : 7;
+        const bool planes_fit = (int64_t)6 * p.m * p.k <= INT32_MAX;          // x planes' buffer range
+        mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;
         mp.waves = 8;
         if (mp.mkind == 8) {
             mp.rpw = kWideRows;
@@ -2377,16 +2395,15 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             const int64_t count = p.m * p.k;
             hipLaunchKernelGGL(split_x_planes_kernel, dim3(stride_grid((count / 8 + 255) / 256)), dim3(256), 0, s,
                                p.x, xs, count);
-            const dim3 g3((unsigned)pl.grid_x, (unsigned)pl.grid_y, (unsigned)pl.kslices);
-            if (pl.mt == 16)
-                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<1>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
-                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
-            else if (pl.mt == 32)
-                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<2>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
-                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
-            else
-                hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<4>), g3, dim3(512), 0, s, p.w, p.x, xs, p.y, part,
-                                   (int)p.n, (int)p.k, (int)p.m, pl.kchunks);
+            const int64_t wgs = pl.grid_x * pl.grid_y * (int64_t)pl.kslices;
+            if (wgs > INT32_MAX) return hipErrorInvalidValue;
+#define DMC_GEMM(MB)                                                                                         \
+    if (pl.mt == 16 * MB)                                                                                    \
+        hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB>), dim3((unsigned)wgs), dim3(512), 0, s, p.w, p.x, xs,     \
+                           p.y, part, (int)p.n, (int)p.k, (int)p.m, pl.kchunks, (int)pl.grid_x, (int)pl.grid_y);  \
+    else
+            DMC_GEMM(1) DMC_GEMM(2) DMC_GEMM(4) return hipErrorInvalidValue;
+#undef DMC_GEMM
             if (pl.kslices > 1)
                 hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,
                                    s, part, pl.kslices, p.y, p.w, p.x, (int)p.m, (int)p.n, (int)p.k);
