@@ -336,7 +336,7 @@ def extended(d, W, reps: int) -> dict:
         dy = d.DeviceBuffer(4 * n * m)
         f = lambda i: d.gemv_rd(dx, dw, dy, m, k, n)  # noqa: E731
         f(0)
-        record(f"C4 rd m={m}", batch_us(d, f, 10), n, k, m)
+        record(f"C4 rd m={m}", batch_us(d, f, 20), n, k, m)
         dx.free()
         dy.free()
     dw.free()
@@ -370,7 +370,9 @@ def extended(d, W, reps: int) -> dict:
             x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
             s = Rotating(d, w, x, 3, n_out=n)
             f = lambda i: d.gemv_rd(s.x, s.w[i % 3], s.y, m, k, n)  # noqa: E731
-            us = batch_us(d, f, 10)
+            # 40 launches after as many untimed ones: the matrix cores reach
+            # their steady rate only after a few milliseconds of this load
+            us = batch_us(d, f, 40)
             tfs = 2.0 * m * n * k / (us * 1e-6) / 1e12
             out[f"C2 rd {name} prefill m={m}"] = {"us": round(us, 3), "TFLOP/s": round(tfs, 1),
                                                   "GB/s": round(b_alg(n, k, m) / (us * 1e-6) / 1e9, 1)}
