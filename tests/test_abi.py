@@ -166,6 +166,12 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 4 * 64 * 14336 * 4, p
     p = d.plan("rd", 512, 4096, 128256, x_addr=256, w_addr=256)   # 4008 tiles: no split
     assert p.workspace_bytes == 3 * 512 * 4096 * 2, p
+    # x's three bf16 planes must stay inside one buffer range (6 m k < 2^31):
+    # beyond that the rows16 layout, which reads x directly
+    p = d.plan("rd", 32768, 11008, 4096, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt) == (-7, 16), p
+    p = d.plan("rd", 32512, 11008, 4096, x_addr=256, w_addr=256)  # 6 m k = 2,147,352,576 < 2^31
+    assert p.slices == -8, p
     monkeypatch.setenv("DMC_HIP_RD_R16_TILES", "4")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
     assert p.slices == -6, p  # tiles only shape the rows16 layout
