@@ -955,35 +955,85 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     f32x4 acc[MB][2];
 #pragma unroll
     for (int mt = 0; mt < MB; ++mt) acc[mt][0] = acc[mt][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // One k-block of 32: the hi term with the raw weights, md and lo with
+    // inf/NaN lanes cleared when the wave's block holds any.
+    auto block = [&](const u32x4 (&a)[2], const u32x4 (&xo)[MB][3]) {
+        u32x4 a2[2];
+        uint32_t mx = 0;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
+        const bool any_special = wave_has_inf_nan(mx);
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            a2[t] = a[t];
+            if (any_special) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) a2[t][v] &= ~inf_nan_mask(a2[t][v]);
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MB; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                acc[mt][t] = mfma_bf16(a[t], xo[mt][0], acc[mt][t]);
+                acc[mt][t] = mfma_bf16(a2[t], xo[mt][1], acc[mt][t]);
+                acc[mt][t] = mfma_bf16(a2[t], xo[mt][2], acc[mt][t]);
+            }
+    };
+    auto read_ops = [&](int xbuf, int b, u32x4 (&a)[2], u32x4 (&xo)[MB][3]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+            a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+#pragma unroll
+        for (int mt = 0; mt < MB; ++mt)
+#pragma unroll
+            for (int q = 0; q < 3; ++q) xo[mt][q] = xpl[xbuf][mt][b][q][lane];
+    };
+    // With 64-row tiles both k-blocks' operands are read from LDS up front,
+    // so the second block's reads are in flight during the first block's
+    // MFMAs (C2 up / down at m = 512: 233 / 239 us against 245 / 241).  With
+    // fewer tiles the extra registers would cost a workgroup per CU (m = 64:
+    // 67 / 68 us against 61 / 63), so each block's operands are read just
+    // before it.
     auto compute = [&](int xbuf) {
+        if constexpr (MB == 4) {
+            u32x4 a[2][2], xo[2][MB][3];
+            read_ops(xbuf, 0, a[0], xo[0]);
+            read_ops(xbuf, 1, a[1], xo[1]);
+            block(a[0], xo[0]);
+            block(a[1], xo[1]);
+        } else {
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            u32x4 a[2], a2[2];
-            uint32_t mx = 0;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
-            }
-            const bool any_special = wave_has_inf_nan(mx);
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                a2[t] = a[t];
-                if (any_special) {
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) a2[t][v] &= ~inf_nan_mask(a2[t][v]);
-                }
-            }
-#pragma unroll
-            for (int mt = 0; mt < MB; ++mt) {
-                const u32x4 hi = xpl[xbuf][mt][b][0][lane], md = xpl[xbuf][mt][b][1][lane],
-                            lo = xpl[xbuf][mt][b][2][lane];
+            for (int b = 0; b < 2; ++b) {
+                u32x4 a[2], a2[2];
+                uint32_t mx = 0;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    acc[mt][t] = mfma_bf16(a[t], hi, acc[mt][t]);
-                    acc[mt][t] = mfma_bf16(a2[t], md, acc[mt][t]);
-                    acc[mt][t] = mfma_bf16(a2[t], lo, acc[mt][t]);
+                    a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
+                }
+                const bool any_special = wave_has_inf_nan(mx);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    a2[t] = a[t];
+                    if (any_special) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) a2[t][v] &= ~inf_nan_mask(a2[t][v]);
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MB; ++mt) {
+                    const u32x4 hi = xpl[xbuf][mt][b][0][lane], md = xpl[xbuf][mt][b][1][lane],
+                                lo = xpl[xbuf][mt][b][2][lane];
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        acc[mt][t] = mfma_bf16(a[t], hi, acc[mt][t]);
+                        acc[mt][t] = mfma_bf16(a2[t], md, acc[mt][t]);
+                        acc[mt][t] = mfma_bf16(a2[t], lo, acc[mt][t]);
+                    }
                 }
             }
         }
