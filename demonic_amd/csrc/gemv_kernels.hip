@@ -2206,17 +2206,25 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             mp.rpw = kWideRows;
             // 16 activation rows per workgroup up to m = 16 (no half-empty
             // MFMA tiles: C1 at m = 12 / 16, 20.0 / 21.3 us against 20.5 /
-            // 22.5 with 32-row tiles, C2 within 0.5 us), 32 (60 KiB of LDS:
-            // two workgroups per CU) up to m = 128, 64 above (C2 shapes, m =
-            // 64: 58-63 us against 67-71; m = 512: 300 against 340-388).
-            const int gmt = env_int("DMC_HIP_GEMM_MT", p.m <= 16 ? 16 : p.m <= 128 ? 32 : 64);
+            // 22.5 with 32-row tiles, C2 within 0.5 us), 32 up to m = 32, 64
+            // above (C2 up / down: m = 48 50 / 55 us against 60 / 66 on 32-row
+            // tiles, m = 128 80 / 79 against 94 / 94, m = 256 124 / 125
+            // against 152 / 158).
+            const int gmt = env_int("DMC_HIP_GEMM_MT", p.m <= 16 ? 16 : p.m <= 32 ? 32 : 64);
             mp.mt = gmt == 16 ? 16 : gmt == 32 ? 32 : 64;
-            // Split k while the grid holds up to 2 workgroups per CU, whole
-            // rounds only (a 2.2-round grid runs 3 rounds): kchunks chunks of
-            // 64 per slice.
+            // Split k while the grid fits one workgroup per CU (16-row tiles:
+            // two), kchunks chunks of 64 per slice; when that leaves a lone
+            // round under 70% full, fill two rounds instead.  Measured on C2's
+            // shapes: one workgroup per CU beats two for 32- and 64-row tiles
+            // at every m from 32 to 512 (m = 128: 80 / 79 us against 89 / 88;
+            // m = 256: 124 / 125 against 140 / 135), except up at m = 192,
+            // whose 168 tiles leave a third of the CUs idle (112 us on three
+            // slices against 124 on one).
             const int64_t tiles = ((p.n + kWideRows - 1) / kWideRows) * ((p.m + mp.mt - 1) / mp.mt);
             const int64_t nchunks = p.k / 64;
-            int64_t want = std::max<int64_t>(1, 2 * cus / tiles);
+            const int64_t per_cu = std::max(1, env_int("DMC_HIP_GEMM_PER_CU", mp.mt == 16 ? 2 : 1));
+            int64_t want = std::max<int64_t>(1, per_cu * cus / tiles);
+            if (tiles < cus && tiles * want * 10 < cus * 7) want = std::max<int64_t>(1, 2 * per_cu * cus / tiles);
             want = std::min<int64_t>({want, nchunks, (int64_t)env_int("DMC_HIP_GEMM_MAX_SLICES", 64)});
             want = std::max<int64_t>(want, 1);
             mp.kchunks = (int)((nchunks + want - 1) / want);

@@ -124,7 +124,7 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
     # prefill-sized M: the gemm layout, 32 or 64 activation rows per workgroup
-    for m, mt in ((17, 32), (32, 32), (128, 32), (129, 64), (512, 64)):
+    for m, mt in ((17, 32), (32, 32), (33, 64), (128, 64), (512, 64)):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 501), p
     # k not a multiple of 64: back to the streaming kernel, activation rows held in
@@ -158,12 +158,19 @@ def test_rowdot_mfma_layouts(monkeypatch):
     # blocks per workgroup shrink while the grid would fall under 2 per CU
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
-    # the gemm layout splits k while the grid stays within 2 workgroups per CU:
-    # C2 up at m = 64 has 112 tiles of 256 x 32, so at most 4 slices of 16
-    # chunks; its workspace holds x's three bf16 planes and the 4 partial sums
+    # the gemm layout splits k while the grid stays within one workgroup per
+    # CU: C2 up at m = 64 has 56 tiles of 256 x 64, so 4 slices of 16 chunks;
+    # its workspace holds x's three bf16 planes and the 4 partial sums
     p = d.plan("rd", 64, 4096, 14336, x_addr=256, w_addr=256)
-    assert (p.slices, p.mt, p.grid_x) == (-8, 32, 56), p
+    assert (p.slices, p.mt, p.grid_x) == (-8, 64, 56), p
     assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 4 * 64 * 14336 * 4, p
+    # up at m = 192: 168 tiles would leave a lone round a third empty, so
+    # k splits to fill two rounds (3 slices)
+    p = d.plan("rd", 192, 4096, 14336, x_addr=256, w_addr=256)
+    assert p.workspace_bytes == 3 * 192 * 4096 * 2 + 3 * 192 * 14336 * 4, p
+    # down at m = 32: 16 tiles of 256 x 32, 16 slices of 14 chunks
+    p = d.plan("rd", 32, 14336, 4096, x_addr=256, w_addr=256)
+    assert (p.mt, p.workspace_bytes) == (32, 3 * 32 * 14336 * 2 + 16 * 32 * 4096 * 4), p
     p = d.plan("rd", 512, 4096, 128256, x_addr=256, w_addr=256)   # 4008 tiles: no split
     assert p.workspace_bytes == 3 * 512 * 4096 * 2, p
     # x's three bf16 planes must stay inside one buffer range (6 m k < 2^31):

@@ -784,7 +784,7 @@ def test_prefill_gemm_within_bound(hip, m, k, n):
     non-finite classes and exact zeros as the reference."""
     x, w = case(m, k, n, seed=9000 + m + k + n, edge=True)
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
-    assert (p.slices, p.mt) == (-8, 16 if m <= 16 else 32 if m <= 128 else 64), p
+    assert (p.slices, p.mt) == (-8, 16 if m <= 16 else 32 if m <= 32 else 64), p
     y = run_rd(hip, x, w)
     rows = np.unique(np.r_[0, n - 1, np.random.default_rng(m).integers(0, n, 160)])
     y_ref = oracle.matmul_bf16_t(x, w[rows])
