@@ -2128,8 +2128,12 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
     const int kv = (int)((k + nw * 512 - 1) / (nw * 512));
     const int mt_cap = kv == 1 ? 8 : kv == 2 ? 4 : kv <= 4 ? 2 : 1;
     const int mt = std::min(mt_for(m), mt_cap);
-    int rows = env_int("DMC_HIP_RD_ROWS", kv <= 4 ? 2 : 1);
-    if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = kv <= 4 ? 2 : 1;
+    // Rows per register buffer: 2, or 1 for long rows (more than 4 vectors
+    // per lane) and for long rows at two or more activation rows (C2 down at
+    // m = 2: 21.4-21.5 us against 22.0-22.2 with 2).
+    const int rows_default = kv > 4 || (kv >= 2 && mt >= 2) ? 1 : 2;
+    int rows = env_int("DMC_HIP_RD_ROWS", rows_default);
+    if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = rows_default;
     const int64_t gy = (m + mt - 1) / mt;
     auto blocks = [&](int64_t r) {
         int64_t b = 0;
@@ -2139,8 +2143,11 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
     // Rows per workgroup, measured on MI355X: 4 for short rows (k <= 4096
     // per 8 waves: up/gate 18.1 us, 8 rows 18.5), fewer when that would leave
     // under 4 workgroups per CU; 8 for long ones (down, k = 14336: 19.0 us,
-    // 4 rows 19.8), fewer when that would leave under 2 per CU.
-    const int rpw_default = kv >= 2 ? 8 : 4;
+    // 4 rows 19.8), fewer when that would leave under 2 per CU.  With two or
+    // more activation rows each weight row's x reads weigh more: 16 short
+    // rows (C2 up at m = 2, capped to 8 by the grid: 19.6 us against 21.8 at
+    // 4; C4: 146.6 against 172.1 at 4 and 148.8 at 8).
+    const int rpw_default = mt >= 2 && kv == 1 ? 16 : kv >= 2 ? 8 : 4;
     const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
     int rpw = env_int("DMC_HIP_RD_RPW", rpw_default);
     if (rpw < 1) rpw = rpw_default;
@@ -2179,7 +2186,11 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     // against 174); for larger M the wide layout where its 256-row workgroups
     // give >= 1.5 per CU (C4), rows16 elsewhere.  (A third layout, 16-row tiles with k split over the waves,
     // measured 1.2-2.7x slower than rows16 on every shape and was removed.)
-    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 2);
+    // From 3 activation rows: at m = 2 the streaming kernel with 16 (or 8)
+    // weight rows per workgroup is as fast or faster (C2 up 19.6 us against
+    // 21.7, down 21.5-22.2 against 22.2, C4 146.6 against 154.5, C1 equal);
+    // at m = 3 and 4 it is 7-80% slower.
+    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 3);
     if (mfma_min_m > 0 && p.m >= mfma_min_m && p.k >= 64 && p.k % 64 == 0 && p.k <= INT32_MAX / 2 &&
         aligned(p.w, 16) && aligned(p.x, 16) && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n &&
         (int64_t)16 * 4 * p.k <= INT32_MAX && (p.m + 15) / 16 <= 65535) {  // rows16: 16 x rows of f32

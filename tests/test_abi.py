@@ -111,12 +111,22 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # M = 1: the streaming kernel
     p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
     assert p.mt == 1 and p.slices >= 1, p
-    # M >= 2 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
+    # M = 2: the streaming kernel, 16 weight rows per workgroup where the grid
+    # keeps 4 workgroups per CU (8 on C2 up/gate)
+    p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 16, 8016), p
+    p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
+    # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
     # (16 weight rows per workgroup, 4 activation rows); larger M on the LM head:
     # the wide layout, 16 activation rows per tile
-    for m in (2, 3, 4):
+    for m in (3, 4):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")
+    p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
+    monkeypatch.delenv("DMC_HIP_RD_MFMA_MIN_M")
     for m in (5, 8):  # two 16-row blocks per workgroup
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
@@ -146,7 +156,7 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
 
 def test_rowdot_mfma_layouts(monkeypatch):
     # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
-    for m, mt, rpw in [(2, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32)]:
+    for m, mt, rpw in [(3, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32)]:
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)

@@ -111,6 +111,7 @@ def test_skinny_mfma_underflowing_products_keep_their_zero_sign(hip, m, k, kind,
     w[0, :] = 0x0001
     w[1, :] = 0x8001
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")  # M = 2 included
     assert hip.plan("rd", m, k, 3, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
     y_ref = ref(x, w)
     assert np.all(np.signbit(y_ref[:, 0])) and not np.any(np.signbit(y_ref[:, 1:]))
@@ -140,6 +141,7 @@ def test_skinny_mfma_zero_outputs_follow_the_reference_chain(hip, kind, monkeypa
     w[6, :7] = 0x8001
     w[7, ::5] = 0x8000                         # -0 weights among positive tiny products
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")  # M = 2 included
     assert hip.plan("rd", m, k, 8, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
     y_ref = ref(x, w)
     assert np.any(np.signbit(y_ref[y_ref == 0])) and np.any(~np.signbit(y_ref[y_ref == 0]))
@@ -156,6 +158,7 @@ def test_rows16_blocks_per_workgroup(hip, m, tiles, monkeypatch):
     rows sampled from every block position and the last rows."""
     k, n = 1024, 40003
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")  # M = 2 included
     monkeypatch.setenv("DMC_HIP_RD_R16_TILES", str(tiles))
     x, w = case(m, k, n, seed=77 + m * 5 + tiles, edge=True)
     w[n - 2, :] = 0
@@ -186,6 +189,27 @@ def test_shapes(hip, m, k, n, layout):
     x, w = case(m, k, n, seed=1000 + m * 7 + k * 13 + n, edge=True)
     y = RUN[layout](hip, x, w)
     check(y, ref(x, w), what=f"{layout} m={m} k={k} n={n}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 14336), (4096, 16387), (14336, 4096), (4096, 40003), (1024, 33), (64, 70)])
+def test_two_activation_rows_stream(hip, k, n):
+    """M = 2 runs the streaming kernel with 16 (or, where the grid would fall
+    under 4 workgroups per CU, 8 or 4) weight rows per workgroup: C2's shapes,
+    a partial last workgroup (n = 16387, 40003), short rows.  Edge data; every
+    element within the rigorous bound, special classes and zero signs as the
+    reference."""
+    x, w = case(2, k, n, seed=8100 + k + n, edge=True)
+    p = hip.plan("rd", 2, k, n, x_addr=256, w_addr=256)  # device regions are 256-byte aligned
+    assert p.slices > 0 and p.mt == 2, p
+    y = run_rd(hip, x, w)
+    rows = np.unique(np.r_[np.arange(0, min(40, n)), np.arange(max(0, n - 40), n),
+                           np.random.default_rng(k + n).integers(0, n, 300)])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    check(y[:, rows], y_ref, what=f"m=2 stream k={k} n={n}")
+    wf = W.bf16_to_f32(w[rows])
+    fin = np.all(np.isfinite(wf), axis=1)
+    for r in range(2):
+        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"m=2 stream k={k} n={n} row {r}")
 
 
 @pytest.mark.parametrize("offset,k,n", [(2, 4096, 300), (6, 4104, 257), (14, 2048, 33), (10, 777, 1000),
@@ -706,6 +730,7 @@ def test_skinny_mfma_special_values(hip, m, kind, monkeypatch):
     w[13, 100] = 0x7F80                # +inf against a normal x in every row
     w[14, 200] = 0x7FC1                # NaN
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")  # M = 2 included
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
     assert p.slices == -kind, "expected the MFMA kernel"
     y = run_rd(hip, x, w)
@@ -726,6 +751,7 @@ def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
     and chunks: every element within the rigorous forward-error bound of the
     reference chain."""
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", str(kind))
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")  # M = 2 included
     x, w = case(m, k, n, seed=m + k + n, scale=0.02)
     assert hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data).slices == -kind
     y = run_rd(hip, x, w)
