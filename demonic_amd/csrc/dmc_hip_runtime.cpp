@@ -139,6 +139,8 @@ struct Ctx {
     std::unordered_map<Key, void *, KeyHash> weights;
     int64_t resident_bytes = 0;
     Buf dx, dy, ws;         // device scratch (reuse is stream-ordered)
+    int live_graphs = 0;    // executable graphs not yet destroyed
+    std::vector<void *> retired_ws;  // outgrown workspaces a live graph may still use
     Buf hx, hy;             // pinned staging
     size_t hx_off = 0, hy_off = 0;
     std::vector<Pending> pending;
@@ -214,7 +216,14 @@ int ensure_dev(Buf &b, size_t need) {
     while (cap < need) cap *= 2;
     if (b.p) {
         HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
-        HIP_TRY(hipFree(b.p), "hipFree");
+        // A captured graph holds the workspace's address: while any graph
+        // lives, an outgrown workspace stays allocated (freed with the last
+        // graph), so a later replay never touches freed memory.
+        if (&b == &c.ws && c.live_graphs > 0) {
+            c.retired_ws.push_back(b.p);
+        } else {
+            HIP_TRY(hipFree(b.p), "hipFree");
+        }
         b.p = nullptr;
         b.cap = 0;
     }
@@ -988,6 +997,7 @@ int64_t dmc_hip_capture_end(void) {
     e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
     (void)hipGraphDestroy(graph);
     if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate"), 0;
+    ctx().live_graphs++;
     return reinterpret_cast<int64_t>(exec);
 }
 
@@ -1005,8 +1015,13 @@ int32_t dmc_hip_graph_destroy(int64_t exec) {
     if (!exec) return DMC_HIP_OK;
     int rc = ensure_init();
     if (rc) return rc;
-    HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    Ctx &c = ctx();
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
     HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)), "hipGraphExecDestroy");
+    if (c.live_graphs > 0 && --c.live_graphs == 0) {
+        for (void *p : c.retired_ws) HIP_TRY(hipFree(p), "hipFree(retired workspace)");
+        c.retired_ws.clear();
+    }
     return DMC_HIP_OK;
 }
 

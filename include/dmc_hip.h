@@ -190,10 +190,13 @@ int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, i
 /* HIP graphs of the library stream.  Between capture_begin and capture_end,
  * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
  * workspace -- column-stream split-K partials, or x's bf16 planes and partial
- * sums for row-dot with m > 8 -- is already large enough, i.e. after one
- * uncaptured call of the same shape) are recorded instead of run; capture_end returns an
+ * sums for row-dot on the gemm layout (m > 16, or 9..16 where the wide layout
+ * would leave CUs idle) -- is already large enough, i.e. after one uncaptured
+ * call of the same shape) are recorded instead of run; capture_end returns an
  * executable graph (0 on error: an entry that allocates or waits was called
- * while capturing) that graph_launch replays on the library stream.  The
+ * while capturing) that graph_launch replays on the library stream.  While
+ * any graph is alive, a workspace outgrown by a later call stays allocated
+ * (graph_destroy of the last graph frees it), so replays stay valid.  The
  * MI355X form of the reference's pipelined command buffers (gpu.rs:206-219,
  * gpu.rs:539-624): one host call issues a whole decode step. */
 int32_t dmc_hip_capture_begin(void);

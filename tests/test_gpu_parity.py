@@ -657,6 +657,47 @@ def test_graph_replay_matches_oracle_each_time(hip):
             b.free()
 
 
+def test_graph_replay_after_workspace_growth(hip):
+    """A graph captured around a gemm-layout GEMV (its x planes and partial
+    sums live in the library workspace), then a larger eager call that
+    outgrows the workspace, then the graph replayed: the replay must still
+    see a live workspace and match the reference, and so must eager calls
+    after the graph is destroyed."""
+    k, n, m1, m2 = 1024, 600, 24, 4096  # m2's workspace (~45 MB) outgrows every earlier test's
+    x1, w = case(m1, k, n, seed=4242, scale=0.02)
+    x2, _ = case(m2, k, n, seed=4243, scale=0.02)
+    dw = hip.DeviceBuffer.from_numpy(w)
+    dx1, dx2 = hip.DeviceBuffer.from_numpy(x1), hip.DeviceBuffer.from_numpy(x2)
+    dy1, dy2 = hip.DeviceBuffer(4 * m1 * n), hip.DeviceBuffer(4 * m2 * n)
+    try:
+        p1 = hip.plan("rd", m1, k, n, x_addr=256, w_addr=256)
+        p2 = hip.plan("rd", m2, k, n, x_addr=256, w_addr=256)
+        assert p1.slices == -8 and p2.workspace_bytes > 2 * p1.workspace_bytes, (p1, p2)
+        hip.gemv_rd(dx1, dw, dy1, m1, k, n)                   # sizes the workspace for m1
+        hip.synchronize()
+        g = hip.Graph()
+        with g:
+            hip.gemv_rd(dx1, dw, dy1, m1, k, n)
+        try:
+            hip.gemv_rd(dx2, dw, dy2, m2, k, n)               # outgrows it
+            hip.synchronize()
+            sample = [0, 1, m2 // 2, m2 - 1]
+            check(dy2.download(np.float32, (m2, n))[sample], ref(x2[sample], w), what="eager m2 after growth")
+            for rep in range(2):
+                dy1.upload(np.full(m1 * n, np.nan, np.float32))
+                g.launch()
+                hip.synchronize()
+                check(dy1.download(np.float32, (m1, n)), ref(x1, w), what=f"replay {rep} after growth")
+        finally:
+            g.destroy()
+        hip.gemv_rd(dx1, dw, dy1, m1, k, n)
+        hip.synchronize()
+        check(dy1.download(np.float32, (m1, n)), ref(x1, w), what="eager m1 after destroy")
+    finally:
+        for b in (dw, dx1, dx2, dy1, dy2):
+            b.free()
+
+
 def test_c3_layer_schedule(hip):
     """One layer of the C3 decode sweep as the bench runs it: weights filled in
     HBM by the counter generator, q/k/v and gate/up as grouped launches, o and
