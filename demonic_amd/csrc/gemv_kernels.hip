@@ -2370,10 +2370,17 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         pl.mt = std::min(mt_for(p.m), 4);
         pl.cb = kCsCols;
         pl.grid_x = (p.n + kCsCols - 1) / kCsCols;
-        // Split k so the launch has ~4 workgroups per CU (env-tunable), each
-        // wave with at least 8 rows.
+        // Split k so the launch has ~4 workgroups per CU; 2 with at most 16
+        // column blocks, 3 with at most 24 (env-tunable); each wave with at
+        // least 8 rows.  Measured with one activation row (shapes as the
+        // logical [N,K]): C2 down [4096,14336] (8 column blocks) 21.2 us at 2
+        // per CU against 22.3 at 4, C1 9.4 against 10.9, C5 [4097,11008]
+        // (9 blocks) 23.0-23.4 against 24.0-24.1; C5 [11008,4097] (22
+        // blocks) 18.2 at 3 against 19.6 at 4; C2 up (28 blocks) 22.5 at 4
+        // against 24.9 at 3.
         const int64_t groups = pl.grid_x * std::min<int64_t>(batch, 32768) * ((p.m + pl.mt - 1) / pl.mt);
-        const int64_t target = (int64_t)env_int("DMC_HIP_CS_GROUPS_PER_CU", 4) * cus;
+        const int gpc = pl.grid_x <= 16 ? 2 : pl.grid_x <= 24 ? 3 : 4;
+        const int64_t target = (int64_t)env_int("DMC_HIP_CS_GROUPS_PER_CU", gpc) * cus;
         const int64_t want = std::max<int64_t>(1, (target + groups - 1) / groups);
         const int64_t krows = un ? kmax - 1 : kmax;  // rows the streaming kernel covers
         int64_t kslice = (krows + want - 1) / want;

@@ -253,14 +253,16 @@ def test_rowdot_unaligned_needs_a_well_filled_last_block():
 
 
 def test_column_stream_plans_split_k_and_size_workspace():
-    # streaming kernel: 512 columns per workgroup, k split so ~4 workgroups per CU
+    # streaming kernel: 512 columns per workgroup, k split so ~2 workgroups per
+    # CU with at most 16 column blocks (C2 down: 8), ~4 with more (C2 up: 28)
     p = d.plan("cs", 1, 14336, 4096, x_addr=256, w_addr=256)
     assert p.vec == 8 and p.waves == 4 and p.grid_x == 8 and p.slices > 1
     assert p.workspace_bytes == p.slices * 4096 * 4
-    assert p.grid_x * p.slices >= 1024 - p.grid_x
+    assert 512 - p.grid_x <= p.grid_x * p.slices <= 512 + p.grid_x, p
     assert p.rows_per_group * p.slices >= 14336 > p.rows_per_group * (p.slices - 1)
     up = d.plan("cs", 1, 4096, 14336, x_addr=256, w_addr=256)
     assert up.grid_x == 28 and up.rows_per_group % 4 == 0
+    assert 1024 - up.grid_x <= up.grid_x * up.slices <= 1024 + up.grid_x, up
     one = d.plan("cs", 1, 32, 4096, x_addr=256, w_addr=256)  # >= 8 k rows per wave
     assert one.slices == 1 and one.workspace_bytes == 0
     assert d.plan("cs", 16, 4096, 4096, x_addr=256, w_addr=256).mt == 4
