@@ -2246,16 +2246,19 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             mp.rpw = kWideRows;
         } else {
             // rows16: T 16-row blocks per workgroup, gridDim.x apart, while
-            // the grid keeps >= 2 workgroups per CU.  Two blocks share each x
-            // split at MC = 8 (C4 m = 8: 165 us against 195 with one block
-            // and 174 on the wide layout); at MC = 4 the split is cheap enough
-            // (equal times), at MC = 16 the registers of more blocks cost
-            // occupancy (205-217 us against 174 on the wide layout).
+            // the grid keeps >= 1 workgroup per CU.  Two blocks share each x
+            // split at MC = 4 and 8 (C4 m = 8: 165 us against 195 with one
+            // block and 174 on the wide layout; C2 up m = 3 / 4 / 6 / 8: 20.4
+            // / 20.5 / 22.5 / 22.8 us against 21.2 / 21.7 / 26.4 / 26.4 with
+            // one; C2 down and C1, 256 blocks, keep one), at MC = 16 the
+            // registers of more blocks cost occupancy (205-217 us against 174
+            // on the wide layout).
             mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
-            int tiles = env_int("DMC_HIP_RD_R16_TILES", mp.mt == 8 ? 2 : 1);
+            int tiles = env_int("DMC_HIP_RD_R16_TILES", mp.mt <= 8 ? 2 : 1);
             if (tiles != 1 && tiles != 2 && tiles != 4) tiles = 1;
             const int64_t blocks16 = (p.n + 15) / 16;
-            while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < 2 * cus) tiles >>= 1;
+            const int64_t min_wg = (int64_t)env_int("DMC_HIP_RD_R16_MIN_WG_PER_CU", 1) * cus;
+            while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < min_wg) tiles >>= 1;
             mp.rpw = 16 * tiles;
         }
         mp.grid_x = (p.n + mp.rpw - 1) / mp.rpw;

@@ -118,14 +118,14 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
     # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
-    # (16 weight rows per workgroup, 4 activation rows); larger M on the LM head:
-    # the wide layout, 16 activation rows per tile
+    # (two 16-row blocks per workgroup, 4 activation rows); larger M on the LM
+    # head: the wide layout, 16 activation rows per tile
     for m in (3, 4):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
-    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 16, 8, 8016), p
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
     monkeypatch.delenv("DMC_HIP_RD_MFMA_MIN_M")
     for m in (5, 8):  # two 16-row blocks per workgroup
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
@@ -156,7 +156,7 @@ def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
 
 def test_rowdot_mfma_layouts(monkeypatch):
     # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
-    for m, mt, rpw in [(3, 4, 16), (4, 4, 16), (5, 8, 32), (8, 8, 32)]:
+    for m, mt, rpw in [(3, 4, 32), (4, 4, 32), (5, 8, 32), (8, 8, 32)]:
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
@@ -165,9 +165,12 @@ def test_rowdot_mfma_layouts(monkeypatch):
     for m, mt in ((9, 16), (16, 16), (20, 32)):
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 65), (m, p)
-    # blocks per workgroup shrink while the grid would fall under 2 per CU
+    # blocks per workgroup shrink while the grid would fall under 1 per CU:
+    # C2 up/gate keeps two (448 workgroups), C2 down and C1 (256 blocks) one
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
-    assert (p.mt, p.rows_per_group, p.grid_x) == (8, 16, 896), p
+    assert (p.mt, p.rows_per_group, p.grid_x) == (8, 32, 448), p
+    p = d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256)
+    assert (p.mt, p.rows_per_group, p.grid_x) == (4, 16, 256), p
     # the gemm layout splits k while the grid stays within one workgroup per
     # CU: C2 up at m = 64 has 56 tiles of 256 x 64, so 4 slices of 16 chunks;
     # its workspace holds x's three bf16 planes and the 4 partial sums
