@@ -2208,7 +2208,17 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // 9 rows too where the wide layout does not fill the device (C2 up and
         // down at m = 12 and 16: 34-38 us against 41-44 on rows16; at m = 8
         // rows16 wins, 27-31 against 31-33).
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m > 16 ? 8 : p.m > 8 ? (wide_fits ? 6 : 8) : 7);
+        // On a small matrix the gemm layout's two extra launches (x split,
+        // slice sum) outweigh its reuse: rows16, which streams the weights
+        // once per 16 activation rows, while that totals at most 80 MiB.
+        // Measured (rows16 / gemm, us): W [1024,4096] at m = 128 24 / 32;
+        // [4096,2048] at m = 64 25.6 / 31.5, at m = 128 48 / 34; C1 at
+        // m = 12 13.5 / 20.9, m = 32 25.5 / 25.9, m = 48 36 / 31; [8192,4096]
+        // at m = 12 22.9 / 24.5, m = 24 44 / 28; C2 at m = 12 38 / 32.
+        const int64_t wbytes = (int64_t)2 * p.n * p.k;
+        const bool small = gy * wbytes <= ((int64_t)80 << 20);
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND",
+                                 p.m <= 8 ? 7 : p.m <= 16 && wide_fits ? 6 : small ? 7 : 8);
         const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
         const bool planes_fit = (int64_t)6 * p.m * p.k <= INT32_MAX;          // x planes' buffer range
         mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;
@@ -2236,6 +2246,12 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             const int64_t per_cu = std::max(1, env_int("DMC_HIP_GEMM_PER_CU", mp.mt == 16 ? 2 : 1));
             int64_t want = std::max<int64_t>(1, per_cu * cus / tiles);
             if (tiles < cus && tiles * want * 10 < cus * 7) want = std::max<int64_t>(1, 2 * per_cu * cus / tiles);
+            // A slice of fewer than 8 chunks pays its pipeline fill and output
+            // too often: halve the split (C2 down at m = 12 / 16 on 16-row
+            // tiles: 35.0 / 37.2 us on 16 slices of 14 chunks against 37.3 /
+            // 40.4 on 32 of 7).
+            const int64_t min_chunks = std::max(1, env_int("DMC_HIP_GEMM_MIN_CHUNKS", 8));
+            while (want > 1 && (nchunks + want - 1) / want < min_chunks) want = (want + 1) / 2;
             want = std::min<int64_t>({want, nchunks, (int64_t)env_int("DMC_HIP_GEMM_MAX_SLICES", 64)});
             want = std::max<int64_t>(want, 1);
             mp.kchunks = (int)((nchunks + want - 1) / want);

@@ -165,6 +165,10 @@ def test_rowdot_mfma_layouts(monkeypatch):
     for m, mt in ((9, 16), (16, 16), (20, 32)):
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 65), (m, p)
+    # ... except on a matrix under 64 MiB, where rows16 saves the gemm layout's
+    # two extra launches (C1 at m = 12)
+    p = d.plan("rd", 12, 4096, 4096, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group) == (-7, 16, 16), p
     # blocks per workgroup shrink while the grid would fall under 1 per CU:
     # C2 up/gate keeps two (448 workgroups), C2 down and C1 (256 blocks) one
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)

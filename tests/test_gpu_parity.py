@@ -657,13 +657,14 @@ def test_graph_replay_matches_oracle_each_time(hip):
             b.free()
 
 
-def test_graph_replay_after_workspace_growth(hip):
+def test_graph_replay_after_workspace_growth(hip, monkeypatch):
     """A graph captured around a gemm-layout GEMV (its x planes and partial
     sums live in the library workspace), then a larger eager call that
     outgrows the workspace, then the graph replayed: the replay must still
     see a live workspace and match the reference, and so must eager calls
     after the graph is destroyed."""
     k, n, m1, m2 = 1024, 600, 24, 4096  # m2's workspace (~45 MB) outgrows every earlier test's
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")  # a matrix this small runs rows16 by default
     x1, w = case(m1, k, n, seed=4242, scale=0.02)
     x2, _ = case(m2, k, n, seed=4243, scale=0.02)
     dw = hip.DeviceBuffer.from_numpy(w)
@@ -842,7 +843,7 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
                                    (17, 4096, 1000), (32, 64, 300), (33, 576, 257), (64, 4096, 513),
                                    (65, 1024, 700), (100, 14336, 260), (128, 4096, 4096), (200, 128, 17),
                                    (130, 1024, 600)])
-def test_prefill_gemm_within_bound(hip, m, k, n):
+def test_prefill_gemm_within_bound(hip, m, k, n, monkeypatch):
     """M > 16 runs the gemm layout by default, and M = 9..16 where the wide
     layout does not fill the device: 16, 32 or 64 activation rows per
     workgroup, partial activation tiles (m = 9, 13, 17, 33, 65, 100, 130, 200), partial
@@ -850,6 +851,7 @@ def test_prefill_gemm_within_bound(hip, m, k, n):
     +-0, +-1e-38, inf/NaN weights).  Every element within the rigorous bound,
     non-finite classes and exact zeros as the reference."""
     x, w = case(m, k, n, seed=9000 + m + k + n, edge=True)
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")  # small matrices run rows16 by default
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
     assert (p.slices, p.mt) == (-8, 16 if m <= 16 else 32 if m <= 32 else 64), p
     y = run_rd(hip, x, w)
@@ -869,6 +871,7 @@ def test_prefill_gemm_unsplit(hip, m, k, n, monkeypatch):
     zero rule runs inside the kernel: edge data, an all-zero weight row, and
     rows whose underflowing products end at -0.0 and +0.0."""
     monkeypatch.setenv("DMC_HIP_GEMM_MAX_SLICES", "1")
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")  # small matrices run rows16 by default
     x, w = case(m, k, n, seed=9500 + m + k + n, edge=True)
     w[3] = 0
     w[5] = 0x0001
