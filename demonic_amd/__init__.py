@@ -68,7 +68,7 @@ def _dims2(x: np.ndarray) -> tuple[int, int]:
 
 
 def matmul_bf16_gpu(x: np.ndarray, w: np.ndarray) -> np.ndarray:
-    """out[m,n] = x[m,k] @ bf16(w[k,n]) -- dmc_matmul_bf16_gpu (gpu.rs:391-408)."""
+    """out[m,n] = x[m,k] @ bf16(w[k,n]) -- dmc_matmul_bf16_gpu (gpu.rs:400-409)."""
     x = _arr(x, np.float32, "x")
     w = _arr(w, np.uint16, "w")
     m, k = _dims2(x)

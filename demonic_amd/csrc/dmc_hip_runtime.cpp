@@ -17,6 +17,7 @@
 #include "../../include/dmc_hip.h"
 #include "gemv_launch.h"
 #include "npz_ingress.h"
+#include "residency.h"
 
 #include <fcntl.h>
 #include <hip/hip_runtime.h>
@@ -66,14 +67,7 @@ bool env_flag(const char *name) {
 // trailing bytes), each mixed with its index through the splitmix64 finalizer
 // into two independent 64-bit lanes.  ~500 scattered host reads per call, the
 // same order of cost as the reference's 256-sample fingerprint (gpu.rs:334-358).
-struct Key {
-    uint64_t a, b;
-    int64_t bytes;
-    bool operator==(const Key &o) const { return a == o.a && b == o.b && bytes == o.bytes; }
-};
-struct KeyHash {
-    size_t operator()(const Key &k) const { return (size_t)(k.a ^ (k.b << 1)); }
-};
+using Key = dmc::WeightKey;
 
 inline uint64_t mix64(uint64_t z) {
     z ^= z >> 30;
@@ -125,9 +119,19 @@ struct Pending {
     size_t bytes;
 };
 
+// DMC_HIP_TIME=1 accounting, after the reference's DMC_GPU_TIME (gpu.rs:45-96):
+// host phases per call, the device's view of each synchronous call from HIP
+// events (x upload, kernels), and per-shape buckets with the GB/s the kernels
+// reached on the weight bytes.
+struct ShapeStats {
+    int64_t k, n, batch;
+    uint64_t calls, wait_ns, gpu_ns;
+};
+
 struct Stats {
     uint64_t calls = 0, stage_ns = 0, key_ns = 0, upload_ns = 0, enqueue_ns = 0, wait_ns = 0,
-             readback_ns = 0, uploads = 0;
+             readback_ns = 0, uploads = 0, gpu_x_ns = 0, gpu_k_ns = 0, timed = 0;
+    std::vector<ShapeStats> shapes;
 };
 
 struct Ctx {
@@ -136,8 +140,7 @@ struct Ctx {
     int cus = 0;
     std::string arch;
     hipStream_t stream = nullptr;
-    std::unordered_map<Key, void *, KeyHash> weights;
-    int64_t resident_bytes = 0;
+    dmc::Residency *weights = nullptr;  // resident weights by content key (created at init)
     Buf dx, dy, ws;         // device scratch (reuse is stream-ordered)
     int live_graphs = 0;    // executable graphs not yet destroyed
     std::vector<void *> retired_ws;  // outgrown workspaces a live graph may still use
@@ -149,6 +152,9 @@ struct Ctx {
     std::vector<void *> ingress;        // pinned chunks for .npz ingress, kIngressChunk bytes each
     std::vector<hipEvent_t> ingress_ev; // one per chunk: its last copy to the device
     bool timing = false;
+    uint64_t time_every = 0;  // DMC_HIP_TIME=N > 1: a stats line every N calls
+    bool x_kernel = false;  // DMC_HIP_X_KERNEL: upload x with a kernel instead of a copy-engine transfer
+    hipEvent_t tev[3] = {};  // DMC_HIP_TIME: before x, before the kernels, after them
     Stats st;
 };
 
@@ -202,7 +208,29 @@ int ensure_init() {
     if (hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking) != hipSuccess)
         return fail(DMC_HIP_ENODEV, "hipStreamCreate failed");
     if (hipMalloc(&c.dummy, 256) != hipSuccess) return fail(DMC_HIP_ENODEV, "hipMalloc failed");
+    c.weights = new dmc::Residency(
+        kMaxResident,
+        [](void **p, size_t bytes) -> int {
+            const hipError_t e = hipMalloc(p, bytes);
+            if (e == hipErrorOutOfMemory) {
+                (void)hipGetLastError();
+                return dmc::Residency::kOom;
+            }
+            return e == hipSuccess ? DMC_HIP_OK : hip_fail(e, "hipMalloc(weight)");
+        },
+        [](void *p) -> int {
+            const hipError_t e = hipFree(p);
+            return e == hipSuccess ? DMC_HIP_OK : hip_fail(e, "hipFree(weight)");
+        },
+        []() -> int {
+            const hipError_t e = hipStreamSynchronize(ctx().stream);
+            return e == hipSuccess ? DMC_HIP_OK : hip_fail(e, "hipStreamSynchronize");
+        });
     c.timing = env_flag("DMC_HIP_TIME");
+    if (c.timing) c.time_every = (uint64_t)std::max(0LL, atoll(getenv("DMC_HIP_TIME")));
+    for (hipEvent_t &ev : c.tev)
+        if (c.timing && hipEventCreate(&ev) != hipSuccess) c.timing = false;
+    c.x_kernel = env_flag("DMC_HIP_X_KERNEL");
     c.ok = true;
     return DMC_HIP_OK;
 }
@@ -270,27 +298,14 @@ int stage(Buf &b, size_t &off, size_t need, unsigned flags, char **out, char **d
     return DMC_HIP_OK;
 }
 
-int release_weights_locked() {
-    Ctx &c = ctx();
-    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
-    for (auto &kv : c.weights) HIP_TRY(hipFree(kv.second), "hipFree(weight)");
-    c.weights.clear();
-    c.resident_bytes = 0;
-    return DMC_HIP_OK;
-}
+int release_weights_locked() { return ctx().weights->release_all(); }
 
-// hipMalloc with the residency policy: on out-of-memory, drop every resident
-// weight once and retry.
-int weight_alloc(void **d, size_t bytes) {
-    hipError_t e = hipMalloc(d, bytes);
-    if (e == hipErrorOutOfMemory) {
-        (void)hipGetLastError();
-        int rc = release_weights_locked();
-        if (rc) return rc;
-        e = hipMalloc(d, bytes);
-    }
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc(weight)");
-    return DMC_HIP_OK;
+// The residency policy's answer as a library code.
+int residency_rc(int rc, int64_t bytes) {
+    if (rc == dmc::Residency::kOom)
+        return fail(DMC_HIP_ENOMEM, "no device memory for a %lld-byte weight (after releasing the cached ones)",
+                    (long long)bytes);
+    return rc;
 }
 
 // Device copy of the host weight [host, host+bytes), uploading on a miss.
@@ -298,8 +313,12 @@ int weight_alloc(void **d, size_t bytes) {
 // is W^T [t_cols, t_rows]: the drop-in x @ W keeps its weight in the row-dot
 // layout, whose kernel needs one launch where the column-stream layout needs
 // two.  The layout and the column count are part of the key, so the same
-// bytes used through another entry or shape get their own copy.
-int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, int64_t t_cols = 0) {
+// bytes used through another entry or shape get their own copy.  `pin`:
+// the caller keeps the device address (dmc_hip_register_weight), so no
+// eviction may free this entry (residency.h).  DMC_HIP_RESIDENT_CAP (bytes)
+// caps what may stay resident.
+int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, int64_t t_cols = 0,
+             bool pin = false) {
     Ctx &c = ctx();
     if (bytes <= 0) {
         *dev = c.dummy;
@@ -310,19 +329,16 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     if (t_rows > 0) key.b = mix64(key.b ^ 0x7472616e73706f73ULL ^ ((uint64_t)t_cols * 0x9E3779B97F4A7C15ULL));
     auto t1 = std::chrono::steady_clock::now();
     c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
-    auto it = c.weights.find(key);
-    if (it != c.weights.end()) {
-        *dev = it->second;
+    if (void *hit = c.weights->find(key, pin)) {
+        *dev = hit;
         return DMC_HIP_OK;
     }
-    if ((int)c.weights.size() >= kMaxResident) {
-        int rc = release_weights_locked();
-        if (rc) return rc;
-    }
+    const char *cap_s = getenv("DMC_HIP_RESIDENT_CAP");
+    const int64_t cap = cap_s && *cap_s ? strtoll(cap_s, nullptr, 10) : 0;
     void *d = nullptr, *raw = nullptr;
-    int rc = weight_alloc(&d, (size_t)(bytes + dmc::kWeightSlack));  // slack: see RdProblem::w_slack
+    int rc = residency_rc(c.weights->reserve(bytes, dmc::kWeightSlack, cap, &d), bytes);  // slack: see RdProblem::w_slack
     if (rc) return rc;
-    if (t_rows > 0 && (rc = weight_alloc(&raw, (size_t)bytes))) {
+    if (t_rows > 0 && (rc = residency_rc(c.weights->reserve_scratch((size_t)bytes, &raw), bytes))) {
         (void)hipFree(d);
         return rc;
     }
@@ -336,15 +352,14 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
         (void)hipFree(d);
         return hip_fail(e, "weight upload");
     }
-    c.weights.emplace(key, d);
-    c.resident_bytes += bytes;
+    c.weights->insert(key, d, bytes, pin);
     c.st.uploads++;
     c.st.upload_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                           std::chrono::steady_clock::now() - t1)
                           .count();
     if (env_flag("DMC_HIP_DEBUG"))
-        fprintf(stderr, "[hip] upload #%zu %lld MB%s\n", c.weights.size(), (long long)(bytes >> 20),
-                raw ? " (transposed)" : "");
+        fprintf(stderr, "[hip] upload #%zu %lld MB%s%s\n", c.weights->count(), (long long)(bytes >> 20),
+                raw ? " (transposed)" : "", pin ? " (pinned)" : "");
     *dev = d;
     return DMC_HIP_OK;
 }
@@ -381,17 +396,51 @@ void stats_line(int64_t k, int64_t n) {
     Stats &s = c.st;
     if (!c.timing) return;
     // The lm-head GEMV (the only n >= 100k call) closes a decode step, the
-    // delimiter of the reference's DMC_GPU_TIME line (gpu.rs:681-683).
-    if (n < 100000 && s.calls % 1024 != 0) return;
+    // delimiter of the reference's DMC_GPU_TIME line (gpu.rs:681-683); with
+    // DMC_HIP_TIME=N (N > 1) a line every N calls instead.
+    if (c.time_every > 1 ? s.calls % c.time_every != 0 : (n < 100000 && s.calls % 1024 != 0)) return;
     fprintf(stderr,
-            "[hip] calls=%llu stage=%lluus key=%lluus upload=%lluus(%llu) enqueue=%lluus "
-            "wait=%lluus readback=%lluus (last k=%lld n=%lld)\n",
+            "[hip] step: calls=%llu stage=%lluus key=%lluus upload=%lluus(%llu) enqueue=%lluus "
+            "wait=%lluus (gpu x=%lluus kernels=%lluus over %llu timed) readback=%lluus (last k=%lld n=%lld)\n",
             (unsigned long long)s.calls, (unsigned long long)(s.stage_ns / 1000),
             (unsigned long long)(s.key_ns / 1000), (unsigned long long)(s.upload_ns / 1000),
             (unsigned long long)s.uploads, (unsigned long long)(s.enqueue_ns / 1000),
-            (unsigned long long)(s.wait_ns / 1000), (unsigned long long)(s.readback_ns / 1000),
-            (long long)k, (long long)n);
+            (unsigned long long)(s.wait_ns / 1000), (unsigned long long)(s.gpu_x_ns / 1000),
+            (unsigned long long)(s.gpu_k_ns / 1000), (unsigned long long)s.timed,
+            (unsigned long long)(s.readback_ns / 1000), (long long)k, (long long)n);
+    for (const ShapeStats &b : s.shapes) {
+        const double bytes = (double)b.calls * 2.0 * (double)b.k * (double)b.n * (double)b.batch;
+        fprintf(stderr, "[hip]   k=%lld n=%lld b=%lld: %llu calls wait=%lluus gpu=%lluus  %.1f GB/s\n",
+                (long long)b.k, (long long)b.n, (long long)b.batch, (unsigned long long)b.calls,
+                (unsigned long long)(b.wait_ns / 1000), (unsigned long long)(b.gpu_ns / 1000),
+                b.gpu_ns ? bytes / (double)b.gpu_ns : 0.0);
+    }
     s = Stats{};
+}
+
+// One synchronous call's device times (events recorded around its work).
+void stats_call(int64_t k, int64_t n, int64_t batch, uint64_t wait_ns) {
+    Ctx &c = ctx();
+    float x_ms = 0.0f, k_ms = 0.0f;
+    if (hipEventElapsedTime(&x_ms, c.tev[0], c.tev[1]) != hipSuccess ||
+        hipEventElapsedTime(&k_ms, c.tev[1], c.tev[2]) != hipSuccess) {
+        (void)hipGetLastError();
+        return;
+    }
+    Stats &s = c.st;
+    const uint64_t gx = (uint64_t)(x_ms * 1e6f), gk = (uint64_t)(k_ms * 1e6f);
+    s.gpu_x_ns += gx;
+    s.gpu_k_ns += gk;
+    s.timed++;
+    for (ShapeStats &b : s.shapes) {
+        if (b.k == k && b.n == n && b.batch == batch) {
+            b.calls++;
+            b.wait_ns += wait_ns;
+            b.gpu_ns += gk;
+            return;
+        }
+    }
+    s.shapes.push_back(ShapeStats{k, n, batch, 1, wait_ns, gk});
 }
 
 bool valid_dims(int64_t m, int64_t k, int64_t n) {
@@ -426,8 +475,8 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
         if (rc) return rc;
     }
     auto t0 = std::chrono::steady_clock::now();
-    char *hx = nullptr, *hy = nullptr, *hy_dev = nullptr;
-    if ((rc = stage(c.hx, c.hx_off, x_bytes, hipHostMallocDefault, &hx))) return rc;
+    char *hx = nullptr, *hx_dev = nullptr, *hy = nullptr, *hy_dev = nullptr;
+    if ((rc = stage(c.hx, c.hx_off, x_bytes, hipHostMallocDefault, &hx, &hx_dev))) return rc;
     if ((rc = stage(c.hy, c.hy_off, y_bytes, hipHostMallocCoherent, &hy, &hy_dev))) return rc;
     // A small y is written by the kernel straight into its pinned staging
     // slice (saves a device-to-host copy launch, ~4 us of a ~45 us call); a
@@ -438,8 +487,15 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if ((rc = ensure_dev(c.dx, x_bytes ? x_bytes : 4))) return rc;
     if (!y_direct && (rc = ensure_dev(c.dy, y_bytes))) return rc;
     float *const ydst = static_cast<float *>(y_direct ? static_cast<void *>(hy_dev) : c.dy.p);
-    if (x_bytes)
-        HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
+    const bool timed = c.timing && !defer;
+    if (timed) HIP_TRY(hipEventRecord(c.tev[0], c.stream), "hipEventRecord");
+    if (x_bytes) {
+        if (c.x_kernel) {
+            HIP_TRY(dmc::launch_copy_from_host(c.dx.p, hx_dev, (int64_t)x_bytes, c.stream), "x upload");
+        } else {
+            HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
+        }
+    }
     c.st.stage_ns += ns_since(t0);
 
     // x @ W with one slice runs on the row-dot kernel over a transposed
@@ -451,6 +507,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if ((rc = cs_as_rd ? resident(r, (int64_t)w_bytes, &dw, k, n) : resident(r, (int64_t)w_bytes, &dw))) return rc;
 
     auto t1 = std::chrono::steady_clock::now();
+    if (timed) HIP_TRY(hipEventRecord(c.tev[1], c.stream), "hipEventRecord");
     hipError_t e;
     if (rd || cs_as_rd) {
         dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
@@ -468,6 +525,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     if (!y_direct)
         HIP_TRY(hipMemcpyAsync(hy, c.dy.p, y_bytes, hipMemcpyDeviceToHost, c.stream), "y readback");
+    if (timed) HIP_TRY(hipEventRecord(c.tev[2], c.stream), "hipEventRecord");
     c.st.enqueue_ns += ns_since(t1);
     c.st.calls++;
     if (defer) {
@@ -475,8 +533,10 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
         return DMC_HIP_OK;
     }
     auto t2 = std::chrono::steady_clock::now();
-    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
-    c.st.wait_ns += ns_since(t2);
+    HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    const uint64_t wait_ns = (uint64_t)ns_since(t2);
+    c.st.wait_ns += wait_ns;
+    if (timed) stats_call(k, n, batch, wait_ns);
     auto t3 = std::chrono::steady_clock::now();
     for (const Pending &p : c.pending) memcpy(p.dst, p.src, p.bytes);
     c.pending.clear();
@@ -488,12 +548,16 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     return DMC_HIP_OK;
 }
 
+int run_host_locked(bool rd, int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n, int64_t batch,
+                    int64_t ls, int64_t rs, bool defer) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return run_host(rd, reinterpret_cast<const float *>(l), reinterpret_cast<const uint16_t *>(r),
+                    reinterpret_cast<float *>(out), m, k, n, batch, ls, rs, defer);
+}
+
 void run_host_or_die(const char *entry, bool rd, int64_t l, int64_t r, int64_t out, int64_t m,
                      int64_t k, int64_t n, int64_t batch, int64_t ls, int64_t rs, bool defer) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    int rc = run_host(rd, reinterpret_cast<const float *>(l), reinterpret_cast<const uint16_t *>(r),
-                      reinterpret_cast<float *>(out), m, k, n, batch, ls, rs, defer);
-    if (rc) fatal(entry);
+    if (run_host_locked(rd, l, r, out, m, k, n, batch, ls, rs, defer)) fatal(entry);
 }
 
 
@@ -729,6 +793,37 @@ void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t
     run_host_or_die("dmc_matmul_bf16_gpu_t", true, l, r, out, m, k, n, 1, 0, 0, false);
 }
 
+// ---- error-returning forms of the drop-in entries ------------------------------
+//
+// Same arguments and results; a failure returns DMC_HIP_E* (message in
+// dmc_hip_last_error) with `out` untouched -- the kernel writes pinned
+// staging, copied to `out` only after the stream has completed -- so the
+// caller can compute the call on its own CPU kernel, as the reference does
+// when its device path is unavailable (gpu.rs:327-332, gpu.rs:483-486).
+
+int32_t dmc_matmul_bf16_gpu_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    return run_host_locked(false, l, r, out, m, k, n, 1, 0, 0, false);
+}
+
+int32_t dmc_matmul_bf16_gpu_t_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    return run_host_locked(true, l, r, out, m, k, n, 1, 0, 0, false);
+}
+
+int32_t dmc_matmul_bf16_gpu_batched_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n,
+                                        int64_t batch, int64_t ls, int64_t rs) {
+    return run_host_locked(false, l, r, out, m, k, n, batch, ls, rs, false);
+}
+
+int32_t dmc_matmul_bf16_gpu_batched_deferred_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k,
+                                                 int64_t n, int64_t batch, int64_t ls, int64_t rs) {
+    return run_host_locked(false, l, r, out, m, k, n, batch, ls, rs, true);
+}
+
+int32_t dmc_matmul_bf16_gpu_flush_try(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return flush_locked();
+}
+
 // ---- additions ----------------------------------------------------------------
 
 int32_t dmc_hip_available(void) {
@@ -811,7 +906,7 @@ int64_t dmc_hip_register_weight(int64_t host_ptr, int64_t bytes) {
     if (bytes <= 0 || !host_ptr) return fail(DMC_HIP_EINVAL, "bad weight range"), 0;
     if (ensure_init()) return 0;
     void *d = nullptr;
-    if (resident(reinterpret_cast<const void *>(host_ptr), bytes, &d)) return 0;
+    if (resident(reinterpret_cast<const void *>(host_ptr), bytes, &d, 0, 0, true)) return 0;
     return reinterpret_cast<int64_t>(d);
 }
 
@@ -826,12 +921,12 @@ int32_t dmc_hip_release_weights(void) {
 
 int64_t dmc_hip_resident_count(void) {
     std::lock_guard<std::mutex> lk(g_mu);
-    return (int64_t)ctx().weights.size();
+    return ctx().weights ? (int64_t)ctx().weights->count() : 0;
 }
 
 int64_t dmc_hip_resident_bytes(void) {
     std::lock_guard<std::mutex> lk(g_mu);
-    return ctx().resident_bytes;
+    return ctx().weights ? ctx().weights->bytes() : 0;
 }
 
 int32_t dmc_hip_gemv_cs(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n,

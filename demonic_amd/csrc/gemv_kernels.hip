@@ -145,6 +145,69 @@ __device__ __forceinline__ u32x4 load_w16(__amdgpu_buffer_rsrc_t r, uint32_t lan
 __device__ __forceinline__ float widen_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// ---- zero outputs of the FMA kernels ------------------------------------------
+//
+// The FMA kernels split k, so an output is a sum of partial chains.  When that
+// sum comes out exactly 0 it can differ from the reference chain (fmaf over
+// ascending k from +0, jit.rs:29655-29670): a run of underflowing products of
+// both signs leaves the chain at the zero of the last one's sign, where a sum
+// of reordered partials is -0 only if every partial is; and reordered partials
+// can cancel exactly where the chain keeps a subnormal residue.  So a zero
+// output is settled by the reference's own rule: +0 when its activation row
+// holds only +-0 (every product is an exact zero and the chain never leaves
+// +0), otherwise the chain itself -- which also gives +0 for an all-zero
+// weight row.  The common path costs one compare and one ballot per output.
+
+// The reference chain for one output: K products x[k] * w[k * wstep], any
+// alignment (2- and 4-byte loads; the rare path only).
+__device__ float chain_strided(const uint16_t *__restrict__ w, int64_t wstep,
+                                            const float *__restrict__ x, int K) {
+    float acc = 0.0f;
+    int k = 0;
+    for (; k + 4 <= K; k += 4) {
+        const uint16_t *p = w + (int64_t)k * wstep;
+        const uint32_t b0 = p[0], b1 = p[wstep], b2 = p[2 * wstep], b3 = p[3 * wstep];
+        const float x0 = x[k], x1 = x[k + 1], x2 = x[k + 2], x3 = x[k + 3];
+        acc = fmaf(x0, __uint_as_float(b0 << 16), acc);
+        acc = fmaf(x1, __uint_as_float(b1 << 16), acc);
+        acc = fmaf(x2, __uint_as_float(b2 << 16), acc);
+        acc = fmaf(x3, __uint_as_float(b3 << 16), acc);
+    }
+    for (; k < K; ++k) acc = fmaf(x[k], __uint_as_float((uint32_t)w[(int64_t)k * wstep] << 16), acc);
+    return acc;
+}
+
+__device__ __forceinline__ const float *readlane_ptr(const float *p, int j) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, j);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), j);
+    return reinterpret_cast<const float *>(((uint64_t)hi << 32) | lo);
+}
+
+// The zero rule for the outputs this wave holds, one per lane: `zero` marks a
+// lane whose output s is exactly 0 and is stored; x is its activation row,
+// w its first weight, wstep the elements between consecutive k.  All 64 lanes
+// call it (wave-uniform control flow): an activation row is scanned by the
+// whole wave, the chains run one per lane.
+__device__ float settle_zero(float s, bool zero, const float *x, const uint16_t *w, int64_t wstep, int K) {
+    uint64_t pend = __builtin_amdgcn_ballot_w64(zero);
+    if (pend == 0) return s;
+    const int lane = threadIdx.x & 63;
+    bool xnz = false;
+    while (pend) {
+        const int j = __builtin_ctzll(pend);
+        const float *xj = readlane_ptr(x, j);
+        uint32_t acc = 0;
+        for (int c = lane; c < K; c += 64) acc |= __float_as_uint(xj[c]) & 0x7fffffffu;
+        const bool nz = __builtin_amdgcn_ballot_w64(acc != 0) != 0;
+        const bool same = zero && x == xj;
+        if (same) xnz = nz;
+        pend &= ~__builtin_amdgcn_ballot_w64(same);
+    }
+    if (zero) s = xnz ? chain_strided(w, wstep, x, K) : 0.0f;
+    return s;
+}
+
 // ---- RD streaming: W [N,K], 16-byte aligned rows, K <= 32768 ------------------
 //
 // One launch serves up to kMaxGroup independent problems sharing K and M
@@ -309,12 +372,16 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
         sum_rows(ba, i0 + 2 * ROWS);
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < MT * nr; t += 64 * NW) {
-        const int m = t / nr, r = t - m * nr;
+    for (int t0 = wave * 64; t0 < MT * nr; t0 += 64 * NW) {  // wave-uniform: settle_zero needs whole waves
+        const int t = t0 + lane;
+        const bool live = t < MT * nr;
+        const int m = live ? t / nr : 0, r = live ? t - m * nr : 0;
         float s = red[0][m][r];
 #pragma unroll
         for (int w = 1; w < NW; ++w) s += red[w][m][r];
-        if (m < mrows) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
+        const bool store = live && m < mrows;
+        s = settle_zero(s, store && s == 0.0f, X + (int64_t)(m0 + m) * K, W + (int64_t)(rb + r) * ldw, 1, K);
+        if (store) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
     }
 }
 
@@ -430,15 +497,16 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
         sum_rows(ba, i0 + 2 * ROWS);
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < 2 * hrows; t += 1024) {
-        const int h = t / hrows, r = t - h * hrows;
+    for (int t0 = wid * 64; t0 < 2 * hrows; t0 += 1024) {  // wave-uniform: settle_zero needs whole waves
+        const int t = t0 + lane;
+        const int h = t < 2 * hrows ? t / hrows : 0, r = t < 2 * hrows ? t - h * hrows : 0;
         const int row = (int)blockIdx.x * rpw + h * hrows + r;
-        if (row < N) {
-            float s = red[h][0][r];
+        const bool store = t < 2 * hrows && row < N;
+        float s = red[h][0][r];
 #pragma unroll
-            for (int w = 1; w < NW; ++w) s += red[h][w][r];
-            Y[row] = s;
-        }
+        for (int w = 1; w < NW; ++w) s += red[h][w][r];
+        s = settle_zero(s, store && s == 0.0f, X, W + (int64_t)(store ? row : 0) * K, 1, K);
+        if (store) Y[row] = s;
     }
 }
 
@@ -463,10 +531,17 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 // included, become bf16 -0.0 (0x8000); their x is +0.0 (read past the end of
 // x), so each such product is -0.0f, the exact additive identity, and padding
 // never turns a -0.0f chain into +0.0f.  M == 1.
+//
+// Short tail: the windows cover elements [0, kmain); the 1 to 8 elements
+// [kmain, K) past the last whole block of windows (K = 4097: one) are one
+// more unaligned load per row, issued once per workgroup before the stream
+// starts by lane r of the last wave for row rb + r, and summed by that lane
+// into a ninth partial.  A last block holding one element would otherwise
+// double every lane's loads for it (K = 4097 measured 53% of peak that way).
 template <int NW, int KV, int ROWS>
 __global__ void __launch_bounds__(64 * NW)
 gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
-                         int K, int64_t ldw, int rpw, int tail) {
+                         int K, int kmain, int64_t ldw, int rpw, int tail) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = (int)blockIdx.x * rpw;
@@ -478,23 +553,6 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
         weight_rsrc(reinterpret_cast<const void *>(base), (uint32_t)((end - base + tail + 3) & ~(uintptr_t)3));
     const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4u);
 
-    uint32_t coff[KV];
-    uint32_t mask[KV][4];
-    u32x4 xa[KV], xb[KV];
-#pragma unroll
-    for (int j = 0; j < KV; ++j) {
-        const int p = (j * NW + wave) * 64 + lane;
-        const int valid = min(max(K - 8 * p, 0), 8);  // elements of window p inside the row
-        coff[j] = valid > 0 ? (uint32_t)p * 16u : kOutOfRange;
-#pragma unroll
-        for (int d = 0; d < 4; ++d)
-            mask[j][d] = (2 * d < valid ? 0x0000ffffu : 0u) | (2 * d + 1 < valid ? 0xffff0000u : 0u);
-        const uint32_t xo = valid > 0 ? (uint32_t)p * 32u : kOutOfRange;
-        xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
-        xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
-    }
-    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
-
     // Row r's first element, in bytes from the descriptor's base.  No branch on
     // r < re (a branch around a load address makes the compiler wait for every
     // load in flight): a row past re yields offsets at or past the range's end,
@@ -503,7 +561,32 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
         return (uint32_t)(reinterpret_cast<uintptr_t>(W + (int64_t)r * ldw) - base);
     };
 
-    __shared__ float red[NW][kMaxRpw];
+    // The short tail's loads (all lanes issue them; only lane r < nr of the
+    // last wave reads memory), oldest of all, so the first wait covers them.
+    const bool tail_lane = kmain < K && wave == NW - 1 && lane < re - rb;
+    const u32x4 tw = load_w16(rs, tail_lane ? row_off(rb + lane) + (uint32_t)kmain * 2u : kOutOfRange);
+    const uint32_t txo = tail_lane ? (uint32_t)kmain * 4u : kOutOfRange;
+    const u32x4 txa = __builtin_amdgcn_raw_buffer_load_b128(xrs, txo, 0, 0);
+    const u32x4 txb = __builtin_amdgcn_raw_buffer_load_b128(xrs, txo + 16u, 0, 0);
+
+    uint32_t coff[KV];
+    uint32_t mask[KV][4];
+    u32x4 xa[KV], xb[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int p = (j * NW + wave) * 64 + lane;
+        const int valid = min(max(kmain - 8 * p, 0), 8);  // elements of window p inside the row
+        coff[j] = valid > 0 ? (uint32_t)p * 16u : kOutOfRange;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+            mask[j][d] = (2 * d < valid ? 0x0000ffffu : 0u) | (2 * d + 1 < valid ? 0xffff0000u : 0u);
+        const uint32_t xo = valid > 0 ? (uint32_t)p * 32u : kOutOfRange;
+        xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+        xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
+    }
+    const float init = (wave * 64 + lane) * 8 < kmain ? 0.0f : -0.0f;
+
+    __shared__ float red[NW + 1][kMaxRpw];  // row NW: the short tail's partials
     u32x4 ba[ROWS][KV], bb[ROWS][KV];
     auto load = [&](u32x4 (&wv)[ROWS][KV], int r0) {
 #pragma unroll
@@ -522,12 +605,23 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
             xr[j][q] = __uint_as_float(xa[j][q]);
             xr[j][q + 4] = __uint_as_float(xb[j][q]);
         }
+    if (kmain < K && wave == NW - 1) {  // the short tail's partial, ascending k from +0
+        float t = 0.0f;
+        const int rem = K - kmain;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t mk = (2 * d < rem ? 0x0000ffffu : 0u) | (2 * d + 1 < rem ? 0xffff0000u : 0u);
+            const uint32_t v = (tw[d] & mk) | (~mk & 0x80008000u);
+            t = fmaf(__uint_as_float(d < 2 ? txa[2 * d] : txb[2 * d - 4]), widen_lo(v), t);
+            t = fmaf(__uint_as_float(d < 2 ? txa[2 * d + 1] : txb[2 * d - 3]), widen_hi(v), t);
+        }
+        if (lane < re - rb) red[NW][lane] = t;
+    }
 
-    // A wave whose windows of the last block all lie past K skips that block's
-    // arithmetic (a wave-uniform branch around arithmetic only; its loads, out
-    // of range, stay unconditional): k = 4097 then costs 1.125x the
-    // arithmetic of k = 4096 instead of 2x.
-    const bool last_block = (((KV - 1) * NW + wave) * 64) * 8 < K;
+    // A wave whose windows of the last block all lie past kmain skips that
+    // block's arithmetic (a wave-uniform branch around arithmetic only; its
+    // loads, out of range, stay unconditional).
+    const bool last_block = (((KV - 1) * NW + wave) * 64) * 8 < kmain;
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
@@ -555,11 +649,16 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
     }
     __syncthreads();
     const int nr = re - rb;
-    for (int t = threadIdx.x; t < nr; t += 64 * NW) {
-        float s = red[0][t];
+    for (int t0 = wave * 64; t0 < nr; t0 += 64 * NW) {  // wave-uniform: settle_zero needs whole waves
+        const int t = t0 + lane;
+        const bool store = t < nr;
+        const int i = store ? t : 0;
+        float s = red[0][i];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w][t];
-        Y[rb + t] = s;
+        for (int w = 1; w < NW; ++w) s += red[w][i];
+        if (kmain < K) s += red[NW][i];
+        s = settle_zero(s, store && s == 0.0f, X, W + (int64_t)(rb + i) * ldw, 1, K);
+        if (store) Y[rb + t] = s;
     }
 }
 
@@ -1431,12 +1530,16 @@ gemv_rd_kernel(const uint16_t *__restrict__ W, int64_t ldw, const float *__restr
             if (lane == 0) red[wave][m * ROWS + r] = s;
         }
     __syncthreads();
-    for (int i = threadIdx.x; i < MT * ROWS; i += kThreads) {
+    for (int i0 = wave * 64; i0 < MT * ROWS; i0 += kThreads) {  // wave-uniform: settle_zero needs whole waves
+        const int i = i0 + lane < MT * ROWS ? i0 + lane : 0;
         const int m = i / ROWS, r = i % ROWS;
         float s = red[0][i];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) s += red[w][i];
-        if (n0 + r < N && m0 + m < M) Y[(int64_t)(m0 + m) * ldy + n0 + r] = s;
+        const bool store = i0 + lane < MT * ROWS && n0 + r < N && m0 + m < M;
+        s = settle_zero(s, store && s == 0.0f, X + (int64_t)(store ? m0 + m : 0) * ldx,
+                        W + (int64_t)(store ? n0 + r : 0) * ldw, 1, K);
+        if (store) Y[(int64_t)(m0 + m) * ldy + n0 + r] = s;
     }
 }
 
@@ -1517,13 +1620,21 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
             for (int e = 0; e < VEC; ++e) red[wave][m][cl * VEC + e] = acc[m][e];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < MT * CB; i += kThreads) {
+    // With one k slice P is y itself and the zero rule applies here;
+    // otherwise sum_slices_kernel applies it to the slices' sum.
+    const bool final_out = kslice >= K;
+    for (int i0 = wave * 64; i0 < MT * CB; i0 += kThreads) {  // wave-uniform: settle_zero needs whole waves
+        const int i = i0 + lane < MT * CB ? i0 + lane : 0;
         const int m = i / CB, c = i % CB;
         const int n = blockIdx.x * CB + c;
         float s = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) s += red[w][m][c];
-        if (n < N && m < M) pz[(int64_t)m * N + n] = s;
+        const bool store = i0 + lane < MT * CB && n < N && m < M;
+        if (final_out)
+            s = settle_zero(s, store && s == 0.0f, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? n : 0),
+                            N, K);
+        if (store) pz[(int64_t)m * N + n] = s;
     }
 }
 
@@ -1640,33 +1751,53 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
 
     const int c0 = cb * kCsCols;
     const int ncol = min(kCsCols, N - c0);
-    float *out = slices == 1 && !UN ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
-    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {
+    // With one k slice (and every row in it) the workgroup writes y and the
+    // zero rule applies here; otherwise sum_slices_stream_kernel applies it.
+    const bool final_out = slices == 1 && !UN;
+    float *out = final_out ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
+    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {  // wave-uniform: MT * 512 is a multiple of 64 * NW
         const int m = t / kCsCols, c = t - m * kCsCols;
-        if (m >= M || c >= ncol) continue;
+        const bool store = m < M && c < ncol;
         float v = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < NW; ++w) v += red[w][m][c];
-        out[(int64_t)m * N + c0 + c] = v;
+        if (final_out)
+            v = settle_zero(v, store && v == 0.0f, xz + (int64_t)(store ? m : 0) * K,
+                            W + z * rs + (store ? c0 + c : 0), N, K);
+        if (store) out[(int64_t)m * N + c0 + c] = v;
     }
 }
 
-// Second pass of the streaming column-stream kernel: y[i] = sum over slices
-// of P[j][i] in ascending j.  A workgroup owns 64 consecutive outputs; its 4
-// waves take slices j = w, w+4, ... (coalesced 256-byte reads), and the four
-// partial sums meet in LDS in wave order.  Every element's order is fixed.
-//
-// With `last` set (the UN streaming kernel left out the matrix's last row):
-// y[i] = fmaf(x[z][m][K-1], w[z][K-1][n], that sum), the chain's final step.
-struct LastRow {
-    const uint16_t *w;  // slice z's row K-1: w + z*rs
-    const float *x;     // x[z][m][K-1]: x + z*ls + m*K
+// Second pass of the column-stream kernels: y[i] = sum over slices of
+// P[j][i] in ascending j, then the zero rule (settle_zero).  `src` names the
+// problem, so an output's activation row and weight column can be found:
+// output i of the launch is (slice z, activation row m, column n) =
+// (i / (M*N), (i / N) % M, i % N), its activation row x + z*ls + m*K, its
+// weights w + z*rs + n, N elements apart.
+struct CsSrc {
+    const uint16_t *w;
+    const float *x;
     int64_t rs, ls, K, N, M;
+    bool last_row;  // the UN streaming kernel left out row K-1 (below)
 };
 
+__device__ __forceinline__ float cs_settle(float v, bool live, int64_t i, const CsSrc &src) {
+    const int64_t mn = src.M * src.N;
+    const int64_t z = live ? i / mn : 0, r = live ? i - z * mn : 0;
+    const int64_t m = r / src.N, n = r - m * src.N;
+    return settle_zero(v, live && v == 0.0f, src.x + z * src.ls + m * src.K, src.w + z * src.rs + n, src.N,
+                       (int)src.K);
+}
+
+// The streaming kernel's pass.  A workgroup owns 64 consecutive outputs; its
+// 4 waves take slices j = w, w+4, ... (coalesced 256-byte reads), and the four
+// partial sums meet in LDS in wave order.  Every element's order is fixed.
+// With `last_row` set (the UN streaming kernel left out the matrix's last
+// row): y[i] = fmaf(x[z][m][K-1], w[z][K-1][n], that sum), the chain's final
+// step.
 __global__ void __launch_bounds__(256)
 sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
-                         int64_t count, const LastRow last) {
+                         int64_t count, const CsSrc src) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
@@ -1683,27 +1814,51 @@ sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slice
     __shared__ float part[4][64];
     part[wave][lane] = s;
     __syncthreads();
-    if (wave == 0 && i < count) {
+    if (wave == 0) {  // wave-uniform: settle_zero needs whole waves
+        const bool live = i < count;
         float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
-        if (last.w) {
-            const int64_t z = i / (last.M * last.N), r = i - z * last.M * last.N;
-            const int64_t m = r / last.N, n = r - m * last.N;
-            const float xv = last.x[z * last.ls + m * last.K];
-            v = fmaf(xv, __uint_as_float((uint32_t)last.w[z * last.rs + n] << 16), v);
+        if (src.last_row && live) {
+            const int64_t z = i / (src.M * src.N), r = i - z * src.M * src.N;
+            const int64_t m = r / src.N, n = r - m * src.N;
+            const float xv = src.x[z * src.ls + m * src.K + (src.K - 1)];
+            v = fmaf(xv, __uint_as_float((uint32_t)src.w[z * src.rs + (src.K - 1) * src.N + n] << 16), v);
         }
-        Y[i] = v;
+        v = cs_settle(v, live, i, src);
+        if (live) Y[i] = v;
     }
 }
 
-// Second CS pass: y[i] = sum over slices in ascending order of P[s][i].
+// The general kernel's pass: y[i] = sum over slices in ascending order of
+// P[s][i], then the zero rule.
 __global__ void __launch_bounds__(kThreads)
 sum_slices_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
-                  int64_t count) {
+                  int64_t count, const CsSrc src) {
     const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    if (i >= count) return;
-    float s = P[i];
-    for (int j = 1; j < slices; ++j) s += P[(int64_t)j * p_slice + i];
-    Y[i] = s;
+    const bool live = i < count;
+    float s = 0.0f;
+    if (live) {
+        s = P[i];
+        for (int j = 1; j < slices; ++j) s += P[(int64_t)j * p_slice + i];
+    }
+    s = cs_settle(s, live, i, src);
+    if (live) Y[i] = s;
+}
+
+// ---- activation upload --------------------------------------------------------
+//
+// The drop-in entries stage x in pinned host memory; one small grid reads it
+// over PCIe (16 bytes per thread where aligned, else 4) into device memory.
+__global__ void __launch_bounds__(256)
+copy_from_host_kernel(uint32_t *__restrict__ dst, const uint32_t *__restrict__ src, int64_t words, bool v4) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    if (v4) {
+        const int64_t n4 = words / 4;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride)
+            reinterpret_cast<uint4 *>(dst)[i] = reinterpret_cast<const uint4 *>(src)[i];
+        for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += stride) dst[i] = src[i];
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < words; i += stride) dst[i] = src[i];
+    }
 }
 
 // ---- measurement probe -------------------------------------------------------
@@ -1995,7 +2150,8 @@ hipError_t rd_unaligned_go(const RdProblem &p, const RdPlan &pl, hipStream_t s) 
     constexpr int ROWS = (KV <= 4 && KV != 2) ? 2 : 1;
     if (pl.rows != ROWS) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemv_rd_unaligned_kernel<NW, KV, ROWS>), dim3((unsigned)pl.grid_x), dim3(64 * NW), 0, s, p.w,
-                       p.x, p.y, (int)p.n, (int)p.k, p.ldw, pl.rpw, p.w_slack >= 2 ? 2 : 0);
+                       p.x, p.y, (int)p.n, (int)p.k, (int)(pl.kmain > 0 ? pl.kmain : p.k), p.ldw, pl.rpw,
+                       p.w_slack >= 2 ? 2 : 0);
     return hipGetLastError();
 }
 
@@ -2293,12 +2449,14 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // N = 4097 would leave a 257th workgroup to start after the others
             // (17.3 us against 15.7 on 8-wave workgroups).
             const int64_t g16 = (p.n + 15) / 16;
-            if (p.m == 1 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 && sp.rows == 2 &&
-                p.k <= kXldsMaxK && g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus) &&
-                env_int("DMC_HIP_RD_XLDS", 1) != 0) {
+            const int xl = env_int("DMC_HIP_RD_XLDS", 1);  // 0: never; 2: wherever the kernel applies
+            if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
+                p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) && xl != 0) {
+                int rpw = env_int("DMC_HIP_RD_XLDS_RPW", 16);
+                if (rpw != 8 && rpw != 16 && rpw != 32) rpw = 16;
                 sp.waves = 16;
-                sp.rpw = 16;
-                sp.grid_x = (p.n + 15) / 16;
+                sp.rpw = rpw;
+                sp.grid_x = (p.n + rpw - 1) / rpw;
             }
             return sp;
         }
@@ -2312,17 +2470,21 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     if (pl.vec < 8 && p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) && last_ok &&
         env_int("DMC_HIP_RD_UNALIGNED", 1) != 0) {
         const int nw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
-        const int kv = (int)((p.k + nw * 512 - 1) / (nw * 512));
+        const int64_t block = (int64_t)nw * 512;
+        // 1..8 elements past whole blocks of windows (k = 4097) go to each
+        // row's short tail; otherwise the last block holds the rest.
+        const int64_t rem = p.k % block;
+        const bool short_tail = p.k > block && rem >= 1 && rem <= 8 && env_int("DMC_HIP_RD_SHORT_TAIL", 1) != 0;
+        const int kv = short_tail ? (int)(p.k / block) : (int)((p.k + block - 1) / block);
         const int rpw_default = kv >= 2 ? 8 : 4;
         const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
         int rpw = rpw_default;
         while (rpw > 2 && (p.n + rpw - 1) / rpw < min_blocks) rpw >>= 1;
-        // Only when the last block of windows is at least half full: measured
-        // on MI355X against the general kernel, k = 4095 67% vs 57% of peak,
-        // 11007 64% vs 60%, 14335 64% vs 56%, but k = 4097 (one element in its
-        // last block) 53% vs 61%.
-        const int64_t block = (int64_t)nw * 512;
-        if (p.k - (kv - 1) * block >= block / 2 && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
+        // Only when the last block of windows is at least half full, or the
+        // rest is a short tail: measured on MI355X against the general
+        // kernel, k = 4095 67% vs 57% of peak, 11007 64% vs 60%, 14335 64% vs
+        // 56%, but k = 4097 as a one-element last block 53% vs 61%.
+        if ((short_tail || p.k - (kv - 1) * block >= block / 2) && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
             (p.n + rpw - 1) / rpw <= INT32_MAX) {
             RdPlan sp{};
             sp.vec = pl.vec;
@@ -2333,6 +2495,7 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             sp.rpw = rpw;
             sp.grid_x = (p.n + rpw - 1) / rpw;
             sp.grid_y = 1;
+            sp.kmain = short_tail ? kv * block : p.k;
             return sp;
         }
     }
@@ -2521,13 +2684,14 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
     }
     if (pl.kvec > 0 && pl.vec < 8) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0 && pl.waves == 16) {
-        if (pl.rows != 2 || pl.rpw != 16 || p.m != 1 || p.k > kXldsMaxK) return hipErrorInvalidValue;
+        if (pl.rows != 2 || (pl.rpw != 8 && pl.rpw != 16 && pl.rpw != 32) || p.m != 1 || p.k > kXldsMaxK)
+            return hipErrorInvalidValue;
 #define DMC_XLDS(KV)                                                                                          \
     case KV:                                                                                                  \
         hipLaunchKernelGGL((gemv_rd_stream_xlds_kernel<KV, 2>), dim3((unsigned)pl.grid_x), dim3(1024), 0, s, p.w, \
                            p.x, p.y, (int)p.n, (int)p.k, pl.rpw);                                             \
         return hipGetLastError();
-        switch (pl.kvec) { DMC_XLDS(2) DMC_XLDS(3) DMC_XLDS(4) }
+        switch (pl.kvec) { DMC_XLDS(1) DMC_XLDS(2) DMC_XLDS(3) DMC_XLDS(4) }
 #undef DMC_XLDS
         return hipErrorInvalidValue;
     }
@@ -2566,10 +2730,9 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
         }
         if (pl.slices > 1 || pl.unaligned) {
             const int64_t total = p.m * p.n * p.batch;
-            LastRow last{};
-            if (pl.unaligned) last = LastRow{p.w + (p.k - 1) * p.n, p.x + (p.k - 1), p.rs, p.ls, p.k, p.n, p.m};
+            const CsSrc src{p.w, p.x, p.rs, p.ls, p.k, p.n, p.m, pl.unaligned};
             hipLaunchKernelGGL(sum_slices_stream_kernel, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, s, P,
-                               total, (int)pl.slices, p.y, total, last);
+                               total, (int)pl.slices, p.y, total, src);
             return hipGetLastError();
         }
         return hipSuccess;
@@ -2589,14 +2752,26 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
     }
     if (pl.slices > 1) {
         const int64_t blocks = (total + kThreads - 1) / kThreads;
+        const CsSrc src{p.w, p.x, p.rs, p.ls, p.k, p.n, p.m, false};
         hipLaunchKernelGGL(sum_slices_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, s, P, p_slice,
-                           (int)pl.slices, p.y, total);
+                           (int)pl.slices, p.y, total, src);
         return hipGetLastError();
     }
     return hipSuccess;
 }
 
 size_t probe_sink_bytes() { return (size_t)kProbeGroups * 4; }
+
+hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t s) {
+    if (bytes <= 0) return hipSuccess;
+    if (bytes % 4 || !aligned(dst, 4) || !aligned(src, 4)) return hipErrorInvalidValue;
+    const int64_t words = bytes / 4;
+    const bool v4 = aligned(dst, 16) && aligned(src, 16);
+    const unsigned groups = (unsigned)std::min<int64_t>(64, std::max<int64_t>(1, (words / (v4 ? 4 : 1) + 255) / 256));
+    hipLaunchKernelGGL(copy_from_host_kernel, dim3(groups), dim3(256), 0, s, static_cast<uint32_t *>(dst),
+                       static_cast<const uint32_t *>(src), words, v4);
+    return hipGetLastError();
+}
 
 hipError_t launch_fill_counter_bf16(uint16_t *dst, int64_t count, int64_t offset, uint64_t key,
                                     const uint16_t *table, hipStream_t s) {

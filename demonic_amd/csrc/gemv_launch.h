@@ -68,6 +68,9 @@ struct RdPlan {
     // gemm layout (mkind 8): k split over `kslices` workgroups of `kchunks`
     // 64-element chunks each; workspace for x's bf16 planes and the partials
     int kslices = 1, kchunks = 0;
+    // streaming over misaligned rows: windows cover k < kmain, and the 1..8
+    // elements [kmain, k) are each row's short tail (0: kmain = k)
+    int64_t kmain = 0;
     size_t workspace_bytes = 0;
 };
 
@@ -126,6 +129,11 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hi
 // holds probe_sink_bytes().
 size_t probe_sink_bytes();
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
+
+// Copy `bytes` (a multiple of 4, both ends 4-byte aligned) from pinned host
+// memory to device memory with a kernel: the drop-in path's activation
+// upload, which a copy-engine transfer delays by its own scheduling.
+hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t stream);
 
 // dst [cols, rows] = src [rows, cols]^T for bf16 bit patterns (weight
 // residency in the row-dot layout, dmc_hip_bf16_transpose_2d).

@@ -212,10 +212,20 @@ def c3_rows(layer: int, idx: int, rows, seed: int = 0) -> np.ndarray:
     """Rows `rows` of projection idx of a layer, regenerated on the host
     (bit-identical to the device fill)."""
     _, n, k = LLAMA3_8B_LAYER[idx]
+    return counter_rows(seed, c3_tensor(layer, idx), rows, k, C3_SCALE)
+
+
+def counter_rows(seed: int, tensor: int, rows, k: int, scale: float = 0.02) -> np.ndarray:
+    """Rows `rows` [len(rows), k] of a counter-generated [N, k] tensor."""
     out = np.empty((len(rows), k), np.uint16)
     for j, r in enumerate(rows):
-        out[j] = counter_bf16(seed, c3_tensor(layer, idx), k, offset=int(r) * k, scale=C3_SCALE)
+        out[j] = counter_bf16(seed, tensor, k, offset=int(r) * k, scale=scale)
     return out
+
+
+# ---- C4: the LM head at full size, generated in HBM ----------------------------------
+
+C4_TENSOR = 900_000  # counter-generator tensor id of the full-size LM-head weight
 
 
 def counter_f32_normal(seed: int, tensor: int, count: int) -> np.ndarray:

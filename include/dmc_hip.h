@@ -45,7 +45,7 @@ extern "C" {
 
 /* ---- drop-in operator surface (compiler/src/gpu.rs) --------------------- */
 
-/* Replaces dmc_matmul_bf16_gpu (gpu.rs:391-408), same ABI as the CPU kernel
+/* Replaces dmc_matmul_bf16_gpu (gpu.rs:400-409), same ABI as the CPU kernel
  * dmc_matmul_bf16 (jit.rs:29488): out[m,n] = l[m,k] @ bf16(r[k,n]).
  * m == 0 or n == 0 returns without touching out (gpu.rs:402); k == 0 writes
  * +0.0 (jit.rs:29655).  Any m runs on the GPU (the reference sends m != 1 to
@@ -71,6 +71,31 @@ void dmc_matmul_bf16_gpu_batched_deferred(int64_t l, int64_t r, int64_t out, int
 /* Replaces dmc_matmul_bf16_gpu_flush (gpu.rs:468-474): materialize every
  * deferred call.  No-op when nothing is pending or before first use. */
 void dmc_matmul_bf16_gpu_flush(void);
+
+/* ---- error-returning forms of the drop-in entries ------------------------ */
+
+/* The five entries above abort the process on a device failure, because the
+ * reference's signatures return nothing.  The reference itself degrades to its
+ * CPU kernel instead: when device init fails (gpu.rs:327-332, 483-486) and for
+ * shapes it does not offload (gpu.rs:404-407, 500-507).  These forms let a
+ * caller do the same: identical arguments and results, but a failure returns
+ * DMC_HIP_E* (the message in dmc_hip_last_error) and leaves `out` untouched
+ * -- the kernel writes pinned staging, which is copied to `out` only once the
+ * stream has completed -- so the caller computes that call on its own CPU
+ * kernel (dmc_matmul_bf16, jit.rs:29488).  No CPU arithmetic happens in the
+ * library.  DMC_HIP_ENOMEM: no device memory for the weight even after the
+ * cached resident weights were released (DMC_HIP_RESIDENT_CAP, in bytes, caps
+ * resident weights, so this can be forced); DMC_HIP_ENODEV: no device, or
+ * DMC_HIP_DISABLE set.  The deferred form queues nothing when it fails.  The
+ * flush form returns the failure of materializing pending deferred calls;
+ * their outputs are then not written. */
+int32_t dmc_matmul_bf16_gpu_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+int32_t dmc_matmul_bf16_gpu_t_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+int32_t dmc_matmul_bf16_gpu_batched_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n,
+                                        int64_t batch, int64_t ls, int64_t rs);
+int32_t dmc_matmul_bf16_gpu_batched_deferred_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k,
+                                                 int64_t n, int64_t batch, int64_t ls, int64_t rs);
+int32_t dmc_matmul_bf16_gpu_flush_try(void);
 
 /* ---- additions for MI355X (no Metal counterpart) ------------------------ */
 

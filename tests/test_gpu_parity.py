@@ -180,6 +180,9 @@ SHAPES = [
     (1, 511, 7), (1, 512, 8), (1, 513, 9), (1, 1000, 33), (1, 2048, 1), (1, 4097, 37),
     (2, 64, 17), (3, 129, 31), (5, 1024, 100), (8, 520, 24), (16, 4096, 40),
     (17, 300, 11), (33, 96, 65), (1, 12288, 6),
+    # misaligned rows with a short tail past whole blocks of windows: one
+    # element (4097), two (4098), seven (8199, 12295: two and three blocks)
+    (1, 4097, 600), (1, 4098, 70), (1, 8199, 300), (1, 12295, 64),
 ]
 
 
@@ -213,7 +216,7 @@ def test_two_activation_rows_stream(hip, k, n):
 
 
 @pytest.mark.parametrize("offset,k,n", [(2, 4096, 300), (6, 4104, 257), (14, 2048, 33), (10, 777, 1000),
-                                        (4, 16384, 70), (2, 11007, 129)])
+                                        (4, 16384, 70), (2, 11007, 129), (2, 4097, 513), (6, 8192, 129)])
 def test_misaligned_weight_view(hip, offset, k, n):
     """W [n,k] starting `offset` bytes into its device region, which ends
     right after the last row: rows on 2-byte boundaries, windows re-aligned
@@ -280,6 +283,86 @@ def test_column_stream_batched_slices_at_odd_strides(hip):
     check(y, oracle.matmul_bf16_batched(x, w, k, n, batch, ls, rs), what="cs batched odd strides")
 
 
+def zero_rows(k, n=8):
+    """Activation rows x [4, k] and weight rows w [n, k] (bf16 bits) whose
+    products are all exact zeros or underflow -- so every device sum is
+    exactly +-0 and the reference chain decides the sign -- plus one row of
+    exact cancellation.  x: +1e-38, -1e-38, 1e-38 with every third negated,
+    all zero.  w: the smallest subnormal everywhere; the same with the last
+    product's sign flipped; then a zero product after the last nonzero one;
+    alternating signs; all zero; +1.0 at k = 0 against -1.0 at k = 3;
+    the first seven negative; -0 weights among positive tiny ones; past row
+    7, all negative tiny."""
+    x = np.full((4, k), np.float32(1e-38), np.float32)
+    x[1] = -x[1]
+    x[2, ::3] = -x[2, ::3]
+    x[3] = 0
+    w = np.full((max(n, 9), k), 0x0001, np.uint16)
+    if k:
+        w[1, k - 1] = 0x8001
+        w[2, k - 1] = 0x0000
+        w[3, 1::2] = 0x8001
+        w[4] = 0
+        w[5] = 0
+        if k >= 4:  # x[0] and x[3] are equal in every activation row
+            w[5, 0] = 0x3F80
+            w[5, 3] = 0xBF80
+        w[6, :7] = 0x8001
+        w[7, ::5] = 0x8000
+        w[8:] = 0x8001
+    return x, np.ascontiguousarray(w[:n])
+
+
+@pytest.mark.parametrize("n", [3, 8, 9])
+@pytest.mark.parametrize("m", [1, 2, 4])
+@pytest.mark.parametrize("k", [1, 7, 1001, 4096, 4097, 8199, 14336])
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_zero_outputs_follow_the_reference_chain(hip, k, m, n, layout):
+    """A split-k sum that comes out exactly zero is settled by the reference's
+    own chain (fmaf over ascending k from +0, jit.rs:29655-29670), so even the
+    order-dependent zeros -- underflowing products whose sign changes along k,
+    a +-0 product after the last nonzero one -- match bit for bit, through
+    every FMA kernel: row-dot streaming, unaligned (odd K, short tails) and general,
+    column-stream streaming (one slice or k split, odd N) and general (N = 3),
+    one to four activation rows (four on K = 4096 / 14336 take the MFMA
+    layout, which applies the same rule)."""
+    x, w = zero_rows(k, n)
+    x = np.ascontiguousarray(x[{1: [2], 2: [1, 2], 4: [0, 1, 2, 3]}[m]])
+    y_ref = ref(x, w)
+    assert np.all(y_ref == 0)
+    y = RUN[layout](hip, x, w)
+    bad = y.view(np.uint32) != y_ref.view(np.uint32)
+    assert not bad.any(), (np.argwhere(bad)[:8], y[bad][:8], y_ref[bad][:8])
+
+
+def test_zero_outputs_follow_the_reference_chain_batched_and_grouped(hip):
+    """The zero rule through the batched column-stream entry (two slices, odd
+    strides) and through a grouped row-dot launch of two problems."""
+    k, n = 4104, 9
+    x, w = zero_rows(k, n)
+    xb = np.concatenate([x[2], np.zeros(3, np.float32), x[1]])       # ls = k + 3
+    wt = np.ascontiguousarray(w.T).reshape(-1)
+    wb = np.concatenate([wt, np.zeros(5, np.uint16), wt[::-1].copy()])  # rs = k*n + 5
+    y = hip.matmul_bf16_gpu_batched(xb, wb, 1, k, n, 2, k + 3, k * n + 5)
+    y_ref = oracle.matmul_bf16_batched(xb, wb, k, n, 2, k + 3, k * n + 5)
+    assert np.array_equal(np.asarray(y).view(np.uint32), np.asarray(y_ref).view(np.uint32)), (y, y_ref)
+    ws = [w, np.ascontiguousarray(w[::-1])]
+    xs = [x[2:3].copy(), x[1:2].copy()]
+    dxs = [hip.DeviceBuffer.from_numpy(v) for v in xs]
+    dws = [hip.DeviceBuffer.from_numpy(v) for v in ws]
+    dys = [hip.DeviceBuffer(4 * n) for _ in ws]
+    try:
+        hip.gemv_rd_grouped(dxs, dws, dys, [n, n], 1, k)
+        hip.synchronize()
+        for i in range(2):
+            got = dys[i].download(np.float32, (n,))
+            want = ref(xs[i], ws[i])[0]
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (i, got, want)
+    finally:
+        for b in dxs + dws + dys:
+            b.free()
+
+
 @pytest.mark.parametrize("k", [1, 7, 1000, 1001, 4096, 14336])
 @pytest.mark.parametrize("layout", LAYOUTS)
 def test_underflowing_products_keep_their_zero_sign(hip, k, layout):
@@ -287,9 +370,8 @@ def test_underflowing_products_keep_their_zero_sign(hip, k, layout):
     (fmaf from +0.0, jit.rs:29655) ends at -0.0 -- and so does every other
     summation order, as long as the device's padding (lanes past K, windows
     past K, masked tails) adds only -0.0.  Row 1: the same products with the
-    opposite sign end at +0.0.  (A zero made of underflowing products of both
-    signs takes the sign of the last one in k order: that case is
-    order-dependent and not asserted.)"""
+    opposite sign end at +0.0.  (Products of both signs: see
+    test_zero_outputs_follow_the_reference_chain.)"""
     x = np.full((1, k), np.float32(-1e-38), np.float32)
     w = np.full((2, k), 0x0001, np.uint16)     # smallest bf16 subnormal: |x*w| ~ 9e-79
     w[1, :] = 0x8001                           # row 1: positive products
@@ -835,6 +917,14 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     y_ref = ref(x, w)
     assert np.all(np.signbit(y_ref[0, 0::2])) and not np.any(np.signbit(y_ref[0, 1::2]))
     check(run_rd(hip, x, w), y_ref, what=f"xlds zero signs k={k}")
+    # products of both signs (order-dependent zeros), every pattern of
+    # zero_rows in turn over the 4096 rows, against x with mixed signs
+    xm, wz = zero_rows(k, 9)
+    w = np.ascontiguousarray(wz[np.arange(n) % 9])
+    xm = np.ascontiguousarray(xm[2:3])
+    y_ref = ref(xm, w)
+    y = run_rd(hip, xm, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
 
 
 # ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
