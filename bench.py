@@ -10,23 +10,27 @@ through them, so >= 1 GiB of other weights streams between two reads of the
 same bytes (MI355X's Infinity Cache is 256 MB).
 
 value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
-              of the K timed steps over their host wall time.  The K steps
-              (2K launches on resident inputs) are captured once into a HIP
-              graph on the library stream and the timed region is one replay
-              of it: the host stays out of the device timeline.  (Launched one
-              Python call at a time, the same kernels run 0.3-0.5 us longer
-              each on some boxes, with no gaps between them, as the host's
-              pacing leaks into the dispatches; `eager` reports that figure.)
+              of the K timed steps over their host wall time, synchronized on
+              both sides.  The K steps (2K launches on resident inputs) are
+              captured once into a HIP graph on the library stream and the
+              timed region is one replay of it.  The per-shape batches below
+              run first, so the timed region starts on a device that has been
+              streaming, as a decode loop's steps do.  `eager` times the same
+              K steps launched one Python call at a time.
 roofline      algorithmic bytes per launch / average launch duration of the
-              row-dot streaming kernels, from HIP events on the library stream
-              around the timed region (2K back-to-back launches).  Each
-              duration includes the fixed cost of a dispatch, which
-              `dispatch_floor_us` measures alone with empty launches (rocprof
-              counts it inside a kernel's duration too).  Peak: MI355X's
-              8 TB/s HBM3E.  `us_per_launch` times each shape in its own
-              back-to-back batch (also a graph replay, as every batch below).
+              row-dot streaming kernels: HIP events on the library stream
+              around a replay of the same K steps, queued behind an untimed
+              replay so the events hold device time only (kernel durations
+              and the gaps between them, as rocprof's kernel trace sees them).
+              Each duration includes the fixed cost of a dispatch, which
+              `dispatch_floor_us` measures alone with empty launches.  Peak:
+              MI355X's 8 TB/s HBM3E.  `us_per_launch` times each shape in its
+              own back-to-back batch, the same way.
 read_ceiling  the same weights streamed by a read-only probe with the same
               128-bit nontemporal loads, timed the same way.
+dropin        the reference's own operator surface, dmc_matmul_bf16_gpu(_t),
+              with host x and y (PCIe and the synchronous round trip
+              included): microseconds per call on C2 up/gate.  Never `value`.
 cpu_baseline  the oracle's restatement of the reference CPU kernel
               dmc_matmul_bf16 (same fmaf chain and threading policy) on this
               host, on a bounded sample of the same workload.
@@ -131,11 +135,14 @@ class Rotating:
 
 
 def batch_us(d, fn, reps: int, graph: bool = True) -> float:
-    """Average duration of `reps` back-to-back launches of fn(0), fn(1), ...,
-    HIP events on the library stream around the batch.  graph=True: the batch
-    is captured once into a HIP graph (after one untimed call that lets the
-    library size its buffers) and the replay is timed; graph=False: one host
-    call per launch."""
+    """Average device time of `reps` back-to-back launches of fn(0), fn(1), ...:
+    HIP events on the library stream around the batch, kernel durations plus
+    the gaps between them.  graph=True: the batch is captured once into a HIP
+    graph (after one untimed call that lets the library size its buffers),
+    and the timed replay is queued behind an untimed one, so the device goes
+    from one to the other without waiting for the host to submit (the events
+    then hold device time only, like rocprof's kernel trace); graph=False: one
+    host call per launch, submission included."""
     fn(0)
     d.synchronize()
     g = None
@@ -146,10 +153,12 @@ def batch_us(d, fn, reps: int, graph: bool = True) -> float:
         g.launch()
     e0, e1 = d.Event(), d.Event()
     d.synchronize()
-    e0.record()
     if g is not None:
+        g.launch()  # untimed: keeps the device busy while the timed replay is submitted
+        e0.record()
         g.launch()
     else:
+        e0.record()
         for i in range(reps):
             fn(i)
     e1.record()
@@ -170,6 +179,9 @@ def main(argv=None) -> int:
     ap.add_argument("--extended", action="store_true",
                     help="also time C1, C3, C4, C5 and the column-stream layout (stderr + 'extended')")
     ap.add_argument("--c3", action="store_true", help="also time C3, the 32-layer decode sweep")
+    ap.add_argument("--crossover", action="store_true",
+                    help="only time the drop-in against the CPU kernel for k*n = 2^10 .. 2^24 (m = 1), "
+                         "the measurement behind DMC_HIP_MIN_MACS")
     a = ap.parse_args(argv)
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -186,6 +198,9 @@ def main(argv=None) -> int:
               file=sys.stderr)
         return 1
     log(f"device {d.device_info()}")
+    if a.crossover:
+        print(json.dumps(crossover(d)), flush=True)
+        return 0
 
     t = time.perf_counter()
     c2 = W.c2()
@@ -210,14 +225,20 @@ def main(argv=None) -> int:
                 launch(name, i)
 
     def timed(run):
-        e0, e1 = d.Event(), d.Event()
+        """Host wall time of run(), bracketed by a synchronize on both sides."""
         d.synchronize()
         t0 = time.perf_counter()
-        e0.record()
         run()
-        e1.record()
         d.synchronize()
-        return time.perf_counter() - t0, e0.elapsed_ms(e1)
+        return time.perf_counter() - t0
+
+    # per-shape launch durations, the read ceiling and the dispatch floor
+    # (measured first: the timed region below then starts on a device that
+    # has been streaming for a while, as a decode loop's steps do)
+    us = {nm: batch_us(d, lambda i, nm=nm: launch(nm, i), a.steps) for nm in order}
+    read_us = {nm: batch_us(d, lambda i, nm=nm: d.probe_read(shapes[nm].w[i % a.copies]), a.steps)
+               for nm in order}
+    floor_us = batch_us(d, lambda i: d.probe_read(None, 0), a.steps)
 
     # timed region: K steps, each the two GEMVs, inputs resident, replayed
     # from a HIP graph captured once (after one untimed replay)
@@ -225,22 +246,24 @@ def main(argv=None) -> int:
         steps()
     graph.launch()
     d.synchronize()
-    wall, ev_ms = timed(graph.launch)
-    graph.destroy()
+    wall = timed(graph.launch)
     bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
     value = bytes_step * a.steps / wall / 1e9
+    # device time of the same K steps (HIP events; see batch_us)
+    e0, e1 = d.Event(), d.Event()
+    graph.launch()
+    e0.record()
+    graph.launch()
+    e1.record()
+    e1.synchronize()
+    ev_ms = e0.elapsed_ms(e1)
+    graph.destroy()
     # the same K steps launched one call at a time (garbage collector paused)
     gc.disable()
     try:
-        eager_wall, eager_ev_ms = timed(steps)
+        eager_wall = timed(steps)
     finally:
         gc.enable()
-
-    # per-shape launch durations, the read ceiling and the dispatch floor
-    us = {nm: batch_us(d, lambda i, nm=nm: launch(nm, i), a.steps) for nm in order}
-    read_us = {nm: batch_us(d, lambda i, nm=nm: d.probe_read(shapes[nm].w[i % a.copies]), a.steps)
-               for nm in order}
-    floor_us = batch_us(d, lambda i: d.probe_read(None, 0), a.steps)
     for nm in order:
         y = shapes[nm].y.download(np.float32, (shapes[nm].shape[0],))
         assert np.all(np.isfinite(y)), nm  # full parity lives in tests/
@@ -271,8 +294,7 @@ def main(argv=None) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16w-f32acc",
         "submission": "one HIP graph replay of the K timed steps (2K kernel launches)",
         "eager": {"value": round(bytes_step * a.steps / eager_wall / 1e9, 1),
-                  "avg_launch_us": round(eager_ev_ms * 1e3 / (a.steps * len(order)), 3),
-                  "note": "the same K steps launched one Python call at a time"},
+                  "note": "the same K steps launched one Python call at a time, host wall time"},
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) f32 activations (PCG64 seed 0)",
         "config": {"workload": "C2 Llama-3-8B FFN decode GEMVs, row-dot layout: up/gate W[14336,4096] "
                                "and down W[4096,14336], m=1, weights resident, cold cache "
@@ -287,6 +309,7 @@ def main(argv=None) -> int:
         "read_ceiling": {"GB/s": round(read_gbs, 1), "us": {nm: round(u, 3) for nm, u in read_us.items()},
                          "frac_of_peak": round(read_gbs / PEAK_GBS, 4)},
         "dispatch_floor_us": round(floor_us, 3),
+        "dropin": dropin(d, W, 300),
         "cpu_baseline": None if a.no_cpu else cpu_baseline(a.cpu_seconds),
     }
     if a.extended:
@@ -323,7 +346,6 @@ def extended(d, W, reps: int) -> dict:
             f(i)
         record(label, batch_us(d, f, reps), n, k)
         s.free()
-    out.update(dropin(d, W, 300))
     # C4 LM head, skinny M: one resident copy (1.05 GB exceeds the 256 MB cache)
     t = time.perf_counter()
     w, _ = W.dense(W.LM_HEAD[0], W.LM_HEAD[1], seed=0, m=1)
@@ -472,6 +494,57 @@ def dropin(d, W, reps: int) -> dict:
         assert np.all(np.isfinite(y)), label
     d.release_weights()
     return out
+
+
+def crossover(d) -> dict:
+    """Per-call time of the synchronous drop-in x @ W (dmc_matmul_bf16_gpu:
+    host x and y, resident weight, content key, launch, wait) against the
+    reference's CPU kernel restated (the oracle's dmc_matmul_bf16, its own
+    thread policy) on this host, for m = 1 and k*n = 2^10 .. 2^24 (k = 2^ceil(e/2),
+    n = 2^floor(e/2)).  The route threshold DMC_HIP_MIN_MACS is the smallest
+    k*n from which the device wins at every larger size measured."""
+    import oracle
+
+    lib = d._lib.load()
+    rows = []
+    rng = np.random.default_rng(0)
+    for e in range(10, 25):
+        k, n = 1 << ((e + 1) // 2), 1 << (e // 2)
+        w = W_bf16(rng, k, n)
+        x = rng.standard_normal(k).astype(np.float32)
+        y = np.empty(n, np.float32)
+        lib.dmc_matmul_bf16_gpu(x.ctypes.data, w.ctypes.data, y.ctypes.data, 1, k, n)  # resident now
+
+        def gpu():
+            lib.dmc_matmul_bf16_gpu(x.ctypes.data, w.ctypes.data, y.ctypes.data, 1, k, n)
+
+        def cpu():
+            oracle.matmul_bf16(x, w)
+
+        times = {}
+        for name, fn in (("gpu_us", gpu), ("cpu_us", cpu)):
+            fn()
+            calls, t0 = 0, time.perf_counter()
+            while True:
+                fn()
+                calls += 1
+                el = time.perf_counter() - t0
+                if (el >= 0.05 and calls >= 5) or calls >= 2000:
+                    break
+            times[name] = round(el / calls * 1e6, 2)
+        rows.append({"k": k, "n": n, "kn": k * n, "cpu_threads": oracle.gemv_ways(k, n), **times})
+        log(f"crossover k*n=2^{e} (k={k} n={n}): gpu {times['gpu_us']:.1f} us  cpu {times['cpu_us']:.1f} us")
+    d.release_weights()
+    wins = [r["gpu_us"] < r["cpu_us"] for r in rows]
+    first = next((i for i in range(len(rows)) if all(wins[i:])), None)
+    return {"crossover_kn": rows[first]["kn"] if first is not None else None, "rows": rows,
+            "host_nproc": os.cpu_count()}
+
+
+def W_bf16(rng, k: int, n: int) -> np.ndarray:
+    """W [k, n] bf16 bits ~ N(0, 0.02) (the x @ W layout)."""
+    from demonic_amd import workloads as W
+    return W.bf16_rne(np.float32(0.02) * rng.standard_normal((k, n), dtype=np.float32))
 
 
 def c3(d, W, tokens: int = 10) -> dict:

@@ -28,7 +28,7 @@ __all__ = [
     "resident_count", "resident_bytes", "device_info", "vault_load_npz", "npz_locate", "f16_upconvert",
 ]
 
-MIN_MACS = 1 << 17  # DMC_HIP_MIN_MACS in include/dmc_hip.h
+MIN_MACS = 1 << 14  # DMC_HIP_MIN_MACS in include/dmc_hip.h
 
 
 def _arr(a: np.ndarray, dtype, name: str) -> np.ndarray:

@@ -152,16 +152,18 @@ __device__ __forceinline__ float widen_hi(uint32_t w) { return __uint_as_float(w
 // ascending k from +0, jit.rs:29655-29670): a run of underflowing products of
 // both signs leaves the chain at the zero of the last one's sign, where a sum
 // of reordered partials is -0 only if every partial is; and reordered partials
-// can cancel exactly where the chain keeps a subnormal residue.  So a zero
-// output is settled by the reference's own rule: +0 when its activation row
-// holds only +-0 (every product is an exact zero and the chain never leaves
-// +0), otherwise the chain itself -- which also gives +0 for an all-zero
-// weight row.  The common path costs one compare and one ballot per output.
+// can cancel exactly where the chain keeps a subnormal residue.  Neither can
+// happen when every product is an exact zero (some factor +-0): the chain then
+// never leaves +0, and neither does the split sum (lanes with elements start
+// at +0, idle ones add -0).  So a zero output is settled by the reference's
+// rule: +0 when no product has two nonzero factors -- an all-zero activation
+// row, an all-zero weight row, or factors that never meet -- and otherwise
+// the chain itself (underflow or exact cancellation, which takes crafted
+// data).  The common path costs one compare and one ballot per output.
 
 // The reference chain for one output: K products x[k] * w[k * wstep], any
 // alignment (2- and 4-byte loads; the rare path only).
-__device__ float chain_strided(const uint16_t *__restrict__ w, int64_t wstep,
-                                            const float *__restrict__ x, int K) {
+__device__ float chain_strided(const uint16_t *__restrict__ w, int64_t wstep, const float *__restrict__ x, int K) {
     float acc = 0.0f;
     int k = 0;
     for (; k + 4 <= K; k += 4) {
@@ -177,35 +179,207 @@ __device__ float chain_strided(const uint16_t *__restrict__ w, int64_t wstep,
     return acc;
 }
 
-__device__ __forceinline__ const float *readlane_ptr(const float *p, int j) {
+template <class T>
+__device__ __forceinline__ const T *readlane_ptr(const T *p, int j) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, j);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), j);
-    return reinterpret_cast<const float *>(((uint64_t)hi << 32) | lo);
+    return reinterpret_cast<const T *>(((uint64_t)hi << 32) | lo);
+}
+
+// Wave-uniform: does some k have x[k] and (w == nullptr, or w[k * wstep])
+// nonzero?  Contiguous rows (wstep <= 1, K <= 2^28): 16-byte buffer loads at
+// the rows' own 4- and 2-byte alignments (exact on gfx950), 8 elements per
+// lane per load, 4096 per round -- one round for K <= 4096.  The weight range
+// ends exactly after element K-1: a load's dword that runs past it comes back
+// as zeros (element K-1 itself when it shares such a dword), so element K-1
+// is also read alone, 2 bytes, and nothing past the row is ever read.
+// Strided columns: one element per lane per load, 64 * 32 per round.  All
+// loads of a round are in flight together; the scan stops at the first round
+// that finds a product.
+__device__ bool wave_any_product(const float *x, const uint16_t *w, int64_t wstep, int K) {
+    const int lane = threadIdx.x & 63;
+    if (K <= 0) return false;
+    if (wstep <= 1 && K <= (1 << 28)) {
+        constexpr int U = 8;
+        const uintptr_t wb = reinterpret_cast<uintptr_t>(w);
+        const __amdgpu_buffer_rsrc_t xr = weight_rsrc(x, (uint32_t)K * 4u);
+        const uintptr_t w0 = wb & ~(uintptr_t)3;
+        const uint32_t wd = (uint32_t)(wb - w0);  // 0 or 2
+        const __amdgpu_buffer_rsrc_t wr =
+            weight_rsrc(reinterpret_cast<const void *>(w ? w0 : reinterpret_cast<uintptr_t>(x)),
+                        w ? wd + 2u * (uint32_t)K : 0u);
+        const uint32_t wl = w ? (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(wr, wd + 2u * (K - 1), 0, 0) : 1u;
+        const uint32_t xl = __float_as_uint(x[K - 1]) & 0x7fffffffu;
+        bool first = true;
+        for (int k0 = 0; k0 < K; k0 += 512 * U) {
+            u32x4 xa[U], xc[U], wv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const uint32_t e = (uint32_t)(k0 + (u * 64 + lane) * 8);
+                xa[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, e * 4u, 0, 0);
+                xc[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, e * 4u + 16u, 0, 0);
+                wv[u] = w ? __builtin_amdgcn_raw_buffer_load_b128(wr, wd + e * 2u, 0, 0) : u32x4{~0u, ~0u, ~0u, ~0u};
+            }
+            uint32_t hit = first && (wl & 0x7fffu) != 0 && xl != 0 ? 1u : 0u;
+            first = false;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int e = k0 + (u * 64 + lane) * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t xv = (i < 4 ? xa[u][i] : xc[u][i - 4]) & 0x7fffffffu;
+                    const uint32_t wv16 = (wv[u][i >> 1] >> (16 * (i & 1))) & 0x7fffu;
+                    hit |= (e + i < K && xv != 0 && wv16 != 0) ? 1u : 0u;
+                }
+            }
+            if (__builtin_amdgcn_ballot_w64(hit != 0) != 0) return true;
+        }
+        return false;
+    }
+    constexpr int U = 32;
+    for (int k0 = 0; k0 < K; k0 += 64 * U) {
+        uint32_t xb[U], wb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min(k0 + u * 64 + lane, K - 1);
+            xb[u] = __float_as_uint(x[k]) & 0x7fffffffu;
+            wb[u] = w ? (uint32_t)w[(int64_t)k * wstep] & 0x7fffu : 1u;
+        }
+        uint32_t hit = 0;
+#pragma unroll
+        for (int u = 0; u < U; ++u) hit |= (k0 + u * 64 + lane < K && xb[u] != 0 && wb[u] != 0) ? 1u : 0u;
+        if (__builtin_amdgcn_ballot_w64(hit != 0) != 0) return true;
+    }
+    return false;
 }
 
 // The zero rule for the outputs this wave holds, one per lane: `zero` marks a
 // lane whose output s is exactly 0 and is stored; x is its activation row,
 // w its first weight, wstep the elements between consecutive k.  All 64 lanes
-// call it (wave-uniform control flow): an activation row is scanned by the
-// whole wave, the chains run one per lane.
+// call it (wave-uniform control flow): rows are scanned by the whole wave,
+// one output at a time, and the chains (if any) run one per lane.
 __device__ float settle_zero(float s, bool zero, const float *x, const uint16_t *w, int64_t wstep, int K) {
     uint64_t pend = __builtin_amdgcn_ballot_w64(zero);
     if (pend == 0) return s;
     const int lane = threadIdx.x & 63;
-    bool xnz = false;
-    while (pend) {
+    // activation rows that hold only +-0, each distinct row scanned once (a
+    // lone zero output skips this: its product scan covers its row)
+    bool xnz = true;
+    if (pend & (pend - 1)) while (pend) {
         const int j = __builtin_ctzll(pend);
         const float *xj = readlane_ptr(x, j);
-        uint32_t acc = 0;
-        for (int c = lane; c < K; c += 64) acc |= __float_as_uint(xj[c]) & 0x7fffffffu;
-        const bool nz = __builtin_amdgcn_ballot_w64(acc != 0) != 0;
+        const bool nz = wave_any_product(xj, nullptr, 0, K);
         const bool same = zero && x == xj;
         if (same) xnz = nz;
         pend &= ~__builtin_amdgcn_ballot_w64(same);
     }
-    if (zero) s = xnz ? chain_strided(w, wstep, x, K) : 0.0f;
+    // outputs whose products all have a zero factor
+    bool chain = false;
+    for (uint64_t todo = __builtin_amdgcn_ballot_w64(zero && xnz); todo; todo &= todo - 1) {
+        const int j = __builtin_ctzll(todo);
+        const bool hit = wave_any_product(readlane_ptr(x, j), readlane_ptr(w, j), wstep, K);
+        if (lane == j) chain = hit;
+    }
+    if (zero) s = chain ? chain_strided(w, wstep, x, K) : 0.0f;
     return s;
+}
+
+// The column-stream kernels and the row-dot kernels that keep x in registers
+// settle zeros without scanning (a column-stream weight column is N elements
+// apart in memory, too far to re-read cheaply; a row-dot workgroup is short
+// lived, and every wave but the storing one should leave at its last
+// barrier).  Each lane
+// tracks whether any of its products had two nonzero factors and folds that
+// into the sign of an exactly-zero partial: -0 for none, +0 otherwise.  The
+// fold survives every later sum -- (-0) + (-0) = -0, (-0) + (+0) = +0, and a
+// nonzero term wins -- so the final sum is -0 exactly when no product
+// anywhere had two nonzero factors (the reference chain is then +0), +0 when
+// the products underflowed or cancelled (the rare case: the chain itself),
+// and otherwise the value.  Non-finite partials pass through unchanged.
+__device__ __forceinline__ float zero_fold(float acc, bool has_product) {
+    return acc == 0.0f ? (has_product ? 0.0f : -0.0f) : acc;
+}
+
+// 0x7fff in the low half when a is nonzero and in the high half when b is:
+// ANDed with a dword holding two bf16 weights, nonzero exactly when one of the
+// two products (a with the low weight, b with the high one) has two nonzero
+// factors.  Computed once per x window; the streaming loops then track
+// products with one AND-OR per weight dword, branch-free.
+__device__ __forceinline__ uint32_t nonzero_pair(float a, float b) {
+    return ((__float_as_uint(a) & 0x7fffffffu) != 0 ? 0x00007fffu : 0u) |
+           ((__float_as_uint(b) & 0x7fffffffu) != 0 ? 0x7fff0000u : 0u);
+}
+
+// The final rule on a folded sum for one output (per lane; the chain is the
+// rare path).
+__device__ __forceinline__ float zero_unfold(float v, bool live, const float *x, const uint16_t *w, int64_t wstep,
+                                             int K) {
+    if (live && v == 0.0f) v = __builtin_signbit(v) ? 0.0f : chain_strided(w, wstep, x, K);
+    return v;
+}
+
+// The zero rule for the row-dot kernel with x in LDS (one long-lived
+// workgroup per CU), run after the workgroup's last barrier, with no cost in
+// the streaming loop.  total(t) gives output
+// t's sum (t < count).  Wave 0 alone stores every nonzero sum and notes in
+// LDS (`hits[NWAVES]`) whether any sum was exactly zero; the other waves wait
+// for that note at one barrier.  Only then (the rare path) do all waves
+// evaluate the totals again, in the same order, so they meet the same zero
+// outputs: lane_hit(t) re-reads the windows this lane summed for output t and
+// says whether one of its products had two nonzero factors, and the waves'
+// answers meet in LDS (`hits[0..NWAVES)`, one word per wave).  A zero output
+// then gets +0 (no such product: every product was an exact zero, so the
+// reference chain never leaves +0) or chain(t) (the products underflowed or
+// cancelled), stored by wave 0.  `hits` holds NWAVES + 1 words.
+template <int NWAVES, class Total, class Hit, class Chain, class Store>
+__device__ __forceinline__ void rd_finish(int count, uint64_t *hits, Total total, Hit lane_hit, Chain chain,
+                                          Store store) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (wave == 0) {
+        uint64_t any = 0;
+        for (int t0 = 0; t0 < count; t0 += 64) {
+            const int t = t0 + lane;
+            if (t < count) {
+                const float v = total(t);
+                if (v != 0.0f) store(t, v);
+                else any = 1;
+            }
+        }
+        any = __builtin_amdgcn_ballot_w64(any != 0);
+        if (lane == 0) hits[NWAVES] = any;
+    }
+    __syncthreads();
+    if (hits[NWAVES] == 0) return;
+    for (int t0 = 0; t0 < count; t0 += 64) {
+        const int t = t0 + lane;
+        const bool live = t < count;
+        const float v = live ? total(t) : 1.0f;
+        const uint64_t zm = __builtin_amdgcn_ballot_w64(live && v == 0.0f);
+        if (zm == 0) continue;  // the same in every wave: the barriers below are safe
+        uint64_t mine = 0;
+        for (uint64_t b = zm; b; b &= b - 1) {
+            const int j = __builtin_ctzll(b);
+            if (__builtin_amdgcn_ballot_w64(lane_hit(t0 + j)) != 0) mine |= 1ull << j;
+        }
+        if (lane == 0) hits[wave] = mine;
+        __syncthreads();
+        uint64_t has = 0;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) has |= hits[w];
+        __syncthreads();  // hits is reused by the next chunk
+        if (wave == 0 && live && v == 0.0f) store(t, ((has >> lane) & 1) ? chain(t) : 0.0f);
+    }
+}
+
+// Does some e have x[e] and the bf16 at half e of w nonzero?  (8 elements)
+__device__ __forceinline__ bool window_hit(const float (&x)[8], const u32x4 &w) {
+    bool hit = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        hit |= (__float_as_uint(x[e]) & 0x7fffffffu) != 0 && ((w[e >> 1] >> (16 * (e & 1))) & 0x7fffu) != 0;
+    return hit;
 }
 
 // ---- RD streaming: W [N,K], 16-byte aligned rows, K <= 32768 ------------------
@@ -332,6 +506,9 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
                     xr[m][j][e] = __uint_as_float(__float_as_uint(xr[m][j][e]) | (has[j] ? 0u : 0x80000000u));
     };
 
+    // xm: nonzero_pair of each x dword pair, set once x has arrived.  Each
+    // lane's partial is zero-folded before the wave sum (zero_fold).
+    uint32_t xm[MT][KV][4];
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
         float acc[MT][ROWS];
 #pragma unroll
@@ -353,7 +530,12 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int q = 0; q < ROWS; ++q) {
-                const float s = wave_sum_dpp(acc[m][q]);
+                uint32_t nz = 0;
+#pragma unroll
+                for (int j = 0; j < KV; ++j)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) nz |= wv[q][j][d] & xm[m][j][d];
+                const float s = wave_sum_dpp(zero_fold(acc[m][q], nz != 0));
                 if (lane == 0 && i0 + q < nr) red[wave][m][i0 + q] = s;
             }
     };
@@ -363,6 +545,12 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);  // keep pad_x's wait for x after every load above
     pad_x();
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) xm[m][j][d] = nonzero_pair(xr[m][j][2 * d], xr[m][j][2 * d + 1]);
     sum_rows(ba, 0);
     for (int i0 = 0; i0 + ROWS < nr; i0 += 2 * ROWS) {
         load(ba, i0 + 2 * ROWS);
@@ -372,16 +560,18 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
         sum_rows(ba, i0 + 2 * ROWS);
     }
     __syncthreads();
-    for (int t0 = wave * 64; t0 < MT * nr; t0 += 64 * NW) {  // wave-uniform: settle_zero needs whole waves
+    // Only the waves that hold outputs stay (wave-uniform, so the rare chain's
+    // loads are too); the others leave, freeing their slots for the next
+    // workgroup.
+    for (int t0 = wave * 64; t0 < mrows * nr; t0 += 64 * NW) {
         const int t = t0 + lane;
-        const bool live = t < MT * nr;
+        const bool live = t < mrows * nr;
         const int m = live ? t / nr : 0, r = live ? t - m * nr : 0;
         float s = red[0][m][r];
 #pragma unroll
         for (int w = 1; w < NW; ++w) s += red[w][m][r];
-        const bool store = live && m < mrows;
-        s = settle_zero(s, store && s == 0.0f, X + (int64_t)(m0 + m) * K, W + (int64_t)(rb + r) * ldw, 1, K);
-        if (store) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
+        s = zero_unfold(s, live, X + (int64_t)(m0 + m) * K, W + (int64_t)(rb + r) * ldw, 1, K);
+        if (live) Y[(int64_t)(m0 + m) * ldy + rb + r] = s;
     }
 }
 
@@ -497,17 +687,35 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
         sum_rows(ba, i0 + 2 * ROWS);
     }
     __syncthreads();
-    for (int t0 = wid * 64; t0 < 2 * hrows; t0 += 1024) {  // wave-uniform: settle_zero needs whole waves
-        const int t = t0 + lane;
-        const int h = t < 2 * hrows ? t / hrows : 0, r = t < 2 * hrows ? t - h * hrows : 0;
-        const int row = (int)blockIdx.x * rpw + h * hrows + r;
-        const bool store = t < 2 * hrows && row < N;
-        float s = red[h][0][r];
+    __shared__ uint64_t hits[2 * NW + 1];
+    const int rows_here = max(0, min(rpw, N - (int)blockIdx.x * rpw));  // outputs t = h * hrows + r
+    rd_finish<2 * NW>(
+        rows_here, hits,
+        [&](int t) {
+            const int h = t / hrows, r = t - h * hrows;
+            float s = red[h][0][r];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[h][w][r];
-        s = settle_zero(s, store && s == 0.0f, X, W + (int64_t)(store ? row : 0) * K, 1, K);
-        if (store) Y[row] = s;
-    }
+            for (int w = 1; w < NW; ++w) s += red[h][w][r];
+            return s;
+        },
+        [&](int t) {  // only the waves of the half that summed row t; x from its LDS copy
+            const int h = t / hrows, r = t - h * hrows;
+            bool hit = false;
+            if (h == half)
+#pragma unroll
+                for (int j = 0; j < KV; ++j) {
+                    const int w = (j * NW + wave) * 64 + lane;
+                    const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
+                    const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
+                    const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
+                                         __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
+                                         __uint_as_float(b[2]), __uint_as_float(b[3])};
+                    hit |= window_hit(xw, load_w16(rs, eoff[j], (uint32_t)r * row_bytes));
+                }
+            return hit;
+        },
+        [&](int t) { return chain_strided(W + (int64_t)((int)blockIdx.x * rpw + t) * K, 1, X, K); },
+        [&](int t, float v) { Y[(int)blockIdx.x * rpw + t] = v; });
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -561,13 +769,19 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
         return (uint32_t)(reinterpret_cast<uintptr_t>(W + (int64_t)r * ldw) - base);
     };
 
-    // The short tail's loads (all lanes issue them; only lane r < nr of the
-    // last wave reads memory), oldest of all, so the first wait covers them.
-    const bool tail_lane = kmain < K && wave == NW - 1 && lane < re - rb;
-    const u32x4 tw = load_w16(rs, tail_lane ? row_off(rb + lane) + (uint32_t)kmain * 2u : kOutOfRange);
-    const uint32_t txo = tail_lane ? (uint32_t)kmain * 4u : kOutOfRange;
-    const u32x4 txa = __builtin_amdgcn_raw_buffer_load_b128(xrs, txo, 0, 0);
-    const u32x4 txb = __builtin_amdgcn_raw_buffer_load_b128(xrs, txo + 16u, 0, 0);
+    // The short tail's weights, loaded by the last wave only (lane r for row
+    // rb + r), before any other load: the first wait covers them, so the
+    // branch adds no wait of its own.  Element by element (2-byte loads):
+    // none reaches past element K-1, so the matrix's last element needs no
+    // padding behind it.  Its x comes through the scalar cache.
+    const int rem = K - kmain;  // 0 .. 8
+    uint32_t tw[8] = {};
+    if (rem > 0 && wave == NW - 1) {
+        const uint32_t tbase = lane < re - rb ? row_off(rb + lane) + (uint32_t)kmain * 2u : kOutOfRange;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            tw[e] = __builtin_amdgcn_raw_buffer_load_b16(rs, e < rem ? tbase + 2u * e : kOutOfRange, 0, 0);
+    }
 
     uint32_t coff[KV];
     uint32_t mask[KV][4];
@@ -605,17 +819,25 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
             xr[j][q] = __uint_as_float(xa[j][q]);
             xr[j][q + 4] = __uint_as_float(xb[j][q]);
         }
-    if (kmain < K && wave == NW - 1) {  // the short tail's partial, ascending k from +0
-        float t = 0.0f;
-        const int rem = K - kmain;
+    // hm: the window mask limited to the halves whose x is nonzero
+    // (nonzero_pair); each lane's partial is zero-folded before the wave sum.
+    uint32_t hm[KV][4];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t mk = (2 * d < rem ? 0x0000ffffu : 0u) | (2 * d + 1 < rem ? 0xffff0000u : 0u);
-            const uint32_t v = (tw[d] & mk) | (~mk & 0x80008000u);
-            t = fmaf(__uint_as_float(d < 2 ? txa[2 * d] : txb[2 * d - 4]), widen_lo(v), t);
-            t = fmaf(__uint_as_float(d < 2 ? txa[2 * d + 1] : txb[2 * d - 3]), widen_hi(v), t);
+    for (int j = 0; j < KV; ++j)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) hm[j][d] = mask[j][d] & nonzero_pair(xr[j][2 * d], xr[j][2 * d + 1]);
+    if (rem > 0 && wave == NW - 1) {  // the short tail's partial, ascending k from +0, zero-folded
+        float t = 0.0f;
+        bool hit = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float xv = X[kmain + min(e, rem - 1)];
+            const uint32_t v = e < rem ? tw[e] : 0x8000u;  // past K: -0 against +0, the exact additive identity
+            const float p = e < rem ? xv : 0.0f;
+            t = fmaf(p, __uint_as_float(v << 16), t);
+            hit |= p != 0.0f && (v & 0x7fffu) != 0;
         }
-        if (lane < re - rb) red[NW][lane] = t;
+        if (lane < re - rb) red[NW][lane] = zero_fold(t, hit);
     }
 
     // A wave whose windows of the last block all lie past kmain skips that
@@ -626,6 +848,7 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
             float acc = init;
+            uint32_t nz = 0;
 #pragma unroll
             for (int j = 0; j < KV; ++j) {
                 if (j == KV - 1 && !last_block) break;
@@ -634,9 +857,10 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
                     const uint32_t v = (wv[q][j][d] & mask[j][d]) | (~mask[j][d] & 0x80008000u);
                     acc = fmaf(xr[j][2 * d], widen_lo(v), acc);
                     acc = fmaf(xr[j][2 * d + 1], widen_hi(v), acc);
+                    nz |= wv[q][j][d] & hm[j][d];
                 }
             }
-            const float s = wave_sum_dpp(acc);
+            const float s = wave_sum_dpp(zero_fold(acc, nz != 0));
             if (lane == 0 && r0 + q < re) red[wave][r0 - rb + q] = s;
         }
     };
@@ -648,17 +872,16 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
         sum_rows(bb, r0 + ROWS);
     }
     __syncthreads();
-    const int nr = re - rb;
-    for (int t0 = wave * 64; t0 < nr; t0 += 64 * NW) {  // wave-uniform: settle_zero needs whole waves
+    for (int t0 = wave * 64; t0 < re - rb; t0 += 64 * NW) {  // as gemv_rd_stream_kernel's
         const int t = t0 + lane;
-        const bool store = t < nr;
-        const int i = store ? t : 0;
-        float s = red[0][i];
+        const bool live = t < re - rb;
+        const int r = live ? t : 0;
+        float s = red[0][r];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w][i];
-        if (kmain < K) s += red[NW][i];
-        s = settle_zero(s, store && s == 0.0f, X, W + (int64_t)(rb + i) * ldw, 1, K);
-        if (store) Y[rb + t] = s;
+        for (int w = 1; w < NW; ++w) s += red[w][r];
+        if (rem > 0) s += red[NW][r];
+        s = zero_unfold(s, live, X, W + (int64_t)(rb + r) * ldw, 1, K);
+        if (live) Y[rb + r] = s;
     }
 }
 
@@ -1581,12 +1804,17 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[m][e] = init;
 
+    // nz: the lane's columns that met a product with two nonzero factors (zero_fold)
+    uint32_t nz[MT][(VEC + 1) / 2] = {};
     auto consume = [&](const WVec<VEC> &wv, int k) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const float xv = xz[(int64_t)min(m, M - 1) * K + k];
 #pragma unroll
             for (int e = 0; e < VEC; ++e) acc[m][e] = fmaf(xv, widen<VEC>(wv, e), acc[m][e]);
+            const uint32_t xm = xv != 0.0f ? 0x7fff7fffu : 0u;
+#pragma unroll
+            for (int d = 0; d < (VEC + 1) / 2; ++d) nz[m][d] |= wv.d[d] & xm;
         }
     };
 
@@ -1604,13 +1832,16 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
         consume(wv, k);
     }
 
-    // Sum the RW row groups of the wave: lanes cl, cl+LPR, cl+2*LPR, ...
+    // Fold, then sum the RW row groups of the wave: lanes cl, cl+LPR, cl+2*LPR, ...
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e)
+        for (int e = 0; e < VEC; ++e) {
+            const uint32_t half = VEC == 1 ? nz[m][0] : nz[m][e >> 1] >> (16 * (e & 1));
+            acc[m][e] = zero_fold(acc[m][e], (half & 0x7fffu) != 0);
 #pragma unroll
             for (int o = LPR; o < 64; o <<= 1) acc[m][e] += __shfl_xor(acc[m][e], o, 64);
+        }
 
     __shared__ float red[kWaves][MT][CB];
     if (g == 0) {
@@ -1621,19 +1852,16 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
     }
     __syncthreads();
     // With one k slice P is y itself and the zero rule applies here;
-    // otherwise sum_slices_kernel applies it to the slices' sum.
+    // otherwise sum_slices_kernel applies it to the slices' (folded) sum.
     const bool final_out = kslice >= K;
-    for (int i0 = wave * 64; i0 < MT * CB; i0 += kThreads) {  // wave-uniform: settle_zero needs whole waves
-        const int i = i0 + lane < MT * CB ? i0 + lane : 0;
+    for (int i = threadIdx.x; i < MT * CB; i += kThreads) {
         const int m = i / CB, c = i % CB;
         const int n = blockIdx.x * CB + c;
         float s = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w) s += red[w][m][c];
-        const bool store = i0 + lane < MT * CB && n < N && m < M;
-        if (final_out)
-            s = settle_zero(s, store && s == 0.0f, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? n : 0),
-                            N, K);
+        const bool store = n < N && m < M;
+        if (final_out) s = zero_unfold(s, store, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? n : 0), N, K);
         if (store) pz[(int64_t)m * N + n] = s;
     }
 }
@@ -1698,6 +1926,9 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[m][e] = init;
 
+    // nz: the bf16 halves of the lane's columns that met a nonzero weight
+    // where x is nonzero (any product with two nonzero factors; zero_fold).
+    uint32_t nz[MT][4] = {};
     auto consume = [&](const u32x4 &wv, int k) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
@@ -1707,6 +1938,9 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
                 const uint32_t d = wv[e >> 1];
                 acc[m][e] = fmaf(xv, (e & 1) ? widen_hi(d) : widen_lo(d), acc[m][e]);
             }
+            const uint32_t xm = xv != 0.0f ? 0x7fff7fffu : 0u;  // wave-uniform
+#pragma unroll
+            for (int d = 0; d < 4; ++d) nz[m][d] |= wv[d] & xm;
         }
     };
 
@@ -1746,30 +1980,32 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) red[wave][m][lane * 8 + e] = acc[m][e];
+        for (int e = 0; e < 8; ++e)
+            red[wave][m][lane * 8 + e] = zero_fold(acc[m][e], ((nz[m][e >> 1] >> (16 * (e & 1))) & 0x7fffu) != 0);
     __syncthreads();
 
     const int c0 = cb * kCsCols;
     const int ncol = min(kCsCols, N - c0);
     // With one k slice (and every row in it) the workgroup writes y and the
-    // zero rule applies here; otherwise sum_slices_stream_kernel applies it.
+    // zero rule applies here; otherwise the folded partial goes to P and
+    // sum_slices_stream_kernel applies it.
     const bool final_out = slices == 1 && !UN;
     float *out = final_out ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
-    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {  // wave-uniform: MT * 512 is a multiple of 64 * NW
+    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {
         const int m = t / kCsCols, c = t - m * kCsCols;
         const bool store = m < M && c < ncol;
         float v = red[0][m][c];
 #pragma unroll
         for (int w = 1; w < NW; ++w) v += red[w][m][c];
         if (final_out)
-            v = settle_zero(v, store && v == 0.0f, xz + (int64_t)(store ? m : 0) * K,
-                            W + z * rs + (store ? c0 + c : 0), N, K);
+            v = zero_unfold(v, store, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? c0 + c : 0), N, K);
         if (store) out[(int64_t)m * N + c0 + c] = v;
     }
 }
 
 // Second pass of the column-stream kernels: y[i] = sum over slices of
-// P[j][i] in ascending j, then the zero rule (settle_zero).  `src` names the
+// P[j][i] in ascending j (partials folded by zero_fold), then the zero rule
+// (zero_unfold).  `src` names the
 // problem, so an output's activation row and weight column can be found:
 // output i of the launch is (slice z, activation row m, column n) =
 // (i / (M*N), (i / N) % M, i % N), its activation row x + z*ls + m*K, its
@@ -1781,12 +2017,11 @@ struct CsSrc {
     bool last_row;  // the UN streaming kernel left out row K-1 (below)
 };
 
-__device__ __forceinline__ float cs_settle(float v, bool live, int64_t i, const CsSrc &src) {
+__device__ __forceinline__ float cs_unfold(float v, bool live, int64_t i, const CsSrc &src) {
     const int64_t mn = src.M * src.N;
     const int64_t z = live ? i / mn : 0, r = live ? i - z * mn : 0;
     const int64_t m = r / src.N, n = r - m * src.N;
-    return settle_zero(v, live && v == 0.0f, src.x + z * src.ls + m * src.K, src.w + z * src.rs + n, src.N,
-                       (int)src.K);
+    return zero_unfold(v, live, src.x + z * src.ls + m * src.K, src.w + z * src.rs + n, src.N, (int)src.K);
 }
 
 // The streaming kernel's pass.  A workgroup owns 64 consecutive outputs; its
@@ -1814,16 +2049,18 @@ sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slice
     __shared__ float part[4][64];
     part[wave][lane] = s;
     __syncthreads();
-    if (wave == 0) {  // wave-uniform: settle_zero needs whole waves
+    if (wave == 0) {
         const bool live = i < count;
         float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
         if (src.last_row && live) {
             const int64_t z = i / (src.M * src.N), r = i - z * src.M * src.N;
             const int64_t m = r / src.N, n = r - m * src.N;
             const float xv = src.x[z * src.ls + m * src.K + (src.K - 1)];
-            v = fmaf(xv, __uint_as_float((uint32_t)src.w[z * src.rs + (src.K - 1) * src.N + n] << 16), v);
+            const uint32_t wb = src.w[z * src.rs + (src.K - 1) * src.N + n];
+            v = zero_fold(fmaf(xv, __uint_as_float(wb << 16), v),
+                          !(v == 0.0f && __builtin_signbit(v)) || (xv != 0.0f && (wb & 0x7fffu) != 0));
         }
-        v = cs_settle(v, live, i, src);
+        v = cs_unfold(v, live, i, src);
         if (live) Y[i] = v;
     }
 }
@@ -1840,7 +2077,7 @@ sum_slices_kernel(const float *__restrict__ P, int64_t p_slice, int slices, floa
         s = P[i];
         for (int j = 1; j < slices; ++j) s += P[(int64_t)j * p_slice + i];
     }
-    s = cs_settle(s, live, i, src);
+    s = cs_unfold(s, live, i, src);
     if (live) Y[i] = s;
 }
 
@@ -2166,7 +2403,6 @@ hipError_t rd_unaligned_dispatch(const RdProblem &p, const RdPlan &pl, hipStream
         case 5: return rd_unaligned_go<8, 5>(p, pl, s);
         case 6: return rd_unaligned_go<8, 6>(p, pl, s);
         case 7: return rd_unaligned_go<8, 7>(p, pl, s);
-        case 8: return rd_unaligned_go<8, 8>(p, pl, s);
         }
         return hipErrorInvalidValue;
     }
@@ -2467,14 +2703,16 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     // readable (padding after it, or not at 2 mod 4 with K odd; see the kernel).
     const uintptr_t last_elem = reinterpret_cast<uintptr_t>(p.w + ((p.n - 1) * p.ldw + p.k - 1));
     const bool last_ok = p.w_slack >= 2 || !((last_elem & 3) == 2 && (p.k & 1) == 1);
-    if (pl.vec < 8 && p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) && last_ok &&
-        env_int("DMC_HIP_RD_UNALIGNED", 1) != 0) {
-        const int nw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
+    const int unw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
+    // 1..8 elements past whole blocks of windows (k = 4097) go to each row's
+    // short tail, read element by element (so the matrix's last element is
+    // always readable); otherwise the last block of windows holds the rest.
+    const bool short_tail = p.k > (int64_t)unw * 512 && p.k % ((int64_t)unw * 512) >= 1 &&
+                            p.k % ((int64_t)unw * 512) <= 8 && env_int("DMC_HIP_RD_SHORT_TAIL", 1) != 0;
+    if (pl.vec < 8 && p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) &&
+        (last_ok || short_tail) && env_int("DMC_HIP_RD_UNALIGNED", 1) != 0) {
+        const int nw = unw;
         const int64_t block = (int64_t)nw * 512;
-        // 1..8 elements past whole blocks of windows (k = 4097) go to each
-        // row's short tail; otherwise the last block holds the rest.
-        const int64_t rem = p.k % block;
-        const bool short_tail = p.k > block && rem >= 1 && rem <= 8 && env_int("DMC_HIP_RD_SHORT_TAIL", 1) != 0;
         const int kv = short_tail ? (int)(p.k / block) : (int)((p.k + block - 1) / block);
         const int rpw_default = kv >= 2 ? 8 : 4;
         const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
@@ -2484,7 +2722,9 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // rest is a short tail: measured on MI355X against the general
         // kernel, k = 4095 67% vs 57% of peak, 11007 64% vs 60%, 14335 64% vs
         // 56%, but k = 4097 as a one-element last block 53% vs 61%.
-        if ((short_tail || p.k - (kv - 1) * block >= block / 2) && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
+        // KV = 8 (k above 28,680) would need more than 256 VGPRs with the
+        // product masks: the general kernel takes it.
+        if (kv <= 7 && (short_tail || p.k - (kv - 1) * block >= block / 2) && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
             (p.n + rpw - 1) / rpw <= INT32_MAX) {
             RdPlan sp{};
             sp.vec = pl.vec;

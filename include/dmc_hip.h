@@ -114,8 +114,13 @@ int32_t dmc_hip_available(void);
 /* The host-independent half of the route decision, shaped like
  * blas_gemm_selected (jit.rs:29346-29351): opt-in flag on, no enclosing
  * `@deterministic` block, and at least DMC_HIP_MIN_MACS multiply-adds.
- * Pure function; touches no device. */
-#define DMC_HIP_MIN_MACS (1LL << 17)
+ * Pure function; touches no device.  The threshold is measured (bench.py
+ * --crossover, m = 1 on an MI355X host): a synchronous drop-in call costs
+ * 19-20 us up to k*n = 2^20, the reference's CPU kernel (dmc_matmul_bf16,
+ * restated) 20.6 us at k*n = 2^14 and 12.3 us at 2^13, so from 2^14 the
+ * device wins at every size.  (The reference's Metal route starts at
+ * 4,000,000 k*n, jit.rs:20933, because a Metal dispatch costs ~165 us.) */
+#define DMC_HIP_MIN_MACS (1LL << 14)
 int32_t dmc_hip_gemv_selected(int32_t hip_on, int32_t deterministic_depth, int64_t m, int64_t k,
                               int64_t n);
 
@@ -133,9 +138,13 @@ int32_t dmc_hip_copy_device(int64_t dst_dev, int64_t src_dev, int64_t bytes); /*
 
 /* Make a host weight resident ahead of its first GEMV (the content-keyed memo
  * of gpu.rs:261-280, filled at load time instead of on first use).  Returns
- * the device address of the resident copy (0 on failure). */
+ * the device address of the resident copy (0 on failure).  The entry is
+ * pinned: the residency cap (2048 cached weights, gpu.rs:266), an
+ * out-of-memory retry and DMC_HIP_RESIDENT_CAP never free it, so the address
+ * stays valid until dmc_hip_release_weights. */
 int64_t dmc_hip_register_weight(int64_t host_ptr, int64_t bytes);
-/* Drop every resident weight (after materializing deferred work). */
+/* Drop every resident weight, registered ones included (after materializing
+ * deferred work); addresses from dmc_hip_register_weight become invalid. */
 int32_t dmc_hip_release_weights(void);
 /* Number and total bytes of resident weights. */
 int64_t dmc_hip_resident_count(void);
@@ -150,6 +159,7 @@ int32_t dmc_hip_gemv_cs(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
 int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k,
                         int64_t n);
 int32_t dmc_hip_synchronize(void);
+
 
 /* Grouped row-dot GEMV on device pointers: `count` independent problems
  * y_i[m, n_i] = x_i[m, k] @ bf16(w_i[n_i, k])', all packed and sharing m and

@@ -68,7 +68,8 @@ def test_selection_predicate():
     assert not sel(False, 0, 1, 512, 512), "selected with the flag off"
     assert not sel(True, 1, 1, 512, 512), "selected inside @deterministic"
     assert not sel(True, 3, 1, 4096, 14336), "nested @deterministic"
-    assert not sel(True, 0, 1, 128, 128), "small GEMV selected"
+    assert not sel(True, 0, 1, 64, 128), "small GEMV selected"
+    assert sel(True, 0, 1, 128, 128), "the measured crossover, k*n = 2^14"
     assert sel(True, 0, 1, 1, d.MIN_MACS), "at the threshold"
     assert not sel(True, 0, 1, 1, d.MIN_MACS - 1), "one under the threshold"
     assert sel(True, 0, 64, 64, 64), "threshold is a MAC count, not per-dimension"
@@ -221,17 +222,17 @@ def test_rowdot_mfma_layouts(monkeypatch):
 
 
 def test_rowdot_falls_back_to_general_kernel():
-    # k beyond the register budget, k == 0, several activation rows on
-    # misaligned weights, x not 16-byte aligned
-    for m, k, x, w in [(1, 32776, 256, 256), (1, 0, 256, 256), (2, 4097, 256, 256), (1, 4097, 260, 256),
-                       (1, 32770, 256, 258)]:
+    # k beyond the register budget (eight windows per lane), k == 0, several
+    # activation rows on misaligned weights, x not 16-byte aligned
+    for m, k, x, w in [(1, 32776, 256, 256), (1, 32767, 256, 256), (1, 28681, 256, 256), (1, 0, 256, 256),
+                       (2, 4097, 256, 256), (1, 4097, 260, 256), (1, 32770, 256, 258)]:
         p = d.plan("rd", m, k, 1000, x_addr=x, w_addr=w)
         assert p.slices == 0 and p.waves == 4, (m, k, x, w, p)
 
 
 @pytest.mark.parametrize("k,w,waves,kvec,rows", [(6145, 256, 8, 2, 1), (4096, 258, 8, 1, 2), (11007, 256, 8, 3, 2),
                                                  (1023, 256, 2, 1, 2), (257, 256, 1, 1, 2), (16384, 262, 8, 4, 2),
-                                                 (32767, 256, 8, 8, 1), (4095, 256, 8, 1, 2)])
+                                                 (28671, 256, 8, 7, 1), (4095, 256, 8, 1, 2)])
 def test_rowdot_misaligned_rows_stream_unaligned(k, w, waves, kvec, rows):
     """Rows that do not start on 16-byte boundaries (odd k, an offset
     weight) at m = 1: the streaming layout with unaligned 128-bit loads,
@@ -252,11 +253,28 @@ def test_rowdot_unaligned_needs_a_readable_last_element():
     assert d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=258).slices == 1   # k even: never straddles
 
 
-def test_rowdot_unaligned_needs_a_well_filled_last_block():
-    """k = 4097 puts one element in a second block of windows: the general
-    kernel measured faster there."""
-    assert d.plan("rd", 1, 4097, 11007, x_addr=256, w_addr=256).slices == 0
+def test_rowdot_unaligned_needs_a_well_filled_last_block_or_a_short_tail():
+    """Misaligned rows stay on the streaming kernel when the last block of
+    windows is at least half full (k = 4095), or when 1..8 elements are left
+    past whole blocks (k = 4097, 8199: a per-row short tail, read element by
+    element, so no padding behind the matrix is needed); a last block holding
+    9 to 2047 elements goes to the general kernel (k = 4105), as does k = 7
+    with no padding after an element at 2 mod 4."""
+    p = d.plan("rd", 1, 4097, 11007, x_addr=256, w_addr=256)
+    assert (p.slices, p.waves, p.rows_per_group) == (1, 8, 4), p
+    assert d.plan("rd", 1, 8199, 4097, x_addr=256, w_addr=256).slices == 2
+    assert d.plan("rd", 1, 4095, 11008, x_addr=256, w_addr=258).slices == 1  # last element at 0 mod 4
+    assert d.plan("rd", 1, 4105, 11007, x_addr=256, w_addr=256).slices == 0
     assert d.plan("rd", 1, 7, 1001, x_addr=256, w_addr=256).slices == 0
+    monkey = os.environ.get("DMC_HIP_RD_SHORT_TAIL")
+    os.environ["DMC_HIP_RD_SHORT_TAIL"] = "0"
+    try:
+        assert d.plan("rd", 1, 4097, 11007, x_addr=256, w_addr=256).slices == 0
+    finally:
+        if monkey is None:
+            del os.environ["DMC_HIP_RD_SHORT_TAIL"]
+        else:
+            os.environ["DMC_HIP_RD_SHORT_TAIL"] = monkey
 
 
 def test_column_stream_plans_split_k_and_size_workspace():
