@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dmc_hip_resident_bytes": (i64, []),
     "dmc_hip_gemv_cs": (i32, [i64] * 9),
     "dmc_hip_gemv_rd": (i32, [i64] * 6),
+    "dmc_hip_gemv_cs_noalloc": (i32, [i64] * 9),
     "dmc_hip_synchronize": (i32, []),
     "dmc_hip_probe_read": (i32, [i64, i64]),
     "dmc_hip_gemv_rd_grouped": (i32, [i64, ctypes.POINTER(i64), ctypes.POINTER(i64),

@@ -155,6 +155,10 @@ struct Ctx {
     uint64_t time_every = 0;  // DMC_HIP_TIME=N > 1: a stats line every N calls
     bool x_kernel = false;  // DMC_HIP_X_KERNEL: upload x with a kernel instead of a copy-engine transfer
     hipEvent_t tev[3] = {};  // DMC_HIP_TIME: before x, before the kernels, after them
+    // the no-allocation entry's fixed scratch, resolved per device at set-up
+    // (this library drives one device, `device`); null if that failed
+    std::unordered_map<int, void *> noalloc_scratch;
+    std::string noalloc_err;
     Stats st;
 };
 
@@ -226,6 +230,16 @@ int ensure_init() {
             const hipError_t e = hipStreamSynchronize(ctx().stream);
             return e == hipSuccess ? DMC_HIP_OK : hip_fail(e, "hipStreamSynchronize");
         });
+    {
+        void *p = nullptr;
+        const hipError_t e = dmc::noalloc_scratch_resolve(&p);
+        if (e == hipSuccess && p) {
+            c.noalloc_scratch[c.device] = p;
+        } else {
+            (void)hipGetLastError();
+            c.noalloc_err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+        }
+    }
     c.timing = env_flag("DMC_HIP_TIME");
     if (c.timing) c.time_every = (uint64_t)std::max(0LL, atoll(getenv("DMC_HIP_TIME")));
     for (hipEvent_t &ev : c.tev)
@@ -944,6 +958,36 @@ int32_t dmc_hip_gemv_cs(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
     const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
     if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
     hipError_t e = dmc::launch_cs(p, pl, c.ws.p, c.stream);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_gemv_cs_noalloc(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n,
+                                int64_t batch, int64_t ls, int64_t rs) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!valid_dims(m, k, n) || batch < 0 || ls < 0 || rs < 0)
+        return fail(DMC_HIP_EINVAL, "bad GEMV shape");
+    if (m == 0 || n == 0 || batch == 0) return DMC_HIP_OK;
+    if (!y_dev || (k > 0 && (!x_dev || !w_dev))) return fail(DMC_HIP_EINVAL, "null pointer");
+    // No set-up here: it allocates (stream, a dummy region).  The caller sets
+    // the library up beforehand, with dmc_hip_available().
+    Ctx &c = ctx();
+    if (!c.tried || !c.ok)
+        return fail(DMC_HIP_ENODEV, "dmc_hip_gemv_cs_noalloc: library not set up (call dmc_hip_available() first)");
+    HIP_TRY(hipSetDevice(c.device), "hipSetDevice");
+    auto it = c.noalloc_scratch.find(c.device);
+    if (it == c.noalloc_scratch.end())
+        return fail(DMC_HIP_EDEVICE, "dmc_hip_gemv_cs_noalloc: no fixed scratch on device %d: %s", c.device,
+                    c.noalloc_err.c_str());
+    dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_dev), reinterpret_cast<const float *>(x_dev),
+                     reinterpret_cast<float *>(y_dev), m, k, n, batch, ls, rs};
+    const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
+    if (pl.workspace_bytes > dmc::noalloc_scratch_bytes())
+        return fail(DMC_HIP_EINVAL,
+                    "dmc_hip_gemv_cs_noalloc: this shape needs %zu bytes of split-k scratch, the fixed maximum is "
+                    "%zu (use dmc_hip_gemv_cs)",
+                    pl.workspace_bytes, dmc::noalloc_scratch_bytes());
+    hipError_t e = dmc::launch_cs(p, pl, it->second, c.stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DMC_HIP_OK;
 }

@@ -3002,6 +3002,20 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
 
 size_t probe_sink_bytes() { return (size_t)kProbeGroups * 4; }
 
+// Split-k partial sums of dmc_hip_gemv_cs_noalloc live here instead of in
+// the library's growable workspace: 32 MiB per GPU, held until the process
+// ends.  In host code `scratch` is a stand-in for the symbol, not a device
+// address; only noalloc_scratch_resolve's result may reach a kernel.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+size_t noalloc_scratch_bytes() { return kNoAllocScratchBytes; }
+
+hipError_t noalloc_scratch_resolve(void **device_address) {
+    *device_address = nullptr;
+    return hipGetSymbolAddress(device_address, HIP_SYMBOL(scratch));
+}
+
 hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t s) {
     if (bytes <= 0) return hipSuccess;
     if (bytes % 4 || !aligned(dst, 4) || !aligned(src, 4)) return hipErrorInvalidValue;

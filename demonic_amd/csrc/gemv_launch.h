@@ -135,6 +135,13 @@ hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStre
 // upload, which a copy-engine transfer delays by its own scheduling.
 hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t stream);
 
+// The fixed scratch of the no-allocation column-stream entry: a file-scope
+// device array of noalloc_scratch_bytes() bytes in gemv_kernels.hip.  Its
+// device address differs per GPU; resolve it once per device, with that
+// device current, and pass only the resolved address to kernels and copies.
+size_t noalloc_scratch_bytes();
+hipError_t noalloc_scratch_resolve(void **device_address);
+
 // dst [cols, rows] = src [rows, cols]^T for bf16 bit patterns (weight
 // residency in the row-dot layout, dmc_hip_bf16_transpose_2d).
 hipError_t launch_transpose_bf16(const uint16_t *src, uint16_t *dst, int64_t rows, int64_t cols, hipStream_t stream);

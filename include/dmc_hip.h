@@ -160,6 +160,21 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
                         int64_t n);
 int32_t dmc_hip_synchronize(void);
 
+/* dmc_hip_gemv_cs for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference.  Same arguments, kernels and results as
+ * dmc_hip_gemv_cs, but the split-k partial sums go to a fixed 32 MiB device
+ * array owned by the library (one per GPU, held until the process ends), and
+ * the call allocates nothing (no hipMalloc, hipFree or allocating library
+ * routine).  The library must be set up first (dmc_hip_available()): the
+ * call returns DMC_HIP_ENODEV otherwise.  A shape whose partial sums exceed
+ * 32 MiB returns DMC_HIP_EINVAL with the sizes in dmc_hip_last_error.  Calls
+ * share the array: they are ordered on the library stream, but work that
+ * overlaps on one GPU outside that order (a captured graph replayed on
+ * another stream while a call runs) races on it.  Nothing in the array needs
+ * to start at zero; it keeps the last call's partials. */
+int32_t dmc_hip_gemv_cs_noalloc(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k,
+                                int64_t n, int64_t batch, int64_t ls, int64_t rs);
 
 /* Grouped row-dot GEMV on device pointers: `count` independent problems
  * y_i[m, n_i] = x_i[m, k] @ bf16(w_i[n_i, k])', all packed and sharing m and
