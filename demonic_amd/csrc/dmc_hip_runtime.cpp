@@ -63,10 +63,12 @@ bool env_flag(const char *name) {
 
 // ---- content key for resident weights --------------------------------------
 //
-// Byte length plus 512 evenly spread 8-byte samples (and the last word and the
-// trailing bytes), each mixed with its index through the splitmix64 finalizer
-// into two independent 64-bit lanes.  ~500 scattered host reads per call, the
-// same order of cost as the reference's 256-sample fingerprint (gpu.rs:334-358).
+// Byte length plus 256 evenly spread 8-byte samples (the reference's density,
+// gpu.rs:334-358), the last word and the trailing bytes, each mixed with its
+// index into two independent 64-bit lanes, the first through the splitmix64
+// finalizer.  The sample positions advance without a division, and the
+// finalizer chain is split four ways (recombined at the end), so the cost is
+// the scattered host reads, not a serial chain of multiplies.
 using Key = dmc::WeightKey;
 
 inline uint64_t mix64(uint64_t z) {
@@ -78,22 +80,34 @@ inline uint64_t mix64(uint64_t z) {
     return z;
 }
 
+constexpr uint64_t kKeySamples = 256;
+
 Key content_key(const void *ptr, int64_t bytes) {
     const unsigned char *p = static_cast<const unsigned char *>(ptr);
-    uint64_t a = mix64((uint64_t)bytes ^ 0x6a09e667f3bcc908ULL);
+    uint64_t a[4];
+    for (int j = 0; j < 4; ++j) a[j] = mix64((uint64_t)bytes ^ (0x6a09e667f3bcc908ULL + (uint64_t)j));
     uint64_t b = mix64((uint64_t)bytes + 0xbb67ae8584caa73bULL);
     const uint64_t words = (uint64_t)bytes / 8;
+    uint64_t n = 0;
     auto fold = [&](uint64_t idx, uint64_t v) {
-        a = mix64(a ^ v ^ (idx * 0x9e3779b97f4a7c15ULL));
+        a[n & 3] = mix64(a[n & 3] ^ v ^ (idx * 0x9e3779b97f4a7c15ULL));
         b = (b ^ v) * 0x100000001b3ULL + idx + 1;
+        ++n;
     };
     if (words > 0) {
-        const uint64_t S = words < 512 ? words : 512;
+        // sample i at word floor(i * words / S)
+        const uint64_t S = words < kKeySamples ? words : kKeySamples, q = words / S, r = words % S;
+        uint64_t idx = 0, acc = 0;
         for (uint64_t i = 0; i < S; ++i) {
-            const uint64_t idx = i * words / S;
             uint64_t v;
             memcpy(&v, p + idx * 8, 8);
             fold(idx, v);
+            idx += q;
+            acc += r;
+            if (acc >= S) {
+                acc -= S;
+                ++idx;
+            }
         }
         uint64_t v;
         memcpy(&v, p + (words - 1) * 8, 8);
@@ -102,7 +116,7 @@ Key content_key(const void *ptr, int64_t bytes) {
     uint64_t tail = 0;
     for (int64_t i = (int64_t)words * 8; i < bytes; ++i) tail = (tail << 8) | p[i];
     fold(words, tail);
-    return Key{a, mix64(b), bytes};
+    return Key{mix64(a[0] ^ mix64(a[1] ^ mix64(a[2] ^ mix64(a[3])))), mix64(b), bytes};
 }
 
 // ---- context ----------------------------------------------------------------
@@ -154,6 +168,8 @@ struct Ctx {
     bool timing = false;
     uint64_t time_every = 0;  // DMC_HIP_TIME=N > 1: a stats line every N calls
     bool x_kernel = false;  // DMC_HIP_X_KERNEL: upload x with a kernel instead of a copy-engine transfer
+    size_t y_direct_max = 0;  // largest y a kernel writes straight to pinned staging (DMC_HIP_Y_DIRECT_MAX)
+    size_t x_direct_max = 0;  // largest x a kernel reads straight from pinned staging (DMC_HIP_X_DIRECT_MAX)
     hipEvent_t tev[3] = {};  // DMC_HIP_TIME: before x, before the kernels, after them
     // the no-allocation entry's fixed scratch, resolved per device at set-up
     // (this library drives one device, `device`); null if that failed
@@ -170,6 +186,7 @@ Ctx &ctx() {
 
 const int kMaxResident = 2048;  // gpu.rs:266
 const size_t kDirectYBytes = 256 << 10;  // largest y a kernel writes straight to pinned staging
+const size_t kDirectXBytes = 64 << 10;   // largest x a kernel reads straight from pinned staging
 
 int hip_fail(hipError_t e, const char *what) {
     return fail(e == hipErrorOutOfMemory ? DMC_HIP_ENOMEM : DMC_HIP_EDEVICE, "%s: %s (%d)", what,
@@ -245,6 +262,12 @@ int ensure_init() {
     for (hipEvent_t &ev : c.tev)
         if (c.timing && hipEventCreate(&ev) != hipSuccess) c.timing = false;
     c.x_kernel = env_flag("DMC_HIP_X_KERNEL");
+    {
+        const char *v = getenv("DMC_HIP_Y_DIRECT_MAX");
+        c.y_direct_max = v && *v ? (size_t)std::max(0LL, atoll(v)) : kDirectYBytes;
+        v = getenv("DMC_HIP_X_DIRECT_MAX");
+        c.x_direct_max = v && *v ? (size_t)std::max(0LL, atoll(v)) : kDirectXBytes;
+    }
     c.ok = true;
     return DMC_HIP_OK;
 }
@@ -432,11 +455,12 @@ void stats_line(int64_t k, int64_t n) {
     s = Stats{};
 }
 
-// One synchronous call's device times (events recorded around its work).
-void stats_call(int64_t k, int64_t n, int64_t batch, uint64_t wait_ns) {
+// One synchronous call's device times (events recorded around its work; x_copied:
+// the x upload had events of its own).
+void stats_call(int64_t k, int64_t n, int64_t batch, uint64_t wait_ns, bool x_copied) {
     Ctx &c = ctx();
     float x_ms = 0.0f, k_ms = 0.0f;
-    if (hipEventElapsedTime(&x_ms, c.tev[0], c.tev[1]) != hipSuccess ||
+    if ((x_copied && hipEventElapsedTime(&x_ms, c.tev[0], c.tev[1]) != hipSuccess) ||
         hipEventElapsedTime(&k_ms, c.tev[1], c.tev[2]) != hipSuccess) {
         (void)hipGetLastError();
         return;
@@ -496,14 +520,19 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     // slice (saves a device-to-host copy launch, ~4 us of a ~45 us call); a
     // large one goes to device memory and crosses PCIe as one copy, which
     // beats scattered stores.
-    const bool y_direct = y_bytes <= kDirectYBytes;
+    const bool y_direct = y_bytes <= c.y_direct_max;
+    // A small x can likewise be read by the kernels straight from its staging
+    // slice (coarse-grained pinned memory: the host's writes are visible to a
+    // kernel launched after them, and the GPU's caches serve the re-reads).
+    const bool x_direct = x_bytes <= c.x_direct_max;
     if (x_bytes) memcpy(hx, l, x_bytes);
-    if ((rc = ensure_dev(c.dx, x_bytes ? x_bytes : 4))) return rc;
+    if (!x_direct && (rc = ensure_dev(c.dx, x_bytes ? x_bytes : 4))) return rc;
     if (!y_direct && (rc = ensure_dev(c.dy, y_bytes))) return rc;
     float *const ydst = static_cast<float *>(y_direct ? static_cast<void *>(hy_dev) : c.dy.p);
+    const float *const xsrc = static_cast<const float *>(x_direct ? static_cast<void *>(hx_dev) : c.dx.p);
     const bool timed = c.timing && !defer;
-    if (timed) HIP_TRY(hipEventRecord(c.tev[0], c.stream), "hipEventRecord");
-    if (x_bytes) {
+    if (timed && !x_direct) HIP_TRY(hipEventRecord(c.tev[0], c.stream), "hipEventRecord");
+    if (x_bytes && !x_direct) {
         if (c.x_kernel) {
             HIP_TRY(dmc::launch_copy_from_host(c.dx.p, hx_dev, (int64_t)x_bytes, c.stream), "x upload");
         } else {
@@ -524,14 +553,12 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if (timed) HIP_TRY(hipEventRecord(c.tev[1], c.stream), "hipEventRecord");
     hipError_t e;
     if (rd || cs_as_rd) {
-        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, static_cast<const float *>(c.dx.p), k,
-                         ydst, n, m, k, n, dmc::kWeightSlack};
+        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, n, m, k, n, dmc::kWeightSlack};
         const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
         if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
         e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
     } else {
-        dmc::CsProblem p{static_cast<const uint16_t *>(dw), static_cast<const float *>(c.dx.p),
-                         ydst, m, k, n, batch, ls, rs};
+        dmc::CsProblem p{static_cast<const uint16_t *>(dw), xsrc, ydst, m, k, n, batch, ls, rs};
         const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
         if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
         e = dmc::launch_cs(p, pl, c.ws.p, c.stream);
@@ -550,7 +577,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
     const uint64_t wait_ns = (uint64_t)ns_since(t2);
     c.st.wait_ns += wait_ns;
-    if (timed) stats_call(k, n, batch, wait_ns);
+    if (timed) stats_call(k, n, batch, wait_ns, !x_direct);
     auto t3 = std::chrono::steady_clock::now();
     for (const Pending &p : c.pending) memcpy(p.dst, p.src, p.bytes);
     c.pending.clear();

@@ -103,3 +103,20 @@ def test_registered_weight_survives_evictions(hip, monkeypatch):
     monkeypatch.delenv("DMC_HIP_RESIDENT_CAP")
     hip.release_weights()
     assert hip.resident_count() == 0 and hip.resident_bytes() == 0
+
+
+def test_consecutive_calls_see_each_new_x(hip):
+    """Back-to-back synchronous calls on one resident weight, each with a new
+    activation written into the same staging slice: every result is the
+    oracle's for that call's x (no stale activation survives from the call
+    before, whichever way x reaches the kernels)."""
+    m, k, n = 1, 4096, 1536
+    _, w = data(m, k, n, seed=5)
+    wt = np.ascontiguousarray(w.T)
+    rng = np.random.default_rng(6)
+    xs = [rng.standard_normal((m, k)).astype(np.float32) for _ in range(3)]
+    want = [oracle.matmul_bf16_t(x, w) for x in xs]
+    for i in range(12):
+        y = hip.matmul_bf16_gpu_t(xs[i % 3], w)
+        assert np.array_equal(y.view(np.uint32), hip.matmul_bf16_gpu(xs[i % 3], wt).view(np.uint32)), i
+        check(y, want[i % 3], what=f"call {i}")
