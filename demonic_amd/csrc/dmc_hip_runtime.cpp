@@ -373,7 +373,7 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     const char *cap_s = getenv("DMC_HIP_RESIDENT_CAP");
     const int64_t cap = cap_s && *cap_s ? strtoll(cap_s, nullptr, 10) : 0;
     void *d = nullptr, *raw = nullptr;
-    int rc = residency_rc(c.weights->reserve(bytes, dmc::kWeightSlack, cap, &d), bytes);  // slack: see RdProblem::w_slack
+    int rc = residency_rc(c.weights->reserve(bytes, dmc::kWeightSlack, cap, &d), bytes);
     if (rc) return rc;
     if (t_rows > 0 && (rc = residency_rc(c.weights->reserve_scratch((size_t)bytes, &raw), bytes))) {
         (void)hipFree(d);
@@ -553,7 +553,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     if (timed) HIP_TRY(hipEventRecord(c.tev[1], c.stream), "hipEventRecord");
     hipError_t e;
     if (rd || cs_as_rd) {
-        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, n, m, k, n, dmc::kWeightSlack};
+        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, n, m, k, n};
         const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
         if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
         e = dmc::launch_rd(p, pl, c.ws.p, c.stream);

@@ -723,102 +723,136 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 // The layout of gemv_rd_stream_kernel (NW waves split k; lane l of wave w
 // owns the 8-element windows p = (j*NW + w)*64 + l of every row, x windows
 // in registers, two register buffers of ROWS rows, unconditional loads), for
-// rows that do not start on a 16-byte boundary: each window is one 128-bit
-// buffer load at the row's own 2-byte-aligned offset.  Measured on gfx950:
-// buffer loads honour such offsets exactly, and the range check is per dword
-// of the load (a dword is returned only when it lies wholly inside the
-// range).  The descriptor starts on the 4-byte boundary at or below the first
-// row; its range ends `tail` (0 or 2) bytes past the last element, rounded up
-// to a dword.  A row's last dword may run 2 bytes past the row: inside the
-// range for every row but the matrix's last, whose element K-1 is lost when
-// it sits at an offset of 2 mod 4 with K odd unless 2 bytes of padding follow
-// the matrix (tail = 2) -- the planner only picks this kernel when one of the
-// two holds.  Without padding the range reaches at most 2 bytes past the last
-// element, in the same aligned dword and so the same page.  Elements
-// at or past K (the next row's bits may be inf or NaN), whole windows past K
-// included, become bf16 -0.0 (0x8000); their x is +0.0 (read past the end of
-// x), so each such product is -0.0f, the exact additive identity, and padding
-// never turns a -0.0f chain into +0.0f.  M == 1.
+// rows that do not start on a 16-byte boundary.
 //
-// Short tail: the windows cover elements [0, kmain); the 1 to 8 elements
-// [kmain, K) past the last whole block of windows (K = 4097: one) are one
-// more unaligned load per row, issued once per workgroup before the stream
-// starts by lane r of the last wave for row rb + r, and summed by that lane
-// into a ninth partial.  A last block holding one element would otherwise
-// double every lane's loads for it (K = 4097 measured 53% of peak that way).
+// Every weight load is a 128-bit buffer load at a 4-byte-aligned offset:
+// rows at 2 mod 4 bytes are read from the dword boundary below them, so the
+// lane's window then holds elements 8p - 1 .. 8p + 6 (a shift h = 1), and
+// its x window is shifted the same way once per workgroup.  Measured on
+// gfx950 at C5's size (W[11008, K]): rows at 4- or 8-byte alignment stream at
+// 15.4-15.8 us, rows at 2-byte alignment read there directly 17.4-17.8 us.
+// For the shift to be one per workgroup all its rows share their alignment:
+// with ldw odd (rows alternate between 0 and 2 mod 4), rstep = 2 (`rsh` = 1) and
+// workgroup pair (2b, 2b + 1) takes the even and the odd rows of one block of
+// 2 * rpw consecutive rows; otherwise rstep = 1 and a workgroup takes rpw
+// consecutive rows.
+//
+// The descriptor starts on the 4-byte boundary at or below the workgroup's
+// first row and ends on the dword that holds its last row's last element
+// (at most 2 bytes past the matrix, in the same dword and so the same page);
+// the range check is per dword, so loads past it return zeros.  Elements
+// outside [0, K) (the neighbouring rows' bits may be inf or NaN), whole
+// windows past K included, become bf16 -0.0 (0x8000); their x is +0.0 (read
+// past either end of x), so each such product is -0.0f, the exact additive
+// identity, and padding never turns a -0.0f chain into +0.0f.  M == 1.
+//
+// Short tail: the windows cover elements [0, kmh), kmh = min(kmain, C - h)
+// with C = 8 * KV * NW * 64; the 0 to 8 elements [kmh, K) past the last
+// whole block of windows (K = 4097: one, or two on shifted rows) are read
+// element by element per row, issued once per workgroup before the stream
+// starts by lane i of the last wave for the workgroup's row i, and summed by
+// that lane into a ninth partial.  A last block holding one element would
+// otherwise double every lane's loads for it (K = 4097 measured 53% of peak
+// that way).
 template <int NW, int KV, int ROWS>
 __global__ void __launch_bounds__(64 * NW)
 gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
-                         int K, int kmain, int64_t ldw, int rpw, int tail) {
+                         int K, int kmain, int64_t ldw, int rpw, int rsh) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rb = (int)blockIdx.x * rpw;
-    const int re = min(N, rb + rpw);
+    // The workgroup's rows: rb + rstep * i, i < nr, rstep = 1 << rsh.  (Shifts,
+    // not divisions: a division is expanded on the vector unit, and every
+    // value derived from it -- the loop bounds, the row offsets -- would
+    // follow it into vector registers.)
+    const int rstep = 1 << rsh;
+    const int blk = (int)blockIdx.x >> rsh;
+    const int rb = (blk << rsh) * rpw + ((int)blockIdx.x - (blk << rsh));
+    // nr = 0 for the odd half of a last block with a single row: its
+    // descriptor's range is then empty, so every load returns zeros, and it
+    // stores nothing.  (No early return: the exit test would have to wait for
+    // its kernel arguments before the other arguments are even requested.)
+    const int nr = rb < N ? min(rpw, ((N - 1 - rb) >> rsh) + 1) : 0;
+    const int64_t rlast = rb + (int64_t)max(nr - 1, 0) * rstep;
 
     const uintptr_t base = reinterpret_cast<uintptr_t>(W + (int64_t)rb * ldw) & ~(uintptr_t)3;
-    const uintptr_t end = reinterpret_cast<uintptr_t>(W + (int64_t)(re - 1) * ldw + K);
-    const __amdgpu_buffer_rsrc_t rs =
-        weight_rsrc(reinterpret_cast<const void *>(base), (uint32_t)((end - base + tail + 3) & ~(uintptr_t)3));
+    const uintptr_t end = reinterpret_cast<uintptr_t>(W + rlast * ldw + K);
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(
+        reinterpret_cast<const void *>(base), nr > 0 ? (uint32_t)((end - base + 3) & ~(uintptr_t)3) : 0u);
     const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4u);
 
-    // Row r's first element, in bytes from the descriptor's base.  No branch on
-    // r < re (a branch around a load address makes the compiler wait for every
-    // load in flight): a row past re yields offsets at or past the range's end,
-    // which read zeros or the last row's tail, and its sum is never stored.
-    auto row_off = [&](int r) -> uint32_t {
-        return (uint32_t)(reinterpret_cast<uintptr_t>(W + (int64_t)r * ldw) - base);
+    // Row i's first element, in bytes from the descriptor's base.  No branch
+    // on i < nr (a branch around a load address makes the compiler wait for
+    // every load in flight): a row past the last yields offsets past the
+    // range's end, which read zeros, and its sum is never stored.
+    auto row_off = [&](int i) -> uint32_t {
+        return (uint32_t)(reinterpret_cast<uintptr_t>(W + (rb + (int64_t)rstep * i) * ldw) - base);
     };
+    const int h = (int)((row_off(0) >> 1) & 1);  // every row's shift, in elements
+    const int kmh = min(kmain, KV * NW * 512 - h);
 
-    // The short tail's weights, loaded by the last wave only (lane r for row
-    // rb + r), before any other load: the first wait covers them, so the
-    // branch adds no wait of its own.  Element by element (2-byte loads):
-    // none reaches past element K-1, so the matrix's last element needs no
-    // padding behind it.  Its x comes through the scalar cache.
-    const int rem = K - kmain;  // 0 .. 8
+    // The short tail's weights, loaded by the last wave only (lane i for row
+    // i), before any other load: the first wait covers them, so the branch
+    // adds no wait of its own.  Element by element (2-byte loads), none past
+    // element K-1.  Its x comes through the scalar cache.
+    const int rem = K - kmh;  // 0 .. 8
     uint32_t tw[8] = {};
     if (rem > 0 && wave == NW - 1) {
-        const uint32_t tbase = lane < re - rb ? row_off(rb + lane) + (uint32_t)kmain * 2u : kOutOfRange;
+        const uint32_t tbase = lane < nr ? row_off(lane) + (uint32_t)kmh * 2u : kOutOfRange;
 #pragma unroll
         for (int e = 0; e < 8; ++e)
             tw[e] = __builtin_amdgcn_raw_buffer_load_b16(rs, e < rem ? tbase + 2u * e : kOutOfRange, 0, 0);
     }
 
+    // Window p: the 16 bytes at 16p past the row's dword boundary, elements
+    // 8p - h + c (c < 8); x[8p .. 8p + 7], and x[8p - 1], which the shift
+    // brings in (from the lane below, or for a wave's first lane through the
+    // scalar cache: a vector load of it for every lane measured 1.2 us per
+    // C5-sized launch).
     uint32_t coff[KV];
     uint32_t mask[KV][4];
     u32x4 xa[KV], xb[KV];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
         const int p = (j * NW + wave) * 64 + lane;
-        const int valid = min(max(kmain - 8 * p, 0), 8);  // elements of window p inside the row
-        coff[j] = valid > 0 ? (uint32_t)p * 16u : kOutOfRange;
+        const int lo = 8 * p - h;  // element of the window's first half-word
+        coff[j] = lo < kmh ? (uint32_t)p * 16u : kOutOfRange;
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-            mask[j][d] = (2 * d < valid ? 0x0000ffffu : 0u) | (2 * d + 1 < valid ? 0xffff0000u : 0u);
-        const uint32_t xo = valid > 0 ? (uint32_t)p * 32u : kOutOfRange;
-        xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
-        xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
+        for (int d = 0; d < 4; ++d) {
+            const int e0 = lo + 2 * d, e1 = e0 + 1;
+            mask[j][d] = (e0 >= 0 && e0 < kmh ? 0x0000ffffu : 0u) | (e1 >= 0 && e1 < kmh ? 0xffff0000u : 0u);
+        }
+        xa[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)p * 32u, 0, 0);
+        xb[j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (uint32_t)p * 32u + 16u, 0, 0);
     }
-    const float init = (wave * 64 + lane) * 8 < kmain ? 0.0f : -0.0f;
+    const float init = 8 * (wave * 64 + lane) - h < kmh ? 0.0f : -0.0f;
 
     __shared__ float red[NW + 1][kMaxRpw];  // row NW: the short tail's partials
     u32x4 ba[ROWS][KV], bb[ROWS][KV];
-    auto load = [&](u32x4 (&wv)[ROWS][KV], int r0) {
+    // Row i's dword boundary: aoff0 + i * rstride bytes.
+    const uint32_t aoff0 = row_off(0) - 2u * (uint32_t)h;
+    const uint32_t rstride = (uint32_t)(rstep * ldw * 2);
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
-            const uint32_t o = row_off(r0 + q);
+            const uint32_t o = aoff0 + (uint32_t)(i0 + q) * rstride;
 #pragma unroll
             for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, coff[j], o);
         }
     };
-    load(ba, rb);
+    load(ba, 0);
     float xr[KV][8];
 #pragma unroll
-    for (int j = 0; j < KV; ++j)
+    for (int j = 0; j < KV; ++j) {
+        const int p0 = (j * NW + wave) * 64;  // the wave's first window
+        const float xfirst = p0 > 0 ? X[8 * p0 - 1] : 0.0f;
+        const float x0[8] = {__uint_as_float(xa[j][0]), __uint_as_float(xa[j][1]), __uint_as_float(xa[j][2]),
+                             __uint_as_float(xa[j][3]), __uint_as_float(xb[j][0]), __uint_as_float(xb[j][1]),
+                             __uint_as_float(xb[j][2]), __uint_as_float(xb[j][3])};
+        const float below = __shfl_up(x0[7], 1, 64);  // x[8p - 1] for every lane but the first
+        xr[j][0] = h ? (lane == 0 ? xfirst : below) : x0[0];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            xr[j][q] = __uint_as_float(xa[j][q]);
-            xr[j][q + 4] = __uint_as_float(xb[j][q]);
-        }
+        for (int c = 1; c < 8; ++c) xr[j][c] = h ? x0[c - 1] : x0[c];
+    }
     // hm: the window mask limited to the halves whose x is nonzero
     // (nonzero_pair); each lane's partial is zero-folded before the wave sum.
     uint32_t hm[KV][4];
@@ -831,20 +865,20 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
         bool hit = false;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float xv = X[kmain + min(e, rem - 1)];
+            const float xv = X[kmh + min(e, rem - 1)];
             const uint32_t v = e < rem ? tw[e] : 0x8000u;  // past K: -0 against +0, the exact additive identity
             const float p = e < rem ? xv : 0.0f;
             t = fmaf(p, __uint_as_float(v << 16), t);
             hit |= p != 0.0f && (v & 0x7fffu) != 0;
         }
-        if (lane < re - rb) red[NW][lane] = zero_fold(t, hit);
+        if (lane < nr) red[NW][lane] = zero_fold(t, hit);
     }
 
-    // A wave whose windows of the last block all lie past kmain skips that
+    // A wave whose windows of the last block all lie past kmh skips that
     // block's arithmetic (a wave-uniform branch around arithmetic only; its
     // loads, out of range, stay unconditional).
-    const bool last_block = (((KV - 1) * NW + wave) * 64) * 8 < kmain;
-    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int r0) {
+    const bool last_block = 8 * (((KV - 1) * NW + wave) * 64) - h < kmh;
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
             float acc = init;
@@ -861,27 +895,28 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
                 }
             }
             const float s = wave_sum_dpp(zero_fold(acc, nz != 0));
-            if (lane == 0 && r0 + q < re) red[wave][r0 - rb + q] = s;
+            if (lane == 0 && i0 + q < nr) red[wave][i0 + q] = s;
         }
     };
-    for (int r0 = rb; r0 < re; r0 += 2 * ROWS) {
-        load(bb, r0 + ROWS);
-        sum_rows(ba, r0);
-        if (r0 + ROWS >= re) break;
-        load(ba, r0 + 2 * ROWS);
-        sum_rows(bb, r0 + ROWS);
+    for (int i0 = 0; i0 < nr; i0 += 2 * ROWS) {
+        load(bb, i0 + ROWS);
+        sum_rows(ba, i0);
+        if (i0 + ROWS >= nr) break;
+        load(ba, i0 + 2 * ROWS);
+        sum_rows(bb, i0 + ROWS);
     }
     __syncthreads();
-    for (int t0 = wave * 64; t0 < re - rb; t0 += 64 * NW) {  // as gemv_rd_stream_kernel's
+    for (int t0 = wave * 64; t0 < nr; t0 += 64 * NW) {  // as gemv_rd_stream_kernel's
         const int t = t0 + lane;
-        const bool live = t < re - rb;
-        const int r = live ? t : 0;
-        float s = red[0][r];
+        const bool live = t < nr;
+        const int i = live ? t : 0;
+        float s = red[0][i];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w][r];
-        if (rem > 0) s += red[NW][r];
-        s = zero_unfold(s, live, X, W + (int64_t)(rb + r) * ldw, 1, K);
-        if (live) Y[rb + r] = s;
+        for (int w = 1; w < NW; ++w) s += red[w][i];
+        if (rem > 0) s += red[NW][i];
+        const int64_t row = rb + (int64_t)rstep * i;
+        s = zero_unfold(s, live, X, W + row * ldw, 1, K);
+        if (live) Y[row] = s;
     }
 }
 
@@ -2388,7 +2423,7 @@ hipError_t rd_unaligned_go(const RdProblem &p, const RdPlan &pl, hipStream_t s) 
     if (pl.rows != ROWS) return hipErrorInvalidValue;
     hipLaunchKernelGGL((gemv_rd_unaligned_kernel<NW, KV, ROWS>), dim3((unsigned)pl.grid_x), dim3(64 * NW), 0, s, p.w,
                        p.x, p.y, (int)p.n, (int)p.k, (int)(pl.kmain > 0 ? pl.kmain : p.k), p.ldw, pl.rpw,
-                       p.w_slack >= 2 ? 2 : 0);
+                       pl.rstep == 2 ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -2559,6 +2594,58 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
 
 }  // namespace
 
+// Streaming over rows at any 2-byte alignment (odd K, offset views), or over
+// aligned rows with a short tail: M == 1, x 16-byte aligned.
+static bool plan_unaligned(const RdProblem &p, int vec, int64_t cus, RdPlan &sp) {
+    if (!(p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) &&
+          env_int("DMC_HIP_RD_UNALIGNED", 1) != 0))
+        return false;
+    const int nw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
+    const int64_t block = (int64_t)nw * 512;
+    // Rows read from the dword below them (ldw odd, or W at 2 mod 4) have
+    // windows shifted by one element, which leaves one more element to the
+    // short tail (at most 8 in all).
+    const bool shifted = (p.ldw & 1) != 0 || !aligned(p.w, 4);
+    const int64_t over = p.k % block;
+    // 1..8 elements past whole blocks of windows (k = 4097) go to each row's
+    // short tail, read element by element; otherwise the last block of
+    // windows holds the rest.
+    const bool short_tail = p.k > block && over >= 1 && over <= (shifted ? 7 : 8) &&
+                            env_int("DMC_HIP_RD_SHORT_TAIL", 1) != 0;
+    const int kv = short_tail ? (int)(p.k / block) : (int)((p.k + block - 1) / block);
+    // ldw odd: rows alternate between 0 and 2 mod 4 bytes, and a workgroup
+    // takes every other row of a block of 2 * rpw, so all its rows share one
+    // alignment (see the kernel).
+    const int rstep = (p.ldw & 1) ? 2 : 1;
+    const int rpw_default = kv >= 2 ? 8 : 4;
+    const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
+    auto groups = [&](int r) { return (p.n + (int64_t)rstep * r - 1) / ((int64_t)rstep * r) * rstep; };
+    int rpw = rpw_default;
+    while (rpw > 2 && groups(rpw) < min_blocks) rpw >>= 1;
+    // Only when the last block of windows is at least half full, or the
+    // rest is a short tail: measured on MI355X against the general
+    // kernel, k = 4095 67% vs 57% of peak, 11007 64% vs 60%, 14335 64% vs
+    // 56%, but k = 4097 as a one-element last block 53% vs 61%.
+    // KV = 8 (k above 28,680) would need more than 256 VGPRs with the
+    // product masks: the general kernel takes it.
+    if (!(kv <= 7 && (short_tail || p.k - (kv - 1) * block >= block / 2) &&
+          ((int64_t)rstep * rpw * p.ldw + 8) * 2 <= INT32_MAX && groups(rpw) <= INT32_MAX))
+        return false;
+    sp = RdPlan{};
+    sp.vec = vec;
+    sp.rows = (kv <= 4 && kv != 2) ? 2 : 1;
+    sp.mt = 1;
+    sp.waves = nw;
+    sp.kvec = kv;
+    sp.rpw = rpw;
+    sp.any_align = true;
+    sp.rstep = rstep;
+    sp.grid_x = groups(rpw);
+    sp.grid_y = 1;
+    sp.kmain = short_tail ? kv * block : p.k;
+    return true;
+}
+
 RdPlan plan_rd(const RdProblem &p, int num_cus) {
     RdPlan pl{};
     // Widest load the row alignment allows: every row start, every activation
@@ -2694,50 +2781,19 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
                 sp.rpw = rpw;
                 sp.grid_x = (p.n + rpw - 1) / rpw;
             }
+            // A last block of windows holding 1..8 elements (k = 4104) costs
+            // the streaming kernel a whole extra block of loads; the unaligned
+            // kernel's short tail reads them element by element (W[11008, 4104]:
+            // 17.5 us streaming, W[11008, 4100] 15.8 us with the short tail).
+            RdPlan up{};
+            if (p.m == 1 && plan_unaligned(p, pl.vec, cus, up) && up.kmain < p.k) return up;
             return sp;
         }
     }
 
-    // Streaming over misaligned rows (odd K, offset views) with unaligned
-    // 128-bit loads: M == 1, x 16-byte aligned, and the matrix's last element
-    // readable (padding after it, or not at 2 mod 4 with K odd; see the kernel).
-    const uintptr_t last_elem = reinterpret_cast<uintptr_t>(p.w + ((p.n - 1) * p.ldw + p.k - 1));
-    const bool last_ok = p.w_slack >= 2 || !((last_elem & 3) == 2 && (p.k & 1) == 1);
-    const int unw = p.k <= 512 ? 1 : p.k <= 1024 ? 2 : p.k <= 2048 ? 4 : 8;
-    // 1..8 elements past whole blocks of windows (k = 4097) go to each row's
-    // short tail, read element by element (so the matrix's last element is
-    // always readable); otherwise the last block of windows holds the rest.
-    const bool short_tail = p.k > (int64_t)unw * 512 && p.k % ((int64_t)unw * 512) >= 1 &&
-                            p.k % ((int64_t)unw * 512) <= 8 && env_int("DMC_HIP_RD_SHORT_TAIL", 1) != 0;
-    if (pl.vec < 8 && p.m == 1 && p.k >= 1 && p.k <= 32768 && p.ldw >= p.k && aligned(p.x, 16) &&
-        (last_ok || short_tail) && env_int("DMC_HIP_RD_UNALIGNED", 1) != 0) {
-        const int nw = unw;
-        const int64_t block = (int64_t)nw * 512;
-        const int kv = short_tail ? (int)(p.k / block) : (int)((p.k + block - 1) / block);
-        const int rpw_default = kv >= 2 ? 8 : 4;
-        const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
-        int rpw = rpw_default;
-        while (rpw > 2 && (p.n + rpw - 1) / rpw < min_blocks) rpw >>= 1;
-        // Only when the last block of windows is at least half full, or the
-        // rest is a short tail: measured on MI355X against the general
-        // kernel, k = 4095 67% vs 57% of peak, 11007 64% vs 60%, 14335 64% vs
-        // 56%, but k = 4097 as a one-element last block 53% vs 61%.
-        // KV = 8 (k above 28,680) would need more than 256 VGPRs with the
-        // product masks: the general kernel takes it.
-        if (kv <= 7 && (short_tail || p.k - (kv - 1) * block >= block / 2) && ((int64_t)rpw * p.ldw + 8) * 2 <= INT32_MAX &&
-            (p.n + rpw - 1) / rpw <= INT32_MAX) {
-            RdPlan sp{};
-            sp.vec = pl.vec;
-            sp.rows = (kv <= 4 && kv != 2) ? 2 : 1;
-            sp.mt = 1;
-            sp.waves = nw;
-            sp.kvec = kv;
-            sp.rpw = rpw;
-            sp.grid_x = (p.n + rpw - 1) / rpw;
-            sp.grid_y = 1;
-            sp.kmain = short_tail ? kv * block : p.k;
-            return sp;
-        }
+    if (pl.vec < 8) {
+        RdPlan up{};
+        if (plan_unaligned(p, pl.vec, cus, up)) return up;
     }
 
     // General kernel.
@@ -2922,7 +2978,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         }
         return hipErrorInvalidValue;
     }
-    if (pl.kvec > 0 && pl.vec < 8) return rd_unaligned_dispatch(p, pl, s);
+    if (pl.kvec > 0 && pl.any_align) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0 && pl.waves == 16) {
         if (pl.rows != 2 || (pl.rpw != 8 && pl.rpw != 16 && pl.rpw != 32) || p.m != 1 || p.k > kXldsMaxK)
             return hipErrorInvalidValue;

@@ -27,10 +27,12 @@ struct RdProblem {
     float *y;           // [m, ldy]
     int64_t ldy;        // elements between output rows (>= n)
     int64_t m, k, n;
-    int64_t w_slack = 0;  // bytes readable past the last weight element (allocation padding)
 };
 
-// Padding the library allocates after every resident weight.
+// Padding the library allocates after every resident weight and weight
+// region: the any-alignment kernel reads whole dwords, so it may read up to 2
+// bytes past a matrix whose last element ends at 2 mod 4 (within the same
+// dword, and here within the allocation too).
 constexpr int64_t kWeightSlack = 16;
 
 struct CsProblem {
@@ -71,6 +73,12 @@ struct RdPlan {
     // streaming over misaligned rows: windows cover k < kmain, and the 1..8
     // elements [kmain, k) are each row's short tail (0: kmain = k)
     int64_t kmain = 0;
+    // streaming over rows at any 2-byte alignment (any_align): a workgroup's
+    // rows are rstep apart (2 when ldw is odd, so that they share one
+    // alignment), rstep consecutive workgroups sharing a block of rstep * rpw
+    // rows
+    bool any_align = false;
+    int rstep = 1;
     size_t workspace_bytes = 0;
 };
 

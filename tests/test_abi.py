@@ -147,12 +147,23 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
 
 
 @pytest.mark.parametrize("k,waves,kvec", [(8, 1, 1), (512, 1, 1), (520, 2, 1), (1024, 2, 1),
-                                          (2048, 4, 1), (4096, 8, 1), (4104, 8, 2),
+                                          (2048, 4, 1), (4096, 8, 1), (4160, 8, 2),
                                           (11008, 8, 3), (32768, 8, 8)])
 def test_rowdot_streaming_kernel_covers_k(k, waves, kvec):
     p = d.plan("rd", 1, k, 1000, x_addr=256, w_addr=256)
     assert (p.waves, p.slices) == (waves, kvec), p
     assert waves * kvec * 512 >= k > (waves * kvec - waves) * 512 or kvec == 1
+
+
+def test_rowdot_aligned_rows_with_a_short_last_block_take_the_short_tail():
+    """Aligned rows whose last block of windows would hold 1..8 elements
+    (k = 4104: 8) stream one block per lane plus a per-row short tail on the
+    any-alignment kernel (reported with vec = 8) instead of a second, nearly
+    empty block; at m >= 2 the streaming kernel keeps them."""
+    p = d.plan("rd", 1, 4104, 11008, x_addr=256, w_addr=256)
+    assert (p.vec, p.waves, p.slices, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, 8, 1, 2, 4, 2752), p
+    assert d.plan("rd", 2, 4104, 11008, x_addr=256, w_addr=256).slices == 2
+    assert d.plan("rd", 1, 4105, 1001, x_addr=256, w_addr=256).slices == 0   # 9 over: the general kernel
 
 
 def test_rowdot_mfma_layouts(monkeypatch):
@@ -243,14 +254,18 @@ def test_rowdot_misaligned_rows_stream_unaligned(k, w, waves, kvec, rows):
     assert p.grid_x * p.rows_per_group >= 11007
 
 
-def test_rowdot_unaligned_needs_a_readable_last_element():
-    """Odd k and n even put the matrix's last element at 2 mod 4: its 128-bit
-    window would need 2 bytes past the caller's allocation, so a caller's
-    weight gets the general kernel (the drop-in's resident copies carry
-    padding and keep the unaligned kernel)."""
-    assert d.plan("rd", 1, 4095, 11008, x_addr=256, w_addr=256).slices == 0
-    assert d.plan("rd", 1, 4095, 11007, x_addr=256, w_addr=256).slices == 1
-    assert d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=258).slices == 1   # k even: never straddles
+def test_rowdot_unaligned_reads_whole_dwords_only():
+    """The any-alignment kernel reads every row from the dword boundary at or
+    below its start, so the dword holding the matrix's last element always
+    lies inside the descriptor (odd k with n even puts that element at 2 mod
+    4: it still streams).  With ldw odd the rows alternate between 0 and 2
+    mod 4, and each workgroup takes every other row of a block of 2 * rpw."""
+    for n in (11008, 11007):
+        p = d.plan("rd", 1, 4095, n, x_addr=256, w_addr=256)
+        assert (p.vec, p.slices, p.rows_per_group) == (1, 1, 4), p
+        assert p.grid_x == 2 * ((n + 7) // 8), p
+    p = d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=258)   # k even, W at 2 mod 4: every row shifted
+    assert (p.vec, p.slices, p.grid_x) == (1, 1, 2752), p
 
 
 def test_rowdot_unaligned_needs_a_well_filled_last_block_or_a_short_tail():
@@ -258,8 +273,8 @@ def test_rowdot_unaligned_needs_a_well_filled_last_block_or_a_short_tail():
     windows is at least half full (k = 4095), or when 1..8 elements are left
     past whole blocks (k = 4097, 8199: a per-row short tail, read element by
     element, so no padding behind the matrix is needed); a last block holding
-    9 to 2047 elements goes to the general kernel (k = 4105), as does k = 7
-    with no padding after an element at 2 mod 4."""
+    9 to 2047 elements goes to the general kernel (k = 4105), as does a
+    single block less than half full (k = 7)."""
     p = d.plan("rd", 1, 4097, 11007, x_addr=256, w_addr=256)
     assert (p.slices, p.waves, p.rows_per_group) == (1, 8, 4), p
     assert d.plan("rd", 1, 8199, 4097, x_addr=256, w_addr=256).slices == 2

@@ -181,8 +181,9 @@ SHAPES = [
     (2, 64, 17), (3, 129, 31), (5, 1024, 100), (8, 520, 24), (16, 4096, 40),
     (17, 300, 11), (33, 96, 65), (1, 12288, 6),
     # misaligned rows with a short tail past whole blocks of windows: one
-    # element (4097), two (4098), seven (8199, 12295: two and three blocks)
-    (1, 4097, 600), (1, 4098, 70), (1, 8199, 300), (1, 12295, 64),
+    # element (4097), two (4098), seven (4103, 8199, 12295: one, two and
+    # three blocks); aligned rows with eight (4104)
+    (1, 4097, 600), (1, 4098, 70), (1, 8199, 300), (1, 12295, 64), (1, 4103, 300), (1, 4104, 301),
 ]
 
 
@@ -889,13 +890,13 @@ def test_skinny_mfma_shapes_within_bound(hip, m, k, n, kind, monkeypatch):
 
 # ---- row-dot streaming with x shared through LDS (16-wave workgroups, M = 1) ----------
 
-XLDS_SHAPES = [(4096, 14336), (4096, 4104), (8192, 8192), (4096, 16384), (16380, 12288)]
+XLDS_SHAPES = [(4096, 14336), (4096, 4112), (8192, 8192), (4096, 16384), (16380, 12288)]
 
 
 @pytest.mark.parametrize("n,k", XLDS_SHAPES)
 def test_shared_x_workgroups(hip, n, k, monkeypatch):
     """Long rows at M = 1 on 16-wave workgroups whose halves share one LDS
-    copy of x: a last window holding one element (k = 4104), the largest K it
+    copy of x: a last block of two windows (k = 4112), the largest K it
     takes, two rounds (n = 8192), and a partial last workgroup whose second
     half holds 4 rows (n = 16380, four rounds)."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
@@ -904,7 +905,7 @@ def test_shared_x_workgroups(hip, n, k, monkeypatch):
     check(run_rd(hip, x, w), ref(x, w), what=f"xlds n={n} k={k}")
 
 
-@pytest.mark.parametrize("k", [4104, 14336])
+@pytest.mark.parametrize("k", [4112, 14336])
 def test_shared_x_zero_signs(hip, k, monkeypatch):
     """The zero-sign rule of test_underflowing_products_keep_their_zero_sign on
     the shared-x layout: even rows end at -0.0, odd rows at +0.0."""
