@@ -1909,7 +1909,7 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
 // of the workgroup's k rows, so x[m][k] is the same for the whole wave and
 // comes through the scalar cache.  The waves' partials meet in LDS in a fixed
 // order; with one k slice the workgroup writes y, otherwise its partial goes
-// to P[s] and sum_slices_stream_kernel adds the slices in slice order.
+// to P[s] and sum_slices_stream_kernel adds the slices in a fixed order.
 // (Finishing inside the same launch needs device-scope fences, which on a
 // multi-XCD part write back and invalidate the whole L2 per workgroup:
 // measured 5x slower than the second launch.)
@@ -2060,41 +2060,51 @@ __device__ __forceinline__ float cs_unfold(float v, bool live, int64_t i, const 
 }
 
 // The streaming kernel's pass.  A workgroup owns 64 consecutive outputs; its
-// 4 waves take slices j = w, w+4, ... (coalesced 256-byte reads), and the four
-// partial sums meet in LDS in wave order.  Every element's order is fixed.
+// NWS waves take slices j = w, w+NWS, ... (coalesced 256-byte reads), and the
+// NWS partial sums meet in LDS in wave order.  Every element's order is fixed.
+// 16 waves when there are at least 16 slices, so that each lane has at most a
+// few partials to fetch and they are all in flight at once (the pass is
+// latency-bound: the partials were just written through other XCDs' L2s).
 // With `last_row` set (the UN streaming kernel left out the matrix's last
 // row): y[i] = fmaf(x[z][m][K-1], w[z][K-1][n], that sum), the chain's final
-// step.
-__global__ void __launch_bounds__(256)
+// step; wave 0 fetches those two operands before the partials.
+template <int NWS>
+__global__ void __launch_bounds__(64 * NWS)
 sum_slices_stream_kernel(const float *__restrict__ P, int64_t p_slice, int slices, float *__restrict__ Y,
                          int64_t count, const CsSrc src) {
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t i = (int64_t)blockIdx.x * 64 + lane;
+    const bool live = i < count;
+    float xv = 0.0f;
+    uint32_t wb = 0;
+    if (src.last_row && wave == 0 && live) {
+        const int64_t mn = src.M * src.N;
+        const int64_t z = i / mn, r = i - z * mn;
+        const int64_t m = r / src.N, n = r - m * src.N;
+        xv = src.x[z * src.ls + m * src.K + (src.K - 1)];
+        wb = src.w[z * src.rs + (src.K - 1) * src.N + n];
+    }
     float s = -0.0f;
     bool first = true;
-    if (i < count) {
-#pragma unroll 8
-        for (int j = wave; j < slices; j += 4) {
+    if (live) {
+#pragma unroll 4
+        for (int j = wave; j < slices; j += NWS) {
             const float v = P[(int64_t)j * p_slice + i];
             s = first ? v : s + v;
             first = false;
         }
     }
-    __shared__ float part[4][64];
+    __shared__ float part[NWS][64];
     part[wave][lane] = s;
     __syncthreads();
     if (wave == 0) {
-        const bool live = i < count;
-        float v = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
-        if (src.last_row && live) {
-            const int64_t z = i / (src.M * src.N), r = i - z * src.M * src.N;
-            const int64_t m = r / src.N, n = r - m * src.N;
-            const float xv = src.x[z * src.ls + m * src.K + (src.K - 1)];
-            const uint32_t wb = src.w[z * src.rs + (src.K - 1) * src.N + n];
+        float v = part[0][lane];
+#pragma unroll
+        for (int w = 1; w < NWS; ++w) v += part[w][lane];
+        if (src.last_row && live)
             v = zero_fold(fmaf(xv, __uint_as_float(wb << 16), v),
                           !(v == 0.0f && __builtin_signbit(v)) || (xv != 0.0f && (wb & 0x7fffu) != 0));
-        }
         v = cs_unfold(v, live, i, src);
         if (live) Y[i] = v;
     }
@@ -3027,8 +3037,12 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
         if (pl.slices > 1 || pl.unaligned) {
             const int64_t total = p.m * p.n * p.batch;
             const CsSrc src{p.w, p.x, p.rs, p.ls, p.k, p.n, p.m, pl.unaligned};
-            hipLaunchKernelGGL(sum_slices_stream_kernel, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, s, P,
-                               total, (int)pl.slices, p.y, total, src);
+            if (pl.slices >= 16)
+                hipLaunchKernelGGL(sum_slices_stream_kernel<16>, dim3((unsigned)((total + 63) / 64)), dim3(1024), 0,
+                                   s, P, total, (int)pl.slices, p.y, total, src);
+            else
+                hipLaunchKernelGGL(sum_slices_stream_kernel<4>, dim3((unsigned)((total + 63) / 64)), dim3(256), 0, s,
+                                   P, total, (int)pl.slices, p.y, total, src);
             return hipGetLastError();
         }
         return hipSuccess;
