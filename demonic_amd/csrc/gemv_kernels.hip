@@ -1228,17 +1228,21 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 // streams from HBM once per 16 * MB rows (the 16-row layouts stream it once
 // per 16).  x arrives already split: split_x_planes_kernel writes its three
 // bf16 terms once per call as planes [3][M][K], and each chunk's operands are
-// copied into LDS (no per-workgroup split).  When 256-row by 16*MB-row tiles
+// copied into LDS (no per-workgroup split).  FUSE (16-row activation tiles):
+// each workgroup loads its chunks of x as f32 and splits them itself on the
+// way into LDS instead, which saves the split launch; at 16 activation rows
+// the repeated split is a few dozen values per thread.  When 256-row by 16*MB-row tiles
 // would leave the device short of workgroups, k is split over `slices`
 // workgroups, each covering kc chunks of 64, whose partial sums go to
 // P[slice][m][n] for gemm_sum_slices_kernel.  Numerics, special values and
 // the zero rule are the wide layout's, tile by tile; with slices the zero
 // rule runs after the sum.
-template <int MB>
+template <int MB, bool FUSE>
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, const uint16_t *__restrict__ XS,
                          float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy) {
     static_assert(MB >= 1 && MB <= 4, "x staging covers at most 512 threads");
+    static_assert(!FUSE || MB == 1, "the in-kernel split serves 16-row activation tiles");
     constexpr int D = 2;  // register sets of the chunk ring (3 and 4 measured no faster)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1279,33 +1283,54 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     for (int j = 0; j < 4; ++j)
         soff[j] = (uint32_t)min(wave * 32 + slr + 8 * j, nrows - 1) * (uint32_t)K * 2u + scol;
     // x items: threads 0 .. 128*MB-1 = (tile xt = tid/128, k-block b = tid/64 % 2,
-    // operand lane): the lane's 8 elements of each of the three planes, by
-    // unconditional buffer loads (rows past M load from past the range: zeros).
+    // operand lane): the lane's 8 elements of each of the three planes (FUSE:
+    // its 8 f32 values, split in `store`), by unconditional buffer loads (rows
+    // past M load from past the range: zeros).
     const bool xthread = tid < 128 * MB;
     const int xt = tid >> 7;
     const int xb = (tid >> 6) & 1;
     const int xm = m0 + xt * 16 + (lane & 15);
     const uint32_t plane_bytes = (uint32_t)M * (uint32_t)K * 2u;
-    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(XS, 3u * plane_bytes);
-    const uint32_t xoff = xthread && xm < M ? ((uint32_t)xm * (uint32_t)K + xb * 32 + (lane >> 4) * 8) * 2u : kOutOfRange;
+    const __amdgpu_buffer_rsrc_t xrs = FUSE ? weight_rsrc(X, 2u * plane_bytes) : weight_rsrc(XS, 3u * plane_bytes);
+    const uint32_t xelem = (uint32_t)xm * (uint32_t)K + xb * 32 + (lane >> 4) * 8;
+    const uint32_t xoff = xthread && xm < M ? xelem * (FUSE ? 4u : 2u) : kOutOfRange;
 
+    constexpr int XQ = FUSE ? 2 : 3;  // x registers per chunk: f32 halves, or the three planes
     struct Regs {
         u32x4 w[4];
-        u32x4 x[3];
+        u32x4 x[XQ];
     };
     auto load = [&](int c, Regs &r) {
         const uint32_t cb = (uint32_t)(c0 + c) * 128u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + cb);
+        if constexpr (FUSE) {
 #pragma unroll
-        for (int q = 0; q < 3; ++q) r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, q * plane_bytes + cb, 0);
+            for (int q = 0; q < 2; ++q) r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, 2u * cb + 16u * q, 0);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 3; ++q)
+                r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, q * plane_bytes + cb, 0);
+        }
     };
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
         if (xthread) {
+            if constexpr (FUSE) {
+                const float v[8] = {__uint_as_float(r.x[0][0]), __uint_as_float(r.x[0][1]),
+                                    __uint_as_float(r.x[0][2]), __uint_as_float(r.x[0][3]),
+                                    __uint_as_float(r.x[1][0]), __uint_as_float(r.x[1][1]),
+                                    __uint_as_float(r.x[1][2]), __uint_as_float(r.x[1][3])};
+                u32x4 hi, md, lo;
+                split8(v, hi, md, lo);
+                xpl[xbuf][xt][xb][0][lane] = hi;
+                xpl[xbuf][xt][xb][1][lane] = md;
+                xpl[xbuf][xt][xb][2][lane] = lo;
+            } else {
 #pragma unroll
-            for (int q = 0; q < 3; ++q) xpl[xbuf][xt][xb][q][lane] = r.x[q];
+                for (int q = 0; q < 3; ++q) xpl[xbuf][xt][xb][q][lane] = r.x[q];
+            }
         }
     };
 
@@ -1470,6 +1495,7 @@ gemm_sum_slices_kernel(const float *__restrict__ P, int slices, float *__restric
     const int64_t count = (int64_t)M * N;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
         float s = P[i];
+#pragma unroll 8
         for (int j = 1; j < slices; ++j) s += P[j * count + i];
         if (s == 0.0f) {
             const int m = (int)(i / N), n = (int)(i - (int64_t)m * N);
@@ -2745,7 +2771,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             want = std::max<int64_t>(want, 1);
             mp.kchunks = (int)((nchunks + want - 1) / want);
             mp.kslices = (int)((nchunks + mp.kchunks - 1) / mp.kchunks);
-            const size_t planes = ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
+            // 16-row activation tiles split x in the kernel (no planes; C2 down
+            // at m = 16: the split launch cost 3-4 us of 37).
+            mp.xfuse = mp.mt == 16 && env_int("DMC_HIP_GEMM_FUSE", 1) != 0;
+            const size_t planes = mp.xfuse ? 0 : ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
             mp.workspace_bytes = planes + (mp.kslices > 1 ? (size_t)mp.kslices * p.m * p.n * 4 : 0);
         } else if (mp.mkind == 6) {
             mp.rpw = kWideRows;
@@ -2953,20 +2982,22 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             if (!workspace || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 || pl.kslices > 65535 ||
                 (int64_t)pl.kslices * pl.kchunks < p.k / 64)
                 return hipErrorInvalidValue;
-            uint16_t *xs = static_cast<uint16_t *>(workspace);
-            const size_t planes = ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
+            if (pl.xfuse && pl.mt != 16) return hipErrorInvalidValue;
+            uint16_t *xs = pl.xfuse ? nullptr : static_cast<uint16_t *>(workspace);
+            const size_t planes = pl.xfuse ? 0 : ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
             float *part = pl.kslices > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + planes) : nullptr;
             const int64_t count = p.m * p.k;
-            hipLaunchKernelGGL(split_x_planes_kernel, dim3(stride_grid((count / 8 + 255) / 256)), dim3(256), 0, s,
-                               p.x, xs, count);
+            if (!pl.xfuse)
+                hipLaunchKernelGGL(split_x_planes_kernel, dim3(stride_grid((count / 8 + 255) / 256)), dim3(256), 0,
+                                   s, p.x, xs, count);
             const int64_t wgs = pl.grid_x * pl.grid_y * (int64_t)pl.kslices;
             if (wgs > INT32_MAX) return hipErrorInvalidValue;
-#define DMC_GEMM(MB)                                                                                         \
-    if (pl.mt == 16 * MB)                                                                                    \
-        hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB>), dim3((unsigned)wgs), dim3(512), 0, s, p.w, p.x, xs,     \
+#define DMC_GEMM(MB, F)                                                                                      \
+    if (pl.mt == 16 * MB && pl.xfuse == F)                                                                   \
+        hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB, F>), dim3((unsigned)wgs), dim3(512), 0, s, p.w, p.x, xs,  \
                            p.y, part, (int)p.n, (int)p.k, (int)p.m, pl.kchunks, (int)pl.grid_x, (int)pl.grid_y);  \
     else
-            DMC_GEMM(1) DMC_GEMM(2) DMC_GEMM(4) return hipErrorInvalidValue;
+            DMC_GEMM(1, true) DMC_GEMM(1, false) DMC_GEMM(2, false) DMC_GEMM(4, false) return hipErrorInvalidValue;
 #undef DMC_GEMM
             if (pl.kslices > 1)
                 hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,

@@ -70,6 +70,7 @@ struct RdPlan {
     // gemm layout (mkind 8): k split over `kslices` workgroups of `kchunks`
     // 64-element chunks each; workspace for x's bf16 planes and the partials
     int kslices = 1, kchunks = 0;
+    bool xfuse = false;  // gemm layout, 16-row activation tiles: x split inside the kernel (no planes)
     // streaming over misaligned rows: windows cover k < kmain, and the 1..8
     // elements [kmain, k) are each row's short tail (0: kmain = k)
     int64_t kmain = 0;
