@@ -182,6 +182,9 @@ def main(argv=None) -> int:
     ap.add_argument("--crossover", action="store_true",
                     help="only time the drop-in against the CPU kernel for k*n = 2^10 .. 2^24 (m = 1), "
                          "the measurement behind DMC_HIP_MIN_MACS")
+    ap.add_argument("--skinny", action="store_true",
+                    help="only C2's shapes at skinny and prefill M, each launch one host call (no HIP "
+                         "graph): the workload of the counter profiles of the MFMA kernels")
     a = ap.parse_args(argv)
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -200,6 +203,9 @@ def main(argv=None) -> int:
     log(f"device {d.device_info()}")
     if a.crossover:
         print(json.dumps(crossover(d)), flush=True)
+        return 0
+    if a.skinny:
+        print(json.dumps(skinny(d, W, a.steps)), flush=True)
         return 0
 
     t = time.perf_counter()
@@ -378,7 +384,7 @@ def extended(d, W, reps: int) -> dict:
     # C2's shapes at a few activation rows (MFMA kernels)
     for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
         n, k = w.shape
-        for m in (2, 4, 8):
+        for m in (2, 4, 8, 16):
             x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
             s = Rotating(d, w, x, 5, n_out=n)
             f = lambda i: d.gemv_rd(s.x, s.w[i % 5], s.y, m, k, n)  # noqa: E731
@@ -493,6 +499,29 @@ def dropin(d, W, reps: int) -> dict:
         log(f"{label}: {us:.2f} us/call  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%} (PCIe-inclusive)")
         assert np.all(np.isfinite(y)), label
     d.release_weights()
+    return out
+
+
+def skinny(d, W, reps: int) -> dict:
+    """C2's shapes at m = 2 .. 16 (the skinny-M MFMA kernels) and 64 / 512
+    (prefill, the gemm layout), `reps` launches each, one host call per
+    launch: no HIP graph, so counter collection sees ordinary dispatches."""
+    out = {}
+    c2 = W.c2()
+    for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
+        n, k = w.shape
+        for m in (2, 4, 8, 12, 16, 64, 512):
+            x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+            s = Rotating(d, w, x, 3, n_out=n)
+            f = lambda i: d.gemv_rd(s.x, s.w[i % 3], s.y, m, k, n)  # noqa: E731
+            f(0)
+            us = batch_us(d, f, reps, graph=False)
+            p = d.plan("rd", m, k, n, x_addr=s.x.addr, w_addr=s.w[0].addr)
+            out[f"C2 rd {name} m={m}"] = {"us": round(us, 3), "GB/s": round(b_alg(n, k, m) / (us * 1e-6) / 1e9, 1),
+                                          "TFLOP/s": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
+                                          "layout": {-6: "wide", -7: "rows16", -8: "gemm"}.get(p.slices, "stream")}
+            log(f"C2 rd {name} m={m}: {us:.2f} us ({out[f'C2 rd {name} m={m}']['layout']})")
+            s.free()
     return out
 
 
