@@ -188,6 +188,8 @@ def main(argv=None) -> int:
     ap.add_argument("--skinny", action="store_true",
                     help="only C2's shapes at skinny and prefill M, each launch one host call (no HIP "
                          "graph): the workload of the counter profiles of the MFMA kernels")
+    ap.add_argument("--f32", action="store_true",
+                    help="only the f32-weight `W @ x` lines (row-dot f32 kernel and drop-in) at C2's shapes")
     a = ap.parse_args(argv)
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -209,6 +211,9 @@ def main(argv=None) -> int:
         return 0
     if a.skinny:
         print(json.dumps(skinny(d, W, a.steps)), flush=True)
+        return 0
+    if a.f32:
+        print(json.dumps(f32_weights(d, a.steps)), flush=True)
         return 0
 
     t = time.perf_counter()
@@ -360,6 +365,7 @@ def extended(d, W, reps: int) -> dict:
             f(i)
         record(label, batch_us(d, f, reps), n, k)
         s.free()
+    out.update(f32_weights(d, reps))
     # C4 LM head, skinny M: one resident copy (1.05 GB exceeds the 256 MB cache)
     t = time.perf_counter()
     w, _ = W.dense(W.LM_HEAD[0], W.LM_HEAD[1], seed=0, m=1)
@@ -416,6 +422,39 @@ def extended(d, W, reps: int) -> dict:
             s.free()
     out.update(helpers(d, c2["up"][0]))
     out.update(ingress(d, c2["down"][0]))
+    return out
+
+
+def f32_weights(d, reps: int) -> dict:
+    """The f32 path of `W @ x` (jit.rs:20806-20831) at C2's shapes with f32
+    weights (235 MB each): the row-dot f32 kernel on device pointers (bytes
+    4NK + 4K + 4N), and the drop-in dmc_matmul_f32_gpu with host x and y."""
+    out = {}
+    rng = np.random.default_rng(32)
+    for n, k in ((14336, 4096), (4096, 14336)):
+        w = np.float32(0.02) * rng.standard_normal((n, k), dtype=np.float32)
+        x = rng.standard_normal(k, dtype=np.float32)
+        copies = 6
+        s = Rotating(d, w, x, copies, n_out=n)
+        f = lambda i: d.gemv_f32_rd(s.x, s.w[i % copies], s.y, 1, k, n)  # noqa: E731
+        for i in range(3):
+            f(i)
+        us = batch_us(d, f, reps)
+        gbs = (4 * n * k + 4 * k + 4 * n) / (us * 1e-6) / 1e9
+        label = f"f32 rd W@x W[{n},{k}]"
+        out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
+        s.free()
+        d.matmul_f32_gpu(w, x)  # first touch: the weight becomes resident
+        calls = 100
+        t = time.perf_counter()
+        for _ in range(calls):
+            d.matmul_f32_gpu(w, x)
+        us = (time.perf_counter() - t) / calls * 1e6
+        label = f"f32 drop-in W@x W[{n},{k}] host x/y"
+        out[label] = {"us": round(us, 3)}
+        log(f"{label}: {us:.2f} us/call (PCIe-inclusive)")
+    d.release_weights()
     return out
 
 

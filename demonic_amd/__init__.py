@@ -95,6 +95,39 @@ def matmul_bf16_gpu_t(x: np.ndarray, w_nk: np.ndarray) -> np.ndarray:
     return out
 
 
+def _f32_operands(l: np.ndarray, r: np.ndarray):
+    l = _arr(l, np.float32, "l")
+    r = _arr(r, np.float32, "r")
+    m, k = _dims2(l)
+    if r.ndim == 1:
+        r = r.reshape(-1, 1)
+    if r.ndim != 2 or r.shape[0] != k:
+        raise ValueError(f"shape mismatch: l {l.shape} @ r {r.shape}")
+    return l, r, m, k, r.shape[1]
+
+
+def matmul_f32_gpu(l: np.ndarray, r: np.ndarray) -> np.ndarray:
+    """out[m,n] = l[m,k] @ r[k,n], all f32 -- dmc_matmul_f32_gpu, the device
+    route of the reference's f32 `@` (jit.rs:20806-20831) on GEMV shapes."""
+    l, r, m, k, n = _f32_operands(l, r)
+    out = np.empty((m, n), np.float32)
+    _lib.load().dmc_matmul_f32_gpu(_ptr(l), _ptr(r), _ptr(out), m, k, n)
+    return out
+
+
+def matmul_f32_gpu_try(l: np.ndarray, r: np.ndarray) -> tuple[int, np.ndarray]:
+    """dmc_matmul_f32_gpu_try: (return code, out); out is untouched (zeros) on failure."""
+    l, r, m, k, n = _f32_operands(l, r)
+    out = np.zeros((m, n), np.float32)
+    rc = _lib.load().dmc_matmul_f32_gpu_try(_ptr(l), _ptr(r), _ptr(out), m, k, n)
+    return int(rc), out
+
+
+def f32_selected(hip_on: bool, deterministic_depth: int, m: int, k: int, n: int) -> bool:
+    """Route predicate of the f32 device route (dmc_hip_f32_selected)."""
+    return bool(_lib.load().dmc_hip_f32_selected(int(hip_on), deterministic_depth, m, k, n))
+
+
 def _check_batched(x, w, out, m, k, n, batch, ls, rs):
     x = _arr(x, np.float32, "x")
     w = _arr(w, np.uint16, "w")
@@ -205,6 +238,11 @@ def gemv_cs(x, w, y, m: int, k: int, n: int, batch: int = 1, ls: int = 0, rs: in
 def gemv_rd(x, w, y, m: int, k: int, n: int) -> None:
     """Enqueue y = x @ bf16(w)' on device regions (w [n,k], the row-dot layout)."""
     _lib.check(_lib.load().dmc_hip_gemv_rd(_addr(x), _addr(w), _addr(y), m, k, n))
+
+
+def gemv_f32_rd(x, w, y, m: int, k: int, n: int) -> None:
+    """Enqueue y = x @ w' on device regions, f32 weights (w [n,k])."""
+    _lib.check(_lib.load().dmc_hip_gemv_f32_rd(_addr(x), _addr(w), _addr(y), m, k, n))
 
 
 def gemv_rd_grouped(xs, ws, ys, ns, m: int, k: int) -> None:
@@ -370,6 +408,24 @@ def plan(layout: str, m: int, k: int, n: int, batch: int = 1, rs: int = 0,
     out = (ctypes.c_int64 * 8)()
     _lib.check(_lib.load().dmc_hip_plan(int(layout == "rd"), x_addr, w_addr, m, k, n, batch, rs, out))
     return Plan(*[int(v) for v in out])
+
+
+@dataclass
+class PlanF32:
+    kvec: int              # 4-element k vectors per lane (0 = general kernel)
+    rows: int              # weight rows per register buffer
+    mt: int                # activation rows per workgroup
+    grid_x: int
+    grid_y: int
+    waves: int
+    rows_per_group: int    # weight rows per workgroup
+
+
+def plan_f32(m: int, k: int, n: int, x_addr: int = 0, w_addr: int = 0) -> PlanF32:
+    """Launch plan of the f32 row-dot GEMV (pure host computation)."""
+    out = (ctypes.c_int64 * 8)()
+    _lib.check(_lib.load().dmc_hip_plan_f32(x_addr, w_addr, m, k, n, out))
+    return PlanF32(*[int(v) for v in out[:7]])
 
 
 def register_weight(w: np.ndarray) -> int:

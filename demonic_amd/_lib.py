@@ -27,6 +27,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dmc_matmul_bf16_gpu_batched_try": (i32, [i64] * 9),
     "dmc_matmul_bf16_gpu_batched_deferred_try": (i32, [i64] * 9),
     "dmc_matmul_bf16_gpu_flush_try": (i32, []),
+    "dmc_matmul_f32_gpu": (None, [i64] * 6),
+    "dmc_matmul_f32_gpu_try": (i32, [i64] * 6),
+    "dmc_hip_f32_selected": (i32, [i32, i32, i64, i64, i64]),
+    "dmc_hip_gemv_f32_rd": (i32, [i64] * 6),
+    "dmc_hip_plan_f32": (i32, [i64, i64, i64, i64, i64, ctypes.POINTER(i64)]),
     "dmc_hip_available": (i32, []),
     "dmc_hip_gemv_selected": (i32, [i32, i32, i64, i64, i64]),
     "dmc_hip_last_error": (cstr, []),

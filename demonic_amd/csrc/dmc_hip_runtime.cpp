@@ -349,13 +349,14 @@ int residency_rc(int rc, int64_t bytes) {
 // With t_rows > 0 the host bytes hold W [t_rows, t_cols] and the device copy
 // is W^T [t_cols, t_rows]: the drop-in x @ W keeps its weight in the row-dot
 // layout, whose kernel needs one launch where the column-stream layout needs
-// two.  The layout and the column count are part of the key, so the same
-// bytes used through another entry or shape get their own copy.  `pin`:
+// two.  `elem` is the element size (2: bf16, 4: f32) the transpose moves.
+// The layout, the column count and the element size are part of the key, so
+// the same bytes used through another entry or shape get their own copy.  `pin`:
 // the caller keeps the device address (dmc_hip_register_weight), so no
 // eviction may free this entry (residency.h).  DMC_HIP_RESIDENT_CAP (bytes)
 // caps what may stay resident.
 int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, int64_t t_cols = 0,
-             bool pin = false) {
+             bool pin = false, int elem = 2) {
     Ctx &c = ctx();
     if (bytes <= 0) {
         *dev = c.dummy;
@@ -363,7 +364,9 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     }
     auto t0 = std::chrono::steady_clock::now();
     Key key = content_key(host, bytes);
-    if (t_rows > 0) key.b = mix64(key.b ^ 0x7472616e73706f73ULL ^ ((uint64_t)t_cols * 0x9E3779B97F4A7C15ULL));
+    if (t_rows > 0)
+        key.b = mix64(key.b ^ 0x7472616e73706f73ULL ^ ((uint64_t)t_cols * 0x9E3779B97F4A7C15ULL) ^
+                      (elem == 4 ? 0x6633320000000000ULL : 0));
     auto t1 = std::chrono::steady_clock::now();
     c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
     if (void *hit = c.weights->find(key, pin)) {
@@ -381,8 +384,10 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     }
     hipError_t e = hipMemcpyAsync(raw ? raw : d, host, (size_t)bytes, hipMemcpyHostToDevice, c.stream);
     if (e == hipSuccess && raw)
-        e = dmc::launch_transpose_bf16(static_cast<const uint16_t *>(raw), static_cast<uint16_t *>(d), t_rows,
-                                       t_cols, c.stream);
+        e = elem == 4 ? dmc::launch_transpose_f32(static_cast<const float *>(raw), static_cast<float *>(d), t_rows,
+                                                  t_cols, c.stream)
+                      : dmc::launch_transpose_bf16(static_cast<const uint16_t *>(raw), static_cast<uint16_t *>(d),
+                                                   t_rows, t_cols, c.stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
     if (raw) (void)hipFree(raw);
     if (e != hipSuccess) {
@@ -599,6 +604,92 @@ int run_host_locked(bool rd, int64_t l, int64_t r, int64_t out, int64_t m, int64
 void run_host_or_die(const char *entry, bool rd, int64_t l, int64_t r, int64_t out, int64_t m,
                      int64_t k, int64_t n, int64_t batch, int64_t ls, int64_t rs, bool defer) {
     if (run_host_locked(rd, l, r, out, m, k, n, batch, ls, rs, defer)) fatal(entry);
+}
+
+// ---- the f32 path of `@` (jit.rs:20806-20831) -----------------------------------
+//
+// out[m,n] = l[m,k] @ r[k,n], all f32: the reference's scalar_matmul /
+// simd_matmul / dmc_matmul_par chain (jit.rs:20715-20802, jit.rs:29415-29466)
+// on the row-dot f32 kernels, for the two GEMV shapes:
+//   W @ x (n <= kF32MaxAct activation columns): l [m,k] is the weight, its
+//     rows the output rows; r's n columns are the activation rows, gathered
+//     into the pinned staging;
+//   x @ W (m <= kF32MaxAct activation rows): r [k,n] is the weight, kept
+//     resident as its transpose [n,k] (one transpose at first use).
+// Other shapes are GEMMs this route does not take (dmc_hip_f32_selected says
+// so up front).  As for bf16, x and y pass through pinned staging and the
+// weight stays resident, keyed by content.
+constexpr int64_t kF32MaxAct = 16;
+
+bool f32_weight_left(int64_t m, int64_t n) { return n <= kF32MaxAct && (n <= m || m > kF32MaxAct); }
+
+int run_host_f32(const float *l, const float *r, float *out, int64_t m, int64_t k, int64_t n) {
+    if (m < 0 || k < 0 || n < 0)
+        return fail(DMC_HIP_EINVAL, "negative size (m=%lld k=%lld n=%lld)", (long long)m, (long long)k, (long long)n);
+    if (m == 0 || n == 0) return DMC_HIP_OK;  // jit.rs:29419
+    if (!valid_dims(m, k, n)) return fail(DMC_HIP_EINVAL, "dimension beyond int32");
+    if (!out || (k > 0 && (!l || !r))) return fail(DMC_HIP_EINVAL, "null pointer");
+    const bool w_left = f32_weight_left(m, n);
+    if (!w_left && m > kF32MaxAct)
+        return fail(DMC_HIP_EINVAL,
+                    "f32 route: GEMV shapes only (m <= %lld or n <= %lld activation rows), got m=%lld n=%lld",
+                    (long long)kF32MaxAct, (long long)kF32MaxAct, (long long)m, (long long)n);
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    // Deferred bf16 calls are materialized first, so their outputs and this
+    // call's staging never meet.
+    if (!c.pending.empty() && (rc = flush_locked())) return rc;
+    auto t0 = std::chrono::steady_clock::now();
+    const int64_t acts = w_left ? n : m, rows = w_left ? m : n;
+    const size_t x_bytes = (size_t)(acts * k) * 4, w_bytes = (size_t)(rows * k) * 4;
+    const size_t y_bytes = (size_t)(m * n) * 4;
+    char *hx = nullptr, *hx_dev = nullptr, *hy = nullptr, *hy_dev = nullptr;
+    if ((rc = stage(c.hx, c.hx_off, x_bytes ? x_bytes : 4, hipHostMallocDefault, &hx, &hx_dev))) return rc;
+    if ((rc = stage(c.hy, c.hy_off, y_bytes, hipHostMallocCoherent, &hy, &hy_dev))) return rc;
+    float *const hxf = reinterpret_cast<float *>(hx);
+    if (w_left && n > 1) {
+        for (int64_t kk = 0; kk < k; ++kk)
+            for (int64_t j = 0; j < n; ++j) hxf[j * k + kk] = r[kk * n + j];
+    } else if (x_bytes) {
+        memcpy(hx, w_left ? r : l, x_bytes);
+    }
+    const bool y_direct = y_bytes <= c.y_direct_max;
+    const bool x_direct = x_bytes <= c.x_direct_max;
+    if (!x_direct && (rc = ensure_dev(c.dx, x_bytes))) return rc;
+    if (!y_direct && (rc = ensure_dev(c.dy, y_bytes))) return rc;
+    float *const ydst = static_cast<float *>(y_direct ? static_cast<void *>(hy_dev) : c.dy.p);
+    const float *const xsrc = static_cast<const float *>(x_direct ? static_cast<void *>(hx_dev) : c.dx.p);
+    if (!x_direct) HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
+    c.st.stage_ns += ns_since(t0);
+    void *dw = nullptr;
+    if ((rc = w_left ? resident(l, (int64_t)w_bytes, &dw) : resident(r, (int64_t)w_bytes, &dw, k, n, false, 4)))
+        return rc;
+    auto t1 = std::chrono::steady_clock::now();
+    // Output (activation a, weight row i) is out[i][a] for W @ x, out[a][i] for x @ W.
+    const dmc::F32Problem p{static_cast<const float *>(dw), k, xsrc, k, ydst,
+                            w_left ? 1 : n, w_left ? n : 1, acts, k, rows};
+    const dmc::F32Plan pl = dmc::plan_f32(p, c.cus);
+    hipError_t e = dmc::launch_f32(p, pl, c.stream);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    if (!y_direct) HIP_TRY(hipMemcpyAsync(hy, c.dy.p, y_bytes, hipMemcpyDeviceToHost, c.stream), "y readback");
+    c.st.enqueue_ns += ns_since(t1);
+    c.st.calls++;
+    auto t2 = std::chrono::steady_clock::now();
+    HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
+    c.st.wait_ns += (uint64_t)ns_since(t2);
+    auto t3 = std::chrono::steady_clock::now();
+    memcpy(out, hy, y_bytes);
+    c.hx_off = 0;
+    c.hy_off = 0;
+    c.st.readback_ns += ns_since(t3);
+    return DMC_HIP_OK;
+}
+
+int run_host_f32_locked(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    return run_host_f32(reinterpret_cast<const float *>(l), reinterpret_cast<const float *>(r),
+                        reinterpret_cast<float *>(out), m, k, n);
 }
 
 
@@ -834,6 +925,10 @@ void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t
     run_host_or_die("dmc_matmul_bf16_gpu_t", true, l, r, out, m, k, n, 1, 0, 0, false);
 }
 
+void dmc_matmul_f32_gpu(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    if (run_host_f32_locked(l, r, out, m, k, n)) fatal("dmc_matmul_f32_gpu");
+}
+
 // ---- error-returning forms of the drop-in entries ------------------------------
 //
 // Same arguments and results; a failure returns DMC_HIP_E* (message in
@@ -865,6 +960,10 @@ int32_t dmc_matmul_bf16_gpu_flush_try(void) {
     return flush_locked();
 }
 
+int32_t dmc_matmul_f32_gpu_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n) {
+    return run_host_f32_locked(l, r, out, m, k, n);
+}
+
 // ---- additions ----------------------------------------------------------------
 
 int32_t dmc_hip_available(void) {
@@ -876,6 +975,13 @@ int32_t dmc_hip_gemv_selected(int32_t hip_on, int32_t deterministic_depth, int64
                               int64_t n) {
     if (!hip_on || deterministic_depth != 0) return 0;
     if (m <= 0 || k <= 0 || n <= 0) return 0;
+    const __int128 macs = (__int128)m * k * n;
+    return macs >= (__int128)DMC_HIP_MIN_MACS ? 1 : 0;
+}
+
+int32_t dmc_hip_f32_selected(int32_t hip_on, int32_t deterministic_depth, int64_t m, int64_t k, int64_t n) {
+    if (!hip_on || deterministic_depth != 0) return 0;
+    if (m <= 0 || k <= 0 || n <= 0 || (m > kF32MaxAct && n > kF32MaxAct)) return 0;
     const __int128 macs = (__int128)m * k * n;
     return macs >= (__int128)DMC_HIP_MIN_MACS ? 1 : 0;
 }
@@ -1032,6 +1138,21 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
     const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
     if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
     hipError_t e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_gemv_f32_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!valid_dims(m, k, n)) return fail(DMC_HIP_EINVAL, "bad GEMV shape");
+    if (m == 0 || n == 0) return DMC_HIP_OK;
+    if (!y_dev || (k > 0 && (!x_dev || !w_dev))) return fail(DMC_HIP_EINVAL, "null pointer");
+    int rc = ensure_init();
+    if (rc) return rc;
+    Ctx &c = ctx();
+    const dmc::F32Problem p{reinterpret_cast<const float *>(w_dev), k, reinterpret_cast<const float *>(x_dev), k,
+                            reinterpret_cast<float *>(y_dev), n, 1, m, k, n};
+    hipError_t e = dmc::launch_f32(p, dmc::plan_f32(p, c.cus), c.stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DMC_HIP_OK;
 }
@@ -1196,6 +1317,21 @@ int32_t dmc_hip_synchronize(void) {
     int rc = ensure_init();
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
+    return DMC_HIP_OK;
+}
+
+int32_t dmc_hip_plan_f32(int64_t x_addr, int64_t w_addr, int64_t m, int64_t k, int64_t n, int64_t *out8) {
+    if (!out8 || !valid_dims(m, k, n)) return fail(DMC_HIP_EINVAL, "bad plan query");
+    int cus;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        cus = ctx().ok ? ctx().cus : 256;
+    }
+    const dmc::F32Problem p{reinterpret_cast<const float *>(w_addr), k, reinterpret_cast<const float *>(x_addr),
+                            k, nullptr, n, 1, m, k, n};
+    const dmc::F32Plan pl = dmc::plan_f32(p, cus);
+    const int64_t v[8] = {pl.kvec, pl.rows, pl.mt, pl.grid_x, pl.grid_y, pl.waves, pl.rpw, 0};
+    memcpy(out8, v, sizeof v);
     return DMC_HIP_OK;
 }
 

@@ -2297,6 +2297,238 @@ transpose_bf16_v8_kernel(const uint16_t *__restrict__ src, uint16_t *__restrict_
     }
 }
 
+// ---- f32 weights, row-dot: the f32 path of `W @ x` -----------------------------
+//
+// The reference's f32 `@` keeps the bf16 kernels' closed form with the weight
+// read as f32: per output, acc = +0, then acc = fma(l[i][k], r[k][j], acc)
+// over ascending k (scalar_matmul, jit.rs:20715-20802, which an f32 `W @ x`
+// takes, jit.rs:20806-20831; dmc_matmul_par's matmul_tile, jit.rs:29448-29466,
+// bit-identical by jit.rs:29404-29408).  Here W [N,K] f32 is the weight (rows
+// are output rows) and X [M,K] the activation rows, as in the bf16 row-dot
+// kernels; the caller orients its [m, n] result through the output strides:
+// output (activation row a, weight row n) goes to Y[a * ys_act + n * ys_row].
+
+// The reference chain of one f32 output (the zero rule's rare path).
+__device__ float chain_f32(const float *__restrict__ w, const float *__restrict__ x, int K) {
+    float acc = 0.0f;
+    for (int k = 0; k < K; ++k) acc = fmaf(x[k], w[k], acc);
+    return acc;
+}
+
+__device__ __forceinline__ float zero_unfold_f32(float v, bool live, const float *x, const float *w, int K) {
+    if (live && v == 0.0f) v = __builtin_signbit(v) ? 0.0f : chain_f32(w, x, K);
+    return v;
+}
+
+// Streaming: gemv_rd_stream_kernel's layout with four f32 weights per 16-byte
+// load.  Lane `lane` of wave `wave` owns the KV vectors of 4 elements starting
+// at ((j*NW + wave)*64 + lane)*4, so for every j the workgroup reads NW KiB of
+// a row contiguously; x's slice stays in registers; the workgroup walks weight
+// rows [rb, rb + rpw) ROWS at a time through two register buffers (the next
+// rows in flight while the current ones are summed), every load
+// unconditional (past K or past the last row: offsets beyond the buffer
+// resource, which read zeros).  Rows 16-byte aligned (K % 4 == 0).  Zero rule:
+// the FMA kernels' fold (zero_fold), x's nonzero mask per element.
+template <int NW, int KV, int ROWS, int MT>
+__global__ void __launch_bounds__(64 * NW)
+gemv_rd_f32_stream_kernel(const float *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                          int K, int M, int rpw, int64_t ys_act, int64_t ys_row) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = (int)blockIdx.x * rpw;
+    const int nr = min(N, rb + rpw) - rb;
+    const int m0 = blockIdx.y * MT;
+    const int mrows = min(MT, M - m0);
+
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m0 * K, (uint32_t)mrows * (uint32_t)K * 4);
+    uint32_t eoff[KV];
+    bool has[KV];
+    u32x4 xv[MT][KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int e = ((j * NW + wave) * 64 + lane) * 4;
+        has[j] = e < K;
+        eoff[j] = has[j] ? (uint32_t)e * 4 : kOutOfRange;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const uint32_t xo = has[j] ? ((uint32_t)min(m, mrows - 1) * (uint32_t)K + (uint32_t)e) * 4 : kOutOfRange;
+            xv[m][j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+        }
+    }
+    // +0 for a lane that owns elements (the chain's start), -0 (the additive
+    // identity) for one that owns none.
+    const float init = (wave * 64 + lane) * 4 < K ? 0.0f : -0.0f;
+
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * K, (uint32_t)((int64_t)nr * K * 4));
+    const uint32_t row_bytes = (uint32_t)K * 4;
+    __shared__ float red[NW][MT][kMaxRpw];
+
+    u32x4 ba[ROWS][KV], bb[ROWS][KV];
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const uint32_t base = (uint32_t)(i0 + q) * row_bytes;
+#pragma unroll
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], base);
+        }
+    };
+    load(ba, 0);
+    float xr[MT][KV][4];
+    uint32_t xm[MT][KV][4];
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
+        float acc[MT][ROWS];
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) acc[m][q] = init;
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int q = 0; q < ROWS; ++q) {
+                    const float w = __uint_as_float(wv[q][j][e]);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
+                }
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                uint32_t nz = 0;
+#pragma unroll
+                for (int j = 0; j < KV; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) nz |= wv[q][j][e] & xm[m][j][e];
+                const float s = wave_sum_dpp(zero_fold(acc[m][q], nz != 0));
+                if (lane == 0 && i0 + q < nr) red[wave][m][i0 + q] = s;
+            }
+    };
+    load(bb, ROWS);
+    __builtin_amdgcn_sched_barrier(0);  // x's wait below comes after every load above
+    // A vector past K reads +0 weights; its x becomes -0, so each of its
+    // products is -0, the exact additive identity.
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t b = xv[m][j][e] | (has[j] ? 0u : 0x80000000u);
+                xr[m][j][e] = __uint_as_float(b);
+                xm[m][j][e] = (b & 0x7fffffffu) != 0 ? 0x7fffffffu : 0u;
+            }
+    sum_rows(ba, 0);
+    for (int i0 = 0; i0 + ROWS < nr; i0 += 2 * ROWS) {
+        load(ba, i0 + 2 * ROWS);
+        sum_rows(bb, i0 + ROWS);
+        if (i0 + 2 * ROWS >= nr) break;
+        load(bb, i0 + 3 * ROWS);
+        sum_rows(ba, i0 + 2 * ROWS);
+    }
+    __syncthreads();
+    for (int t0 = wave * 64; t0 < mrows * nr; t0 += 64 * NW) {
+        const int t = t0 + lane;
+        const bool live = t < mrows * nr;
+        const int m = live ? t / nr : 0, r = live ? t - m * nr : 0;
+        float s = red[0][m][r];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w][m][r];
+        s = zero_unfold_f32(s, live, X + (int64_t)(m0 + m) * K, W + (int64_t)(rb + r) * K, K);
+        if (live) Y[(int64_t)(m0 + m) * ys_act + (int64_t)(rb + r) * ys_row] = s;
+    }
+}
+
+// General: any K (0 included), 4-byte alignment, row strides ldw and ldx.
+// Four waves, one weight row each; lane `lane` takes k = lane + 64 i, four
+// loads in flight; MT activation rows per workgroup (x from the caches).
+template <int MT>
+__global__ void __launch_bounds__(256)
+gemv_rd_f32_kernel(const float *__restrict__ W, int64_t ldw, const float *__restrict__ X, int64_t ldx,
+                   float *__restrict__ Y, int N, int K, int M, int64_t ys_act, int64_t ys_row) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = (int)blockIdx.x * 4 + wave;
+    const int m0 = blockIdx.y * MT;
+    const int mrows = min(MT, M - m0);
+    if (n >= N) return;  // wave-uniform; no barrier follows
+    const float *__restrict__ w = W + (int64_t)n * ldw;
+    const float *__restrict__ x = X + (int64_t)m0 * ldx;
+    const float init = lane < K ? 0.0f : -0.0f;
+    float acc[MT];
+    uint32_t nz[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        acc[m] = init;
+        nz[m] = 0;
+    }
+    for (int k0 = 0; k0 < K; k0 += 256) {
+        float wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + 64 * u + lane;
+            wv[u] = k < K ? w[k] : 0.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m < mrows) {  // wave-uniform
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int k = k0 + 64 * u + lane;
+                    if (k < K) {
+                        const float xk = x[(int64_t)m * ldx + k];
+                        acc[m] = fmaf(xk, wv[u], acc[m]);
+                        nz[m] |= (__float_as_uint(xk) & 0x7fffffffu) != 0 &&
+                                         (__float_as_uint(wv[u]) & 0x7fffffffu) != 0
+                                     ? 1u
+                                     : 0u;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m < mrows) {
+            float s = wave_sum_dpp(zero_fold(acc[m], nz[m] != 0));
+            if (lane == 0) {
+                s = zero_unfold_f32(s, true, x + (int64_t)m * ldx, w, K);
+                Y[(int64_t)(m0 + m) * ys_act + (int64_t)n * ys_row] = s;
+            }
+        }
+    }
+}
+
+// dst [cols, rows] = src [rows, cols]^T for 4-byte elements (the resident
+// transposed copy of an f32 `x @ W` weight): 64 x 64 tiles through LDS, one
+// padded column per tile row so the transposed reads spread over the banks.
+constexpr int kTileF = 64;
+
+__global__ void __launch_bounds__(256)
+transpose_f32_kernel(const float *__restrict__ src, float *__restrict__ dst, int64_t rows, int64_t cols,
+                     int64_t tiles_c, int64_t ntiles) {
+    __shared__ float tile[kTileF][kTileF + 1];
+    const int t = threadIdx.x;
+    const int lc = t & 63, lr0 = t >> 6;
+    for (int64_t tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
+        const int64_t r0 = (tl / tiles_c) * kTileF, c0 = (tl % tiles_c) * kTileF;
+#pragma unroll
+        for (int i = 0; i < kTileF / 4; ++i) {
+            const int lr = lr0 + 4 * i;
+            const int64_t r = r0 + lr, c = c0 + lc;
+            tile[lr][lc] = r < rows && c < cols ? src[r * cols + c] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kTileF / 4; ++i) {
+            const int lr = lr0 + 4 * i;
+            const int64_t dr = c0 + lr, dc = r0 + lc;
+            if (dr < cols && dc < rows) dst[dr * rows + dc] = tile[lc][lr];
+        }
+        __syncthreads();
+    }
+}
+
 // IEEE binary16 bits (in the low 16 bits of h) to binary32 bits, exactly, by
 // integer steps: the f16_bits_to_f32 of compiler/src/jit.rs:29231-29257
 // (subnormals normalized, NaN payloads and the signalling bit kept, which a
@@ -3099,6 +3331,133 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
         return hipGetLastError();
     }
     return hipSuccess;
+}
+
+// ---- f32 weights, row-dot ------------------------------------------------------
+
+F32Plan plan_f32(const F32Problem &p, int num_cus) {
+    F32Plan pl{};
+    const int64_t cus = num_cus > 0 ? num_cus : 256;
+    // Streaming: 16-byte rows, x rows alike, K within 8 vectors of 4 per lane
+    // over 8 waves.  Waves as for bf16 by bytes per row (1 KiB per wave per
+    // vector); activation rows per workgroup within the register budget; rows
+    // per workgroup as for bf16 rows of the same byte length (4, 8 for long
+    // rows), fewer while that leaves under 4 (2 for long rows) workgroups per CU.
+    if (p.k >= 4 && p.k % 4 == 0 && p.k <= 16384 && p.ldw == p.k && p.ldx == p.k && aligned(p.w, 16) &&
+        aligned(p.x, 16) && env_int("DMC_HIP_F32_STREAM", 1) != 0) {
+        const int nw = p.k <= 256 ? 1 : p.k <= 512 ? 2 : p.k <= 1024 ? 4 : 8;
+        const int kv = (int)((p.k + nw * 256 - 1) / (nw * 256));
+        const int mt = std::min(p.m <= 1 ? 1 : p.m <= 2 ? 2 : 4, kv <= 2 ? 4 : kv <= 4 ? 2 : 1);
+        const int rows = kv <= 2 ? 2 : 1;
+        const int64_t gy = (p.m + mt - 1) / mt;
+        int rpw = kv >= 3 ? 8 : 4;
+        const int64_t min_blocks = (kv >= 2 ? 2 : 4) * cus;
+        while (rpw > rows && (p.n + rpw - 1) / rpw * gy < min_blocks) rpw >>= 1;
+        rpw = std::max(rows, rpw / rows * rows);
+        const int64_t gx = (p.n + rpw - 1) / rpw;
+        if ((int64_t)(rpw + 4 * rows) * p.k * 4 <= INT32_MAX && gy <= 65535 && gx <= INT32_MAX) {
+            pl.waves = nw;
+            pl.kvec = kv;
+            pl.rows = rows;
+            pl.mt = mt;
+            pl.rpw = rpw;
+            pl.grid_x = gx;
+            pl.grid_y = gy;
+            return pl;
+        }
+    }
+    pl.mt = p.m <= 1 ? 1 : p.m <= 4 ? 4 : 16;
+    pl.waves = 4;
+    pl.kvec = 0;
+    pl.rows = 1;
+    pl.rpw = 4;
+    pl.grid_x = (p.n + 3) / 4;
+    pl.grid_y = (p.m + pl.mt - 1) / pl.mt;
+    return pl;
+}
+
+namespace {
+
+template <int NW, int KV, int ROWS, int MT>
+hipError_t f32s_go(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
+    static_assert((MT * KV <= 8 && ROWS * KV <= 8) || KV == 1, "register budget");
+    hipLaunchKernelGGL((gemv_rd_f32_stream_kernel<NW, KV, ROWS, MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.grid_y),
+                       dim3(64 * NW), 0, s, p.w, p.x, p.y, (int)p.n, (int)p.k, (int)p.m, pl.rpw, p.ys_act,
+                       p.ys_row);
+    return hipGetLastError();
+}
+
+template <int NW, int KV, int ROWS>
+hipError_t f32s_mt(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
+    switch (pl.mt) {
+    case 1: return f32s_go<NW, KV, ROWS, 1>(p, pl, s);
+    case 2:
+        if constexpr (KV <= 4) return f32s_go<NW, KV, ROWS, 2>(p, pl, s);
+        break;
+    case 4:
+        if constexpr (KV <= 2) return f32s_go<NW, KV, ROWS, 4>(p, pl, s);
+        break;
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int MT>
+hipError_t f32g_go(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
+    hipLaunchKernelGGL((gemv_rd_f32_kernel<MT>), dim3((unsigned)pl.grid_x, (unsigned)pl.grid_y), dim3(256), 0, s,
+                       p.w, p.ldw, p.x, p.ldx, p.y, (int)p.n, (int)p.k, (int)p.m, p.ys_act, p.ys_row);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_f32(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
+    if (p.m <= 0 || p.n <= 0) return hipSuccess;
+    if (p.k < 0 || p.m > INT32_MAX || p.n > INT32_MAX || p.k > INT32_MAX || pl.grid_x < 1 || pl.grid_y < 1 ||
+        pl.grid_y > 65535 || pl.grid_x > INT32_MAX || pl.grid_x * pl.rpw < p.n || pl.grid_y * pl.mt < p.m)
+        return hipErrorInvalidValue;
+    if (pl.kvec > 0) {
+        // The shapes the streaming kernel assumes (plan_f32's conditions).
+        if (p.k % 4 != 0 || p.ldw != p.k || p.ldx != p.k || !aligned(p.w, 16) || !aligned(p.x, 16) ||
+            (int64_t)pl.kvec * pl.waves * 256 < p.k || pl.rpw < pl.rows || pl.rpw > kMaxRpw ||
+            pl.rows != (pl.kvec <= 2 ? 2 : 1) || (int64_t)(pl.rpw + 4 * pl.rows) * p.k * 4 > INT32_MAX)
+            return hipErrorInvalidValue;
+        if (pl.waves == 8) {
+            switch (pl.kvec) {
+            case 1: return f32s_mt<8, 1, 2>(p, pl, s);
+            case 2: return f32s_mt<8, 2, 2>(p, pl, s);
+            case 3: return f32s_mt<8, 3, 1>(p, pl, s);
+            case 4: return f32s_mt<8, 4, 1>(p, pl, s);
+            case 5: return f32s_mt<8, 5, 1>(p, pl, s);
+            case 6: return f32s_mt<8, 6, 1>(p, pl, s);
+            case 7: return f32s_mt<8, 7, 1>(p, pl, s);
+            case 8: return f32s_mt<8, 8, 1>(p, pl, s);
+            }
+        } else if (pl.kvec == 1) {
+            switch (pl.waves) {
+            case 1: return f32s_mt<1, 1, 2>(p, pl, s);
+            case 2: return f32s_mt<2, 1, 2>(p, pl, s);
+            case 4: return f32s_mt<4, 1, 2>(p, pl, s);
+            }
+        }
+        return hipErrorInvalidValue;
+    }
+    if (pl.rpw != 4 || (p.k > 0 && (!aligned(p.w, 4) || !aligned(p.x, 4) || p.ldw < p.k || p.ldx < p.k)))
+        return hipErrorInvalidValue;
+    switch (pl.mt) {
+    case 1: return f32g_go<1>(p, pl, s);
+    case 4: return f32g_go<4>(p, pl, s);
+    case 16: return f32g_go<16>(p, pl, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_transpose_f32(const float *src, float *dst, int64_t rows, int64_t cols, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const int64_t tiles_c = (cols + kTileF - 1) / kTileF;
+    const int64_t ntiles = tiles_c * ((rows + kTileF - 1) / kTileF);
+    hipLaunchKernelGGL(transpose_f32_kernel, dim3(stride_grid(ntiles)), dim3(256), 0, s, src, dst, rows, cols, tiles_c,
+                       ntiles);
+    return hipGetLastError();
 }
 
 size_t probe_sink_bytes() { return (size_t)kProbeGroups * 4; }

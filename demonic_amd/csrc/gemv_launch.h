@@ -133,6 +133,31 @@ hipError_t launch_rd_group(const RdGroup &g, const RdPlan &plan, hipStream_t str
 
 hipError_t launch_cs(const CsProblem &p, const CsPlan &plan, void *workspace, hipStream_t stream);
 
+// f32 weights, row-dot (the f32 path of `W @ x`, jit.rs:20806-20831): output
+// (activation row a, weight row i) = sum_k x[a, k] * w[i, k], an f32 fma per
+// product from +0 as for bf16, stored at y[a * ys_act + i * ys_row] (the
+// drop-in writes either orientation of its [m, n] result).
+struct F32Problem {
+    const float *w;  // [n, ldw]
+    int64_t ldw;
+    const float *x;  // [m, ldx]
+    int64_t ldx;
+    float *y;
+    int64_t ys_act, ys_row;
+    int64_t m, k, n;
+};
+// Streaming (kvec > 0: 16-byte rows, k <= 16384; the bf16 streaming layout with
+// 4 weights per load) or general (kvec == 0: any k and 4-byte alignment, one
+// row per wave).
+struct F32Plan {
+    int waves, kvec, rows, mt, rpw;
+    int64_t grid_x, grid_y;
+};
+F32Plan plan_f32(const F32Problem &p, int num_cus);
+hipError_t launch_f32(const F32Problem &p, const F32Plan &plan, hipStream_t stream);
+// dst [cols, rows] = src [rows, cols]^T for 4-byte elements.
+hipError_t launch_transpose_f32(const float *src, float *dst, int64_t rows, int64_t cols, hipStream_t stream);
+
 // Measurement probe: a read-only nontemporal pass over [src, src+bytes) in
 // 16-byte granules (bytes == 0: an empty launch, the dispatch floor).  `sink`
 // holds probe_sink_bytes().

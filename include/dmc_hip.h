@@ -106,6 +106,41 @@ int32_t dmc_matmul_bf16_gpu_flush_try(void);
  * `W @ x` with x:[k,1] (m = 1).  Same error behaviour and synchronicity. */
 void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
 
+/* ---- f32 weights: the f32 path of `@` ------------------------------------ */
+
+/* Device route for the reference's f32 matmul on GEMV shapes, same ABI as
+ * dmc_matmul_par (jit.rs:29415): out[m,n] = l[m,k] @ r[k,n], all f32
+ * row-major, each output the ascending-k fma chain from +0 of scalar_matmul /
+ * simd_matmul / matmul_tile (jit.rs:20715-20802, jit.rs:29448-29466), up to
+ * summation order as for bf16 (normwise <= 1e-5, NaN/+-inf classes and zero
+ * signs kept).  It replaces the single-threaded scalar_matmul that an f32
+ * `W @ x` takes (emit_2d_matmul_at, jit.rs:20806-20831: W [m,k] @ x [k,1],
+ * n = 1).  Served shapes: n <= 16 (W @ x: l is the weight, kept resident by
+ * content) and m <= 16 (x @ W: r is the weight, kept resident as its
+ * transpose); any other shape is DMC_HIP_EINVAL (the void form aborts) --
+ * ask dmc_hip_f32_selected first.  m == 0 or n == 0 returns without touching
+ * out (jit.rs:29419); k == 0 writes +0.0.  Synchronous; pending deferred bf16
+ * calls are materialized first.  The _try form returns DMC_HIP_E* with out
+ * untouched instead of aborting. */
+void dmc_matmul_f32_gpu(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+int32_t dmc_matmul_f32_gpu_try(int64_t l, int64_t r, int64_t out, int64_t m, int64_t k, int64_t n);
+
+/* The route predicate for dmc_matmul_f32_gpu, shaped like
+ * dmc_hip_gemv_selected: opt-in flag on, outside `@deterministic`, a served
+ * shape (m <= 16 or n <= 16) and at least DMC_HIP_MIN_MACS multiply-adds.
+ * Pure function; touches no device. */
+int32_t dmc_hip_f32_selected(int32_t hip_on, int32_t deterministic_depth, int64_t m, int64_t k, int64_t n);
+
+/* Device-pointer f32 row-dot GEMV: y[m,n] = x[m,k] @ w[n,k]' (w f32, rows
+ * the output columns), enqueued on the library stream without waiting. */
+int32_t dmc_hip_gemv_f32_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, int64_t k, int64_t n);
+
+/* Launch plan of the f32 row-dot GEMV (w [n,k], x [m,k]) for tests and
+ * reports: out8 = {kvec (0: the general kernel; > 0: the streaming kernel's
+ * 4-element vectors per lane), rows per register buffer, activation rows per
+ * workgroup, grid_x, grid_y, waves, weight rows per workgroup, 0}. */
+int32_t dmc_hip_plan_f32(int64_t x_addr, int64_t w_addr, int64_t m, int64_t k, int64_t n, int64_t *out8);
+
 /* 1 when a gfx950 device is usable (initializing the context on first call),
  * 0 otherwise; DMC_HIP_DISABLE=1 in the environment forces 0.  The analogue
  * of blas_gemm_available() (jit.rs:29359). */

@@ -54,6 +54,8 @@ def load(variant: str = "port") -> ctypes.CDLL:
     lib.oracle_matmul_bf16_t.argtypes = [_P, _P, _P, _i64, _i64, _i64]
     lib.oracle_gemv_points.argtypes = [_P, _i64, _P, _i64, _i32, _i64, _P, _P, _i64, _P]
     lib.oracle_matmul_bf16_batched.argtypes = [_P, _P, _P, _i64, _i64, _i64, _i64, _i64]
+    lib.oracle_matmul_f32.argtypes = [_P, _P, _P, _i64, _i64, _i64]
+    lib.oracle_gemv_points_f32.argtypes = [_P, _i64, _P, _i64, _i64, _P, _P, _i64, _P]
     lib.oracle_matmul_threads.restype = _i32
     lib.oracle_matmul_threads.argtypes = [_i64, _i64, _i64]
     lib.oracle_gemv_ways.restype = _i32
@@ -143,6 +145,37 @@ def gemv_points(x, w, layout: str, mi, ni) -> np.ndarray:
         lay = 1
     out = np.empty(mi.shape, np.float32)
     load().oracle_gemv_points(_p(x), x.shape[1], _p(w), ldw, lay, k, _p(mi), _p(ni), mi.size, _p(out))
+    return out
+
+
+def matmul_f32(l, r) -> np.ndarray:
+    """Reference f32 `@` (dmc_matmul_par / scalar_matmul): l[m,k] @ r[k,n]."""
+    l = _c(l, np.float32)
+    if l.ndim == 1:
+        l = l[None, :]
+    r = _c(r, np.float32)
+    if r.ndim == 1:
+        r = r[:, None]
+    m, k = l.shape
+    k2, n = r.shape
+    assert k == k2, (l.shape, r.shape)
+    out = np.empty((m, n), np.float32)
+    load().oracle_matmul_f32(_p(l), _p(r), _p(out), m, k, n)
+    return out
+
+
+def gemv_points_f32(x, w_nk, mi, ni) -> np.ndarray:
+    """f32 closed form at outputs (mi[p], ni[p]) of x[m,k] @ w_nk[n,k]'."""
+    x = _c(x, np.float32)
+    if x.ndim == 1:
+        x = x[None, :]
+    w_nk = _c(w_nk, np.float32)
+    mi = _c(mi, np.int64)
+    ni = _c(ni, np.int64)
+    k = x.shape[1]
+    assert w_nk.shape[1] == k
+    out = np.empty(mi.shape, np.float32)
+    load().oracle_gemv_points_f32(_p(x), k, _p(w_nk), k, k, _p(mi), _p(ni), mi.size, _p(out))
     return out
 
 

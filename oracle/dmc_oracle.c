@@ -20,6 +20,10 @@
  *                           above (jit.rs:20916-20946)
  *   oracle_gemv_points      the same closed form evaluated for a subset of
  *                           outputs (sampled-row parity at full sizes)
+ *   oracle_matmul_f32       compiler/src/jit.rs:29415-29466  dmc_matmul_par / matmul_tile,
+ *                           = scalar_matmul / simd_matmul    jit.rs:20525-20802
+ *                           (the f32 `@`, jit.rs:20806-20831)
+ *   oracle_gemv_points_f32  that closed form for a subset of outputs, W [N,K]
  *
  * The numeric contract (docs/SPEC.md:1149-1163, docs/NUMERICS.md:28-33): each
  * output is acc = +0.0f; for k ascending: acc = fmaf(x[k], w(k), acc).  fmaf
@@ -308,6 +312,50 @@ ORACLE_API void oracle_gemv_points(const float *x, int64_t ldx, const uint16_t *
             int64_t kk = g_mutation == MUT_DESCENDING_K ? kend - 1 - t : t;
             uint16_t h = layout == 0 ? w[kk * ldw + n] : w[n * ldw + kk];
             acc = step(xr[kk], oracle_bf16_to_f32(h), acc);
+        }
+        out[p] = acc;
+    }
+}
+
+/* The reference's f32 matmul (dmc_matmul_par's matmul_tile, jit.rs:29448-
+ * 29466; bit-identical to the inline scalar_matmul and simd_matmul kernels,
+ * jit.rs:29404-29408 and jit.rs:20769-20775): out[m,n] = l[m,k] @ r[k,n], all
+ * f32 row-major; per output acc = +0.0f, then acc = fmaf(l[i][kk], r[kk][j],
+ * acc) for kk ascending -- matmul_tile's loop nest (row zeroed, kk outer, j
+ * inner).  m == 0 or n == 0 returns (jit.rs:29419); k == 0 leaves the zeros.
+ * Serial: the reference partitions output rows over threads
+ * (jit.rs:29421-29445), which changes no value. */
+ORACLE_API void oracle_matmul_f32(const float *l, const float *r, float *out, int64_t m, int64_t k, int64_t n) {
+    if (m <= 0 || n <= 0) return;
+    const float init = g_mutation == MUT_NEG_ZERO_INIT ? -0.0f : 0.0f;
+    const int64_t kend = g_mutation == MUT_DROP_LAST_K && k > 0 ? k - 1 : k;
+    for (int64_t i = 0; i < m; ++i) {
+        float *c = out + i * n;
+        for (int64_t j = 0; j < n; ++j) c[j] = init;
+        for (int64_t t = 0; t < kend; ++t) {
+            const int64_t kk = g_mutation == MUT_DESCENDING_K ? kend - 1 - t : t;
+            const float a = l[i * k + kk];
+            for (int64_t j = 0; j < n; ++j) {
+                const float b = g_mutation == MUT_TRANSPOSED_W ? r[j * k + kk] : r[kk * n + j];
+                c[j] = step(a, b, c[j]);
+            }
+        }
+    }
+}
+
+/* The f32 closed form at selected outputs, weight stored [N,K] (row-dot):
+ * out[p] = chain over k of x[mi[p]][k] * w[ni[p]][k], from +0, ascending. */
+ORACLE_API void oracle_gemv_points_f32(const float *x, int64_t ldx, const float *w, int64_t ldw, int64_t k,
+                                       const int64_t *mi, const int64_t *ni, int64_t npts, float *out) {
+    const float init = g_mutation == MUT_NEG_ZERO_INIT ? -0.0f : 0.0f;
+    const int64_t kend = g_mutation == MUT_DROP_LAST_K && k > 0 ? k - 1 : k;
+    for (int64_t p = 0; p < npts; ++p) {
+        const float *xr = x + mi[p] * ldx;
+        const float *wr = w + ni[p] * ldw;
+        float acc = init;
+        for (int64_t t = 0; t < kend; ++t) {
+            const int64_t kk = g_mutation == MUT_DESCENDING_K ? kend - 1 - t : t;
+            acc = step(xr[kk], wr[kk], acc);
         }
         out[p] = acc;
     }

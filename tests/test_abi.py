@@ -385,3 +385,64 @@ def test_package_has_no_cpu_gemv_and_never_imports_the_oracle():
     src += "\n".join(p.read_text() for p in (ROOT / "demonic_amd" / "csrc").glob("*"))
     assert "import oracle" not in src and "from oracle" not in src
     assert "fmaf(" not in (ROOT / "demonic_amd" / "csrc" / "dmc_hip_runtime.cpp").read_text()
+
+
+# ---- the f32 route (jit.rs:20806-20831) -----------------------------------------------------
+
+def test_f32_selection_predicate():
+    sel = d.f32_selected
+    assert sel(True, 0, 4096, 4096, 1), "W @ x refused"
+    assert sel(True, 0, 1, 4096, 4096), "x @ W refused"
+    assert sel(True, 0, 16, 4096, 4096) and sel(True, 0, 4096, 4096, 16)
+    assert not sel(True, 0, 17, 4096, 17), "a GEMM shape selected"
+    assert not sel(False, 0, 4096, 4096, 1) and not sel(True, 1, 4096, 4096, 1)
+    assert not sel(True, 0, 64, 128, 1), "small GEMV selected"
+    assert not sel(True, 0, 0, 4096, 1) and not sel(True, 0, 4096, 0, 1)
+
+
+@pytest.mark.parametrize("k,waves,kvec,rows", [(4, 1, 1, 2), (256, 1, 1, 2), (1000, 4, 1, 2), (2048, 8, 1, 2),
+                                               (4096, 8, 2, 2), (6144, 8, 3, 1), (14336, 8, 7, 1),
+                                               (16384, 8, 8, 1)])
+def test_f32_streaming_plan_covers_k(k, waves, kvec, rows):
+    p = d.plan_f32(1, k, 14336, x_addr=256, w_addr=256)
+    assert (p.waves, p.kvec, p.rows) == (waves, kvec, rows), p
+    assert kvec * waves * 256 >= k > (kvec - 1) * waves * 256 or kvec == 1
+    assert p.grid_x * p.rows_per_group >= 14336 and p.rows_per_group % p.rows == 0
+
+
+@pytest.mark.parametrize("k,x_addr,w_addr", [(4097, 256, 256), (4098, 256, 256), (16388, 256, 256),
+                                             (4096, 260, 256), (4096, 256, 264)])
+def test_f32_general_kernel_for_odd_k_misaligned_or_long_rows(k, x_addr, w_addr):
+    p = d.plan_f32(1, k, 14336, x_addr=x_addr, w_addr=w_addr)
+    assert p.kvec == 0 and p.waves == 4 and p.rows_per_group == 4 and p.grid_x == 14336 // 4, p
+
+
+def test_f32_activation_rows_per_workgroup():
+    assert d.plan_f32(4, 4096, 4096, x_addr=256, w_addr=256).mt == 4      # kvec 2: up to 4
+    assert d.plan_f32(16, 4096, 4096, x_addr=256, w_addr=256).grid_y == 4
+    assert d.plan_f32(4, 14336, 4096, x_addr=256, w_addr=256).mt == 1     # kvec 7: one
+    assert d.plan_f32(16, 4097, 64, x_addr=256, w_addr=256).mt == 16      # general
+
+
+def test_f32_entries_reject_gemm_shapes_before_touching_a_device():
+    lib = _lib.load()
+    l = np.ones((17, 8), np.float32)
+    r = np.ones((8, 17), np.float32)
+    out = np.full((17, 17), 7.0, np.float32)
+    assert lib.dmc_matmul_f32_gpu_try(l.ctypes.data, r.ctypes.data, out.ctypes.data, 17, 8, 17) == -2
+    assert b"GEMV shapes only" in lib.dmc_hip_last_error()
+    assert np.all(out == 7.0)
+    assert lib.dmc_matmul_f32_gpu_try(0, 0, out.ctypes.data, 1, 8, -1) == -2
+    assert lib.dmc_matmul_f32_gpu_try(0, 0, out.ctypes.data, 0, 8, 4) == 0  # m == 0: no-op
+    assert lib.dmc_hip_gemv_f32_rd(0, 0, 0, -1, 4, 4) == -2
+
+
+def test_f32_dropin_fails_loudly_without_a_device():
+    code = ("import numpy as np, demonic_amd as d\n"
+            "print(d.matmul_f32_gpu_try(np.ones((4, 8), np.float32), np.ones(8, np.float32))[0], flush=True)\n"
+            "d.matmul_f32_gpu(np.ones((4, 8), np.float32), np.ones(8, np.float32))\nprint('returned')\n")
+    r = _run_isolated(code, DMC_HIP_DISABLE="1")
+    assert r.returncode != 0
+    assert r.stdout.split("\n")[0] == "-1"  # DMC_HIP_ENODEV from the try form
+    assert "dmc_hip: fatal: dmc_matmul_f32_gpu" in r.stderr
+    assert "returned" not in r.stdout
