@@ -455,7 +455,30 @@ def f32_weights(d, reps: int) -> dict:
         out[label] = {"us": round(us, 3)}
         log(f"{label}: {us:.2f} us/call (PCIe-inclusive)")
     d.release_weights()
+    out["f32 cpu W@x"] = f32_cpu_baseline(w, x)
+    log(f"f32 cpu W@x: {out['f32 cpu W@x']['value']} GB/s ({out['f32 cpu W@x']['sample']})")
     return out
+
+
+def f32_cpu_baseline(w: np.ndarray, x: np.ndarray, seconds: float = 2.0) -> dict:
+    """The reference's f32 `W @ x` restated (oracle matmul_f32: the scalar_matmul
+    chain, one thread as the reference runs it, jit.rs:20715-20802) on the
+    first 512 rows of w, timed on this host."""
+    import oracle
+
+    ws = np.ascontiguousarray(w[:512])
+    k = ws.shape[1]
+    oracle.matmul_f32(ws, x)
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        oracle.matmul_f32(ws, x)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    per = el / calls
+    return {"value": round((4 * 512 * k + 4 * k + 4 * 512) / per / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port", "sample": f"W[512,{k}] f32 @ x: {calls} calls in {el:.1f}s"}
 
 
 def ingress(d, w) -> dict:
