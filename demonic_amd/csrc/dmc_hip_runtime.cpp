@@ -561,7 +561,7 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
         dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, n, m, k, n};
         const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
         if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
-        e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
+        e = dmc::launch_rd(p, pl, pl.workspace_bytes ? c.ws.p : nullptr, c.stream);
     } else {
         dmc::CsProblem p{static_cast<const uint16_t *>(dw), xsrc, ydst, m, k, n, batch, ls, rs};
         const dmc::CsPlan pl = dmc::plan_cs(p, c.cus);
@@ -1137,7 +1137,7 @@ int32_t dmc_hip_gemv_rd(int64_t x_dev, int64_t w_dev, int64_t y_dev, int64_t m, 
                      k, reinterpret_cast<float *>(y_dev), n, m, k, n};
     const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
     if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
-    hipError_t e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
+    hipError_t e = dmc::launch_rd(p, pl, pl.workspace_bytes ? c.ws.p : nullptr, c.stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return DMC_HIP_OK;
 }
@@ -1207,7 +1207,7 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
             dmc::RdProblem p{g.w[i], k, g.x[i], k, g.y[i], g.n[i], m, k, g.n[i]};
             const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
             if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
-            hipError_t e = dmc::launch_rd(p, pl, c.ws.p, c.stream);
+            hipError_t e = dmc::launch_rd(p, pl, pl.workspace_bytes ? c.ws.p : nullptr, c.stream);
             if (e != hipSuccess) return hip_fail(e, "kernel launch");
         }
     }

@@ -2929,10 +2929,11 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
 
     // MFMA kernels for skinny M >= 2: packed rows, k a multiple of 64.  The
     // layout, by measurement on MI355X: rows16 with compact x for M <= 8 (C4
-    // m = 2..4: 155-167 us against 170-214 for the wide layout; m = 8: 165
-    // against 174); for larger M the wide layout where its 256-row workgroups
-    // give >= 1.5 per CU (C4), rows16 elsewhere.  (A third layout, 16-row tiles with k split over the waves,
-    // measured 1.2-2.7x slower than rows16 on every shape and was removed.)
+    // m = 2..4: 155-167 us against 170-214 for the wide layout; m = 8: 164-165
+    // against 166 on the gemm layout and 173-174 on the wide one); from 9
+    // rows the gemm layout (below).  The wide layout is kept for DMC_HIP_RD_MFMA_KIND=6.
+    // (A third layout, 16-row tiles with k split over the waves, measured
+    // 1.2-2.7x slower than rows16 on every shape and was removed.)
     // From 3 activation rows: at m = 2 the streaming kernel with 16 (or 8)
     // weight rows per workgroup is as fast or faster (C2 up 19.6 us against
     // 21.7, down 21.5-22.2 against 22.2, C4 146.6 against 154.5, C1 equal);
@@ -2948,13 +2949,12 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.mt = 16;
         mp.kvec = 0;
         const int64_t gy = (p.m + 15) / 16;
-        const bool wide_fits = 2 * ((p.n + kWideRows - 1) / kWideRows) * gy >= 3 * cus &&
-                               (int64_t)kWideRows * p.k * 2 <= INT32_MAX;
-        // Above 16 activation rows, the gemm layout (16 * MB rows per
-        // workgroup: W streams once per 32 or 64 rows instead of per 16); from
-        // 9 rows too where the wide layout does not fill the device (C2 up and
-        // down at m = 12 and 16: 34-38 us against 41-44 on rows16; at m = 8
-        // rows16 wins, 27-31 against 31-33).
+        // From 9 activation rows, the gemm layout (16 * MB rows per workgroup:
+        // W streams once per 16, 32 or 64 rows; at 16-row tiles it splits x
+        // in the kernel): C2 up and down at m = 12 and 16, 34-38 us against
+        // 41-44 on rows16 (at m = 8 rows16 wins, 27-31 against 31-33); C4 at
+        // m = 12 / 16, 164.3 / 166.3 us against 177.0 / 177.4 on the wide
+        // layout (same box), k in one slice there.
         // On a small matrix the gemm layout's two extra launches (x split,
         // slice sum) outweigh its reuse: rows16, which streams the weights
         // once per 16 activation rows, while that totals at most 80 MiB.
@@ -2964,8 +2964,7 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // at m = 12 22.9 / 24.5, m = 24 44 / 28; C2 at m = 12 38 / 32.
         const int64_t wbytes = (int64_t)2 * p.n * p.k;
         const bool small = gy * wbytes <= ((int64_t)80 << 20);
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND",
-                                 p.m <= 8 ? 7 : p.m <= 16 && wide_fits ? 6 : small ? 7 : 8);
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m <= 8 ? 7 : small ? 7 : 8);
         const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
         const bool planes_fit = (int64_t)6 * p.m * p.k <= INT32_MAX;          // x planes' buffer range
         mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;
@@ -3211,8 +3210,12 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             return hipGetLastError();
         }
         if (pl.mkind == 8) {
-            if (!workspace || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 || pl.kslices > 65535 ||
-                (int64_t)pl.kslices * pl.kchunks < p.k / 64)
+            // The workspace holds x's planes (unless the kernel splits x
+            // itself) and the slice partials (when k is split): a fused
+            // single-slice plan needs none and may be given none.
+            const bool needs_ws = !pl.xfuse || pl.kslices > 1;
+            if ((needs_ws && !workspace) || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 ||
+                pl.kslices > 65535 || (int64_t)pl.kslices * pl.kchunks < p.k / 64)
                 return hipErrorInvalidValue;
             if (pl.xfuse && pl.mt != 16) return hipErrorInvalidValue;
             uint16_t *xs = pl.xfuse ? nullptr : static_cast<uint16_t *>(workspace);

@@ -119,8 +119,9 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
     # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
-    # (two 16-row blocks per workgroup, 4 activation rows); larger M on the LM
-    # head: the wide layout, 16 activation rows per tile
+    # (two 16-row blocks per workgroup, 4 activation rows); 9..16 rows on the LM
+    # head: the gemm layout with 16-row tiles, x split in the kernel, k in one
+    # slice (no workspace)
     for m in (3, 4):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
@@ -133,7 +134,8 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
     for m in (9, 16):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-6, 16, 256, 8, 501), p
+        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x, p.workspace_bytes) == \
+            (-8, 16, 256, 8, 501, 0), p
     # prefill-sized M: the gemm layout, 32 or 64 activation rows per workgroup
     for m, mt in ((17, 32), (32, 32), (33, 64), (128, 64), (512, 64)):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
@@ -210,7 +212,7 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert p.slices == -8, p
     monkeypatch.setenv("DMC_HIP_RD_R16_TILES", "4")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
-    assert p.slices == -6, p  # tiles only shape the rows16 layout
+    assert p.slices == -8, p  # tiles only shape the rows16 layout
     p = d.plan("rd", 4, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.rows_per_group, p.grid_x) == (-7, 64, 2004), p
     monkeypatch.delenv("DMC_HIP_RD_R16_TILES")
@@ -446,3 +448,11 @@ def test_f32_dropin_fails_loudly_without_a_device():
     assert r.stdout.split("\n")[0] == "-1"  # DMC_HIP_ENODEV from the try form
     assert "dmc_hip: fatal: dmc_matmul_f32_gpu" in r.stderr
     assert "returned" not in r.stdout
+
+
+def test_gemm_layout_with_fused_split_and_one_slice_has_no_workspace():
+    """m = 9..16 on 65k-98k rows: the tiles fill the device, so the gemm layout
+    keeps k in one slice and splits x itself -- no workspace (the launch is
+    then given none)."""
+    p = d.plan("rd", 12, 1024, 80000, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.workspace_bytes, p.grid_x) == (-8, 16, 0, 313), p

@@ -1,8 +1,9 @@
 """GPU parity at the full size of two BASELINE configurations.
 
-C4: the LM head W [128256, 4096] (1.05 GB) at M = 1, 2, 4, 8, 16, each M on
-the kernel its real shape plans (streaming at M = 1 and 2, rows16 with two
-blocks per workgroup at 4 and 8, the wide MFMA layout at 16).  C3: the whole
+C4: the LM head W [128256, 4096] (1.05 GB) at M = 1, 2, 4, 8, 12, 16, each M
+on the kernel its real shape plans (streaming at M = 1 and 2, rows16 with two
+blocks per workgroup at 4 and 8, the gemm MFMA layout with x split in the
+kernel and k in one slice at 12 and 16).  C3: the whole
 32-layer Llama-3-8B decode sweep (13.97 GB of weights), scheduled as the bench
 runs it, every projection of every layer sampled with that layer's own x.
 
@@ -21,8 +22,8 @@ from parity import check, check_bound
 pytestmark = pytest.mark.gpu
 
 # M -> (kind, rows per workgroup) the real C4 shape must plan: kind is the
-# streaming kernel's windows per lane (> 0) or -(MFMA layout) (6 wide, 7 rows16)
-C4_PLANS = {1: (1, 4), 2: (1, 16), 4: (-7, 32), 8: (-7, 32), 16: (-6, 256)}
+# streaming kernel's windows per lane (> 0) or -(MFMA layout) (7 rows16, 8 gemm)
+C4_PLANS = {1: (1, 4), 2: (1, 16), 4: (-7, 32), 8: (-7, 32), 12: (-8, 256), 16: (-8, 256)}
 
 
 @pytest.fixture(scope="module")
@@ -49,7 +50,7 @@ def test_c4_full_lm_head(hip, c4_weight, m):
         hip.synchronize()
         y = dy.download(np.float32, (m, n))
     # 512 random rows, the first and last, and the last row of every
-    # 256-row block (the wide layout's workgroup boundary)
+    # 256-row block (the gemm layout's workgroup boundary)
     rng = np.random.default_rng(m)
     rows = np.unique(np.r_[0, n - 1, rng.integers(0, n, 512), np.arange(255, n, 256)])
     wr = W.counter_rows(0, W.C4_TENSOR, rows, k, 0.02)

@@ -955,6 +955,26 @@ def test_prefill_gemm_within_bound(hip, m, k, n, monkeypatch):
         check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm m={m} k={k} n={n} row {r}")
 
 
+@pytest.mark.parametrize("m,k,n", [(9, 1024, 700), (16, 4096, 513)])
+def test_gemm_fused_single_slice_needs_no_workspace(hip, m, k, n, monkeypatch):
+    """16-row activation tiles split x in the kernel, so with k in one slice
+    (what the planner picks when the tiles alone fill the device, e.g. m =
+    9..16 on 65k-98k rows) the plan has no workspace and the launch gets none:
+    through the drop-in and through device pointers."""
+    monkeypatch.setenv("DMC_HIP_GEMM_MAX_SLICES", "1")
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")
+    x, w = case(m, k, n, seed=9700 + m + k + n, edge=True)
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert (p.slices, p.mt, p.workspace_bytes) == (-8, 16, 0), p
+    y_ref = ref(x, w)
+    check(run_rd(hip, x, w), y_ref, what=f"gemm fused unsplit m={m} k={k} n={n}")
+    with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        hip.gemv_rd(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        check(dy.download(np.float32, (m, n)), y_ref, what=f"gemm fused unsplit device m={m} k={k} n={n}")
+
+
 @pytest.mark.parametrize("m,k,n", [(17, 4096, 1000), (64, 576, 513), (100, 1024, 260)])
 def test_prefill_gemm_unsplit(hip, m, k, n, monkeypatch):
     """The gemm layout with k in one slice (DMC_HIP_GEMM_MAX_SLICES=1: what it
