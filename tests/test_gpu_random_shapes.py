@@ -1,0 +1,111 @@
+"""Seeded random shapes through every entry, against the oracle.
+
+The shape-specific tests pin the cases each kernel was written for; this
+sweep draws shapes the planners were not tuned on -- activation rows 1..40
+(every kernel family: streaming, shared-x, misaligned rows, general, the
+three MFMA layouts with partial tiles and k slices), k with every residue mod
+64 and 8 including odd values, n from 1 to ~3000 -- so a plan that no
+hand-written case reaches still meets the parity rule.  Each case runs the
+bf16 weight through `x @ W'` (row-dot), the drop-in `x @ W`, and the
+column-stream kernels on device pointers, and an f32 weight through the
+f32 route.  Half the cases carry edge data (subnormals, +-0, +-1e-38,
+inf/NaN weights); where the edge data makes a row ill-conditioned the
+elementwise bound applies (tests/parity.py).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from demonic_amd import workloads as W
+from parity import check, check_bound
+from test_gpu_parity import case, run_cs, run_cs_dev, run_rd
+
+pytestmark = pytest.mark.gpu
+
+MS = [1, 1, 1, 2, 3, 4, 5, 7, 8, 9, 12, 13, 16, 17, 24, 33, 40]
+
+
+def draw(i):
+    rng = np.random.default_rng(20000 + i)
+    m = int(rng.choice(MS))
+    kind = i % 4
+    if kind == 0:
+        k = 64 * int(rng.integers(1, 48))            # MFMA-eligible
+    elif kind == 1:
+        k = 8 * int(rng.integers(1, 400))            # 16-byte rows
+    elif kind == 2:
+        k = int(rng.integers(1, 3200))               # any residue
+    else:
+        k = 2 * int(rng.integers(1, 1600)) + 1       # odd
+    n = int(rng.integers(1, 3000 if m * k < 40000 else 800))
+    while m * k * n > 12_000_000:
+        n = max(1, n // 2)
+    return m, k, n, bool(i % 2)
+
+
+CASES = [draw(i) for i in range(160)]
+
+
+def compare(y, y_ref, x, wf, what):
+    """The parity rule; rows whose products include inf/NaN or that the edge
+    data leaves ill-conditioned are held to the elementwise bound instead."""
+    try:
+        check(y, y_ref, what=what)
+    except AssertionError:
+        fin = np.all(np.isfinite(wf), axis=1)
+        for r in range(y.shape[0]):
+            check_bound(y[r, fin], y_ref[r, fin], x[r], wf[fin], what=f"{what} row {r}")
+        nf = ~np.isfinite(y_ref)
+        assert np.array_equal(np.isnan(y[nf]), np.isnan(y_ref[nf])), what
+        z = np.isfinite(y_ref) & (y_ref == 0)
+        assert np.array_equal(y[z].view(np.uint32), y_ref[z].view(np.uint32)), what
+
+
+@pytest.mark.parametrize("m,k,n,edge", CASES)
+def test_random_shape_bf16(hip, m, k, n, edge):
+    x, w = case(m, k, n, seed=m * 7919 + k * 31 + n, edge=edge)
+    y_ref = oracle.matmul_bf16_t(x, w)
+    wf = W.bf16_to_f32(w)
+    for run, name in ((run_rd, "rd"), (run_cs, "cs"), (run_cs_dev, "cs_dev")):
+        compare(run(hip, x, w), y_ref, x, wf, f"random {name} m={m} k={k} n={n} edge={edge}")
+
+
+@pytest.mark.parametrize("m,k,n,edge", CASES[::2])
+def test_random_shape_f32(hip, m, k, n, edge):
+    rng = np.random.default_rng(m * 31 + k * 7 + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)  # [n, k]: the weight rows
+    if edge:
+        flat = w.reshape(-1)
+        pos = rng.integers(0, flat.size, size=max(1, flat.size // 100))
+        flat[pos] = rng.choice(np.array([0.0, -0.0, 1e-38, -1e-45, np.inf, np.nan], np.float32), size=pos.size)
+    y_ref = oracle.matmul_f32(x, np.ascontiguousarray(w.T))  # [m, n]
+    if m <= 16 or n <= 16:  # the shapes the drop-in serves, in both orientations
+        y = hip.matmul_f32_gpu(x, np.ascontiguousarray(w.T))
+        compare(y, y_ref, x, w, f"random f32 x@W m={m} k={k} n={n}")
+        y = hip.matmul_f32_gpu(w, np.ascontiguousarray(x.T))  # [n, m]: the same products, fma(w, x)
+        compare(np.ascontiguousarray(y.T), y_ref, x, w, f"random f32 W@x m={m} k={k} n={n}")
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(max(4, 4 * m * n)) as dy:
+        hip.gemv_f32_rd(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (m, n))
+    compare(y, y_ref, x, w, f"random f32 device m={m} k={k} n={n}")
+
+
+MFMA_CASES = [c for c in CASES if c[1] % 64 == 0 and c[0] >= 2]
+
+
+@pytest.mark.parametrize("kind", ["6", "7", "8"])
+@pytest.mark.parametrize("m,k,n,edge", MFMA_CASES)
+def test_random_shape_each_mfma_layout(hip, m, k, n, edge, kind, monkeypatch):
+    """The MFMA-eligible draws (k % 64 == 0, m >= 2) on each layout forced:
+    wide (256 rows per workgroup), rows16, gemm (16/32/64-row activation
+    tiles, x split in the kernel or by a launch, k slices)."""
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", kind)
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")
+    x, w = case(m, k, n, seed=m * 104729 + k + n, edge=edge)
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert p.slices == -int(kind), p
+    compare(run_rd(hip, x, w), oracle.matmul_bf16_t(x, w), x, W.bf16_to_f32(w),
+            f"random mfma kind={kind} m={m} k={k} n={n} edge={edge}")
