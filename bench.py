@@ -272,14 +272,21 @@ def main(argv=None) -> int:
     wall = timed(graph.launch)
     bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
     value = bytes_step * a.steps / wall / 1e9
-    # device time of the same K steps (HIP events; see batch_us), over enough
-    # back-to-back replays of the timed graph that they hold >= 400 launches
+    # device time of the same K steps (HIP events; see batch_us), repeated in
+    # one graph until it holds >= 400 launches: each graph replay carries a
+    # fixed cost of its own (~20-30 us on these boxes), which 40 launches
+    # (--steps 20) would otherwise charge to their kernels
     replays = max(1, -(-400 // (2 * a.steps)))
+    if replays > 1:
+        graph.destroy()
+        with d.Graph() as graph:
+            for _ in range(replays):
+                steps()
+        graph.launch()
     e0, e1 = d.Event(), d.Event()
     graph.launch()
     e0.record()
-    for _ in range(replays):
-        graph.launch()
+    graph.launch()
     e1.record()
     e1.synchronize()
     ev_ms = e0.elapsed_ms(e1) / replays
