@@ -844,7 +844,10 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
         const int p0 = (j * NW + wave) * 64;  // the wave's first window
-        const float xfirst = p0 > 0 ? X[8 * p0 - 1] : 0.0f;
+        // x[8 p0 - 1] only where it exists: a wave whose windows all lie
+        // past K (K = 2450 on 8 waves) must not read beyond x (a plain load,
+        // no range check), and its masked windows need a finite x.
+        const float xfirst = p0 > 0 && 8 * p0 - 1 < K ? X[8 * p0 - 1] : 0.0f;
         const float x0[8] = {__uint_as_float(xa[j][0]), __uint_as_float(xa[j][1]), __uint_as_float(xa[j][2]),
                              __uint_as_float(xa[j][3]), __uint_as_float(xb[j][0]), __uint_as_float(xb[j][1]),
                              __uint_as_float(xb[j][2]), __uint_as_float(xb[j][3])};

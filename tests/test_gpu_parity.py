@@ -232,6 +232,27 @@ def test_misaligned_weight_view(hip, offset, k, n):
     check(y, ref(x, w), what=f"view +{offset} k={k} n={n}")
 
 
+@pytest.mark.parametrize("k", [2450, 2306, 3074])
+def test_any_alignment_rowdot_with_waves_past_k_on_device_pointers(hip, k):
+    """Rows at 4-byte (not 16-byte) alignment on the any-alignment kernel with
+    8 waves, where the last waves' windows all lie past K: x sits in a device
+    region of exactly K floats, and its last element is +inf, so a masked
+    window that picked up a real x value would turn -0 weights into NaN."""
+    n = 567
+    rng = np.random.default_rng(k)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    x[0, -1] = np.inf
+    w = W.bf16_rne(rng.standard_normal((n, k)).astype(np.float32))
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(4 * n) as dy:
+        p = hip.plan("rd", 1, k, n, x_addr=dx.addr, w_addr=dw.addr)
+        assert p.vec == 2 and p.slices == 1 and p.waves == 8, p
+        hip.gemv_rd(dx, dw, dy, 1, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (1, n))
+    check(y, ref(x, w), what=f"any-alignment device k={k}")
+
+
 @pytest.mark.parametrize("offset,k,n", [(2, 4096, 300), (6, 777, 1000), (2, 11008, 4097), (0, 4097, 4097),
                                         (10, 3, 9), (2, 2, 513)])
 def test_column_stream_weight_views_at_any_2_byte_offset(hip, offset, k, n):

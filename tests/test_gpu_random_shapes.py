@@ -109,3 +109,70 @@ def test_random_shape_each_mfma_layout(hip, m, k, n, edge, kind, monkeypatch):
     assert p.slices == -int(kind), p
     compare(run_rd(hip, x, w), oracle.matmul_bf16_t(x, w), x, W.bf16_to_f32(w),
             f"random mfma kind={kind} m={m} k={k} n={n} edge={edge}")
+
+
+def draw_batched(i):
+    rng = np.random.default_rng(30000 + i)
+    k = int(rng.choice([int(rng.integers(1, 900)), 8 * int(rng.integers(1, 200))]))
+    n = int(rng.choice([int(rng.integers(1, 700)), 8 * int(rng.integers(1, 120))]))
+    batch = int(rng.integers(1, 9))
+    m = int(rng.choice([1, 1, 2, 3]))
+    ls = m * k + int(rng.integers(0, 3)) * int(rng.choice([0, 1, 8]))
+    if rng.integers(0, 4) == 0:
+        ls = 0  # one activation broadcast to every slice
+    rs = k * n + int(rng.choice([0, 1, 2, 8, 64]))
+    return m, k, n, batch, ls, rs, bool(i % 2)
+
+
+@pytest.mark.parametrize("m,k,n,batch,ls,rs,edge", [draw_batched(i) for i in range(40)])
+def test_random_batched(hip, m, k, n, batch, ls, rs, edge):
+    """The batched entry (column-stream kernels, affine slices at any strides,
+    a broadcast activation) against each slice's reference."""
+    rng = np.random.default_rng(m + k * 3 + n * 5 + batch)
+    x = rng.standard_normal(max(1, (batch - 1) * ls + m * k)).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal((batch - 1) * rs + k * n).astype(np.float32))
+    if edge:
+        pos = rng.integers(0, w.size, size=max(1, w.size // 200))
+        w[pos] = rng.choice(np.array([0x0001, 0x8001, 0x0000, 0x8000, 0x7F80], np.uint16), size=pos.size)
+    y = hip.matmul_bf16_gpu_batched(x, w, m, k, n, batch, ls, rs)
+    for z in range(batch):
+        xz = x[z * ls: z * ls + m * k].reshape(m, k)
+        wz = w[z * rs: z * rs + k * n].reshape(k, n)
+        y_ref = oracle.matmul_bf16(xz, wz)
+        compare(y[z * m * n:(z + 1) * m * n].reshape(m, n), y_ref, xz, W.bf16_to_f32(np.ascontiguousarray(wz.T)),
+                f"random batched m={m} k={k} n={n} batch={batch} ls={ls} rs={rs} slice {z}")
+
+
+def draw_grouped(i):
+    rng = np.random.default_rng(40000 + i)
+    k = int(rng.choice([8 * int(rng.integers(1, 1200)), int(rng.integers(1, 5000))]))
+    m = int(rng.choice([1, 1, 2, 3, 4]))
+    ns = [int(rng.integers(0, 1500)) for _ in range(int(rng.integers(1, 11)))]
+    return k, ns, m
+
+
+@pytest.mark.parametrize("k,ns,m", [draw_grouped(i) for i in range(24)])
+def test_random_grouped(hip, k, ns, m):
+    """Grouped row-dot launches of 1..10 problems (empty ones included, more
+    than 8 split into launches, shapes outside the streaming kernel one by
+    one) against each problem's reference."""
+    rng = np.random.default_rng(k + sum(ns) + m)
+    xs = [rng.standard_normal((m, k)).astype(np.float32) for _ in ns]
+    ws = [W.bf16_rne(np.float32(0.02) * rng.standard_normal((n, k)).astype(np.float32)) for n in ns]
+    dxs = [hip.DeviceBuffer.from_numpy(x) for x in xs]
+    dws = [hip.DeviceBuffer.from_numpy(w) if w.size else hip.DeviceBuffer(16) for w in ws]
+    dys = [hip.DeviceBuffer(max(4 * m * n, 4)) for n in ns]
+    try:
+        hip.gemv_rd_grouped(dxs, dws, dys, ns, m, k)
+        hip.synchronize()
+        for i, n in enumerate(ns):
+            if n == 0:
+                continue
+            y = dys[i].download(np.float32, (m, n))
+            y_ref = oracle.matmul_bf16_t(xs[i], ws[i])
+            wf = W.bf16_to_f32(ws[i])
+            for r in range(m):
+                check_bound(y[r], y_ref[r], xs[i][r], wf, what=f"random grouped k={k} problem {i} row {r}")
+    finally:
+        for b in dxs + dws + dys:
+            b.free()
