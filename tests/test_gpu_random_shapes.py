@@ -61,13 +61,31 @@ def compare(y, y_ref, x, wf, what):
         assert np.array_equal(y[z].view(np.uint32), y_ref[z].view(np.uint32)), what
 
 
+def run_rd_dev(hip, x, w, woff=0):
+    """x @ W' through dmc_hip_gemv_rd on device regions sized exactly to the
+    operands (the weight `woff` bytes into a region that ends at its last
+    element), so a read past any operand leaves its allocation."""
+    m, k = x.shape
+    n = w.shape[0]
+    wb = np.frombuffer(np.ascontiguousarray(w).tobytes(), np.uint8)
+    with hip.DeviceBuffer(woff + wb.size) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        dw.upload(wb, offset=woff)
+        hip.gemv_rd(dx, dw.addr + woff, dy, m, k, n)
+        hip.synchronize()
+        return dy.download(np.float32, (m, n))
+
+
 @pytest.mark.parametrize("m,k,n,edge", CASES)
 def test_random_shape_bf16(hip, m, k, n, edge):
     x, w = case(m, k, n, seed=m * 7919 + k * 31 + n, edge=edge)
     y_ref = oracle.matmul_bf16_t(x, w)
     wf = W.bf16_to_f32(w)
-    for run, name in ((run_rd, "rd"), (run_cs, "cs"), (run_cs_dev, "cs_dev")):
-        compare(run(hip, x, w), y_ref, x, wf, f"random {name} m={m} k={k} n={n} edge={edge}")
+    woff = 2 * (m + k + n) % 16  # weight views at 2-byte offsets (0 .. 14)
+    runs = ((run_rd, "rd"), (run_cs, "cs"), (run_cs_dev, "cs_dev"),
+            (lambda h, a, b: run_rd_dev(h, a, b), "rd_dev"), (lambda h, a, b: run_rd_dev(h, a, b, woff), "rd_view"))
+    for run, name in runs:
+        compare(run(hip, x, w), y_ref, x, wf, f"random {name} m={m} k={k} n={n} edge={edge} woff={woff}")
 
 
 @pytest.mark.parametrize("m,k,n,edge", CASES[::2])
