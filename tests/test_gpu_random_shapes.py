@@ -76,6 +76,20 @@ def run_rd_dev(hip, x, w, woff=0):
         return dy.download(np.float32, (m, n))
 
 
+def run_cs_view(hip, x, w, woff):
+    """x @ W' through dmc_hip_gemv_cs with W^T [K,N] `woff` bytes into a
+    region that ends at its last element (rows at any 2-byte alignment)."""
+    m, k = x.shape
+    n = w.shape[0]
+    wb = np.frombuffer(np.ascontiguousarray(w.T).tobytes(), np.uint8)
+    with hip.DeviceBuffer(woff + wb.size) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        dw.upload(wb, offset=woff)
+        hip.gemv_cs(dx, dw.addr + woff, dy, m, k, n)
+        hip.synchronize()
+        return dy.download(np.float32, (m, n))
+
+
 @pytest.mark.parametrize("m,k,n,edge", CASES)
 def test_random_shape_bf16(hip, m, k, n, edge):
     x, w = case(m, k, n, seed=m * 7919 + k * 31 + n, edge=edge)
@@ -83,7 +97,8 @@ def test_random_shape_bf16(hip, m, k, n, edge):
     wf = W.bf16_to_f32(w)
     woff = 2 * (m + k + n) % 16  # weight views at 2-byte offsets (0 .. 14)
     runs = ((run_rd, "rd"), (run_cs, "cs"), (run_cs_dev, "cs_dev"),
-            (lambda h, a, b: run_rd_dev(h, a, b), "rd_dev"), (lambda h, a, b: run_rd_dev(h, a, b, woff), "rd_view"))
+            (lambda h, a, b: run_rd_dev(h, a, b), "rd_dev"), (lambda h, a, b: run_rd_dev(h, a, b, woff), "rd_view"),
+            (lambda h, a, b: run_cs_view(h, a, b, woff), "cs_view"))
     for run, name in runs:
         compare(run(hip, x, w), y_ref, x, wf, f"random {name} m={m} k={k} n={n} edge={edge} woff={woff}")
 
