@@ -209,3 +209,97 @@ def test_random_grouped(hip, k, ns, m):
     finally:
         for b in dxs + dws + dys:
             b.free()
+
+
+def draw_graph(i):
+    rng = np.random.default_rng(50000 + i)
+    calls = []
+    for _ in range(int(rng.integers(2, 6))):
+        layout = str(rng.choice(["rd", "cs"]))
+        m = int(rng.choice([1, 1, 2, 4, 9, 20]))
+        k = int(rng.choice([64 * int(rng.integers(1, 40)), 8 * int(rng.integers(1, 300)), int(rng.integers(2, 2000))]))
+        n = int(rng.integers(8, 1500))
+        calls.append((layout, m, k, n))
+    return calls
+
+
+@pytest.mark.parametrize("calls", [draw_graph(i) for i in range(12)])
+def test_random_graph_replays(hip, calls):
+    """A random sequence of row-dot and column-stream GEMVs (split-K
+    workspace, MFMA layouts, misaligned rows) captured once after an eager
+    call of each, replayed three times with new activations uploaded between
+    replays: every replay matches the reference."""
+    rng = np.random.default_rng(len(calls) * 977 + sum(c[2] for c in calls))
+    ops = []
+    try:
+        for layout, m, k, n in calls:
+            w = W.bf16_rne(np.float32(0.05) * rng.standard_normal((n, k)).astype(np.float32))
+            wl = w if layout == "rd" else np.ascontiguousarray(w.T)
+            ops.append((layout, m, k, n, w, hip.DeviceBuffer.from_numpy(wl), hip.DeviceBuffer(4 * m * k),
+                        hip.DeviceBuffer(4 * m * n)))
+
+        def issue():
+            for layout, m, k, n, _, dw, dx, dy in ops:
+                (hip.gemv_rd if layout == "rd" else hip.gemv_cs)(dx, dw, dy, m, k, n)
+
+        for _, m, k, _, _, _, dx, _ in ops:
+            dx.upload(rng.standard_normal((m, k)).astype(np.float32))
+        issue()  # eager: sizes the workspace the captured calls share
+        hip.synchronize()
+        with hip.Graph() as g:
+            issue()
+        try:
+            for rep in range(3):
+                xs = []
+                for _, m, k, n, _, _, dx, dy in ops:
+                    x = rng.standard_normal((m, k)).astype(np.float32)
+                    dx.upload(x)
+                    dy.upload(np.full(m * n, np.nan, np.float32))
+                    xs.append(x)
+                g.launch()
+                hip.synchronize()
+                for (layout, m, k, n, w, _, _, dy), x in zip(ops, xs):
+                    y = dy.download(np.float32, (m, n))
+                    compare(y, oracle.matmul_bf16_t(x, w), x, W.bf16_to_f32(w),
+                            f"graph replay {rep} {layout} m={m} k={k} n={n}")
+        finally:
+            g.destroy()
+    finally:
+        for op in ops:
+            for b in op[5:]:
+                b.free()
+
+
+def draw_deferred(i):
+    rng = np.random.default_rng(60000 + i)
+    return [(int(rng.integers(1, 600)), int(rng.integers(8, 700)), int(rng.integers(1, 4)),
+             bool(rng.integers(0, 4) == 0)) for _ in range(int(rng.integers(2, 9)))]
+
+
+@pytest.mark.parametrize("seq", [draw_deferred(i) for i in range(12)])
+def test_random_deferred_sequences(hip, seq):
+    """Random runs of deferred batched calls; some read the previous call's
+    pending output as their activation (the overlap rule flushes first), and
+    the sequence ends at a flush: every output matches the reference chain
+    of the values it was computed from."""
+    rng = np.random.default_rng(sum(k * n for k, n, _, _ in seq))
+    outs, refs = [], []
+    prev = None
+    for k, n, batch, chain in seq:
+        if chain and prev is not None and prev[1] >= k:
+            pk, pn, pout, pref = prev
+            x, x_ref = pout[:k], pref[:k]  # the pending output, read as activations
+            batch = 1
+        else:
+            x = rng.standard_normal(batch * k).astype(np.float32)
+            x_ref = x.copy()
+        w = W.bf16_rne(rng.standard_normal(batch * k * n).astype(np.float32))
+        out = np.full(batch * n, np.nan, np.float32)
+        hip.matmul_bf16_gpu_batched_deferred(x, w, out, 1, k, n, batch, k, k * n)
+        ref = oracle.matmul_bf16_batched(x_ref, w, k, n, batch, k, k * n)
+        outs.append(out)
+        refs.append(ref)
+        prev = (k, batch * n, out, ref)
+    hip.flush()
+    for i, (out, ref) in enumerate(zip(outs, refs)):
+        check(out, ref, tol=1e-4, what=f"deferred call {i}")
