@@ -12,6 +12,8 @@ f32 route.  Half the cases carry edge data (subnormals, +-0, +-1e-38,
 inf/NaN weights); where the edge data makes a row ill-conditioned the
 elementwise bound applies (tests/parity.py).
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -23,10 +25,14 @@ from test_gpu_parity import case, run_cs, run_cs_dev, run_rd
 pytestmark = pytest.mark.gpu
 
 MS = [1, 1, 1, 2, 3, 4, 5, 7, 8, 9, 12, 13, 16, 17, 24, 33, 40]
+# More draws or another seed for an exploratory run (the committed defaults
+# are what the suite runs).
+DRAWS = int(os.environ.get("DMC_TEST_RANDOM_DRAWS", "160"))
+SEED = int(os.environ.get("DMC_TEST_RANDOM_SEED", "0"))
 
 
 def draw(i):
-    rng = np.random.default_rng(20000 + i)
+    rng = np.random.default_rng(20000 + SEED * 100000 + i)
     m = int(rng.choice(MS))
     kind = i % 4
     if kind == 0:
@@ -43,7 +49,7 @@ def draw(i):
     return m, k, n, bool(i % 2)
 
 
-CASES = [draw(i) for i in range(160)]
+CASES = [draw(i) for i in range(DRAWS)]
 
 
 def compare(y, y_ref, x, wf, what):
@@ -145,7 +151,7 @@ def test_random_shape_each_mfma_layout(hip, m, k, n, edge, kind, monkeypatch):
 
 
 def draw_batched(i):
-    rng = np.random.default_rng(30000 + i)
+    rng = np.random.default_rng(30000 + SEED * 100000 + i)
     k = int(rng.choice([int(rng.integers(1, 900)), 8 * int(rng.integers(1, 200))]))
     n = int(rng.choice([int(rng.integers(1, 700)), 8 * int(rng.integers(1, 120))]))
     batch = int(rng.integers(1, 9))
@@ -157,7 +163,7 @@ def draw_batched(i):
     return m, k, n, batch, ls, rs, bool(i % 2)
 
 
-@pytest.mark.parametrize("m,k,n,batch,ls,rs,edge", [draw_batched(i) for i in range(40)])
+@pytest.mark.parametrize("m,k,n,batch,ls,rs,edge", [draw_batched(i) for i in range(DRAWS // 4)])
 def test_random_batched(hip, m, k, n, batch, ls, rs, edge):
     """The batched entry (column-stream kernels, affine slices at any strides,
     a broadcast activation) against each slice's reference."""
@@ -177,14 +183,14 @@ def test_random_batched(hip, m, k, n, batch, ls, rs, edge):
 
 
 def draw_grouped(i):
-    rng = np.random.default_rng(40000 + i)
+    rng = np.random.default_rng(40000 + SEED * 100000 + i)
     k = int(rng.choice([8 * int(rng.integers(1, 1200)), int(rng.integers(1, 5000))]))
     m = int(rng.choice([1, 1, 2, 3, 4]))
     ns = [int(rng.integers(0, 1500)) for _ in range(int(rng.integers(1, 11)))]
     return k, ns, m
 
 
-@pytest.mark.parametrize("k,ns,m", [draw_grouped(i) for i in range(24)])
+@pytest.mark.parametrize("k,ns,m", [draw_grouped(i) for i in range(DRAWS * 3 // 20)])
 def test_random_grouped(hip, k, ns, m):
     """Grouped row-dot launches of 1..10 problems (empty ones included, more
     than 8 split into launches, shapes outside the streaming kernel one by
@@ -212,7 +218,7 @@ def test_random_grouped(hip, k, ns, m):
 
 
 def draw_graph(i):
-    rng = np.random.default_rng(50000 + i)
+    rng = np.random.default_rng(50000 + SEED * 100000 + i)
     calls = []
     for _ in range(int(rng.integers(2, 6))):
         layout = str(rng.choice(["rd", "cs"]))
@@ -223,7 +229,7 @@ def draw_graph(i):
     return calls
 
 
-@pytest.mark.parametrize("calls", [draw_graph(i) for i in range(12)])
+@pytest.mark.parametrize("calls", [draw_graph(i) for i in range(DRAWS * 3 // 40)])
 def test_random_graph_replays(hip, calls):
     """A random sequence of row-dot and column-stream GEMVs (split-K
     workspace, MFMA layouts, misaligned rows) captured once after an eager
@@ -271,12 +277,12 @@ def test_random_graph_replays(hip, calls):
 
 
 def draw_deferred(i):
-    rng = np.random.default_rng(60000 + i)
+    rng = np.random.default_rng(60000 + SEED * 100000 + i)
     return [(int(rng.integers(1, 600)), int(rng.integers(8, 700)), int(rng.integers(1, 4)),
              bool(rng.integers(0, 4) == 0)) for _ in range(int(rng.integers(2, 9)))]
 
 
-@pytest.mark.parametrize("seq", [draw_deferred(i) for i in range(12)])
+@pytest.mark.parametrize("seq", [draw_deferred(i) for i in range(DRAWS * 3 // 40)])
 def test_random_deferred_sequences(hip, seq):
     """Random runs of deferred batched calls; some read the previous call's
     pending output as their activation (the overlap rule flushes first), and
