@@ -134,6 +134,12 @@ class Rotating:
             b.free()
 
 
+# --no-graph: every batch launched one host call at a time (profiled runs:
+# under rocprofv3 the replay of a captured graph has aborted or crashed the
+# process on these boxes, while the same replays run cleanly without it)
+GRAPHS = True
+
+
 def batch_us(d, fn, reps: int, graph: bool = True) -> float:
     """Average device time of `reps` back-to-back launches of fn(0), fn(1), ...:
     HIP events on the library stream around the batch, kernel durations plus
@@ -146,7 +152,7 @@ def batch_us(d, fn, reps: int, graph: bool = True) -> float:
     fn(0)
     d.synchronize()
     g = None
-    if graph:
+    if graph and GRAPHS:
         with d.Graph() as g:
             for i in range(reps):
                 fn(i)
@@ -179,6 +185,9 @@ def main(argv=None) -> int:
     ap.add_argument("--extended", action="store_true",
                     help="also time C1, C3, C4, C5 and the column-stream layout (stderr + 'extended')")
     ap.add_argument("--c3", action="store_true", help="also time C3, the 32-layer decode sweep")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch every batch one host call at a time, HIP graphs left out entirely "
+                         "(for profiled runs; the timed C2 steps then run eagerly too)")
     ap.add_argument("--no-c3", action="store_true",
                     help="leave C3 out of --extended (its HIP-graph replays are not traced: under rocprofv3 "
                          "one aborted the queue with a malformed-packet error)")
@@ -191,6 +200,8 @@ def main(argv=None) -> int:
     ap.add_argument("--f32", action="store_true",
                     help="only the f32-weight `W @ x` lines (row-dot f32 kernel and drop-in) at C2's shapes")
     a = ap.parse_args(argv)
+    global GRAPHS
+    GRAPHS = not a.no_graph
 
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the GEMV shards by weight rows "
@@ -264,33 +275,44 @@ def main(argv=None) -> int:
     floor_us = batch_us(d, lambda i: d.probe_read(None, 0), reps)
 
     # timed region: K steps, each the two GEMVs, inputs resident, replayed
-    # from a HIP graph captured once (after one untimed replay)
-    with d.Graph() as graph:
-        steps()
-    graph.launch()
-    d.synchronize()
-    wall = timed(graph.launch)
-    bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
-    value = bytes_step * a.steps / wall / 1e9
-    # device time of the same K steps (HIP events; see batch_us), repeated in
-    # one graph until it holds >= 400 launches: each graph replay carries a
-    # fixed cost of its own (~20-30 us on these boxes), which 40 launches
-    # (--steps 20) would otherwise charge to their kernels
+    # from a HIP graph captured once (after one untimed replay); with
+    # --no-graph launched one call at a time
     replays = max(1, -(-400 // (2 * a.steps)))
-    if replays > 1:
-        graph.destroy()
-        with d.Graph() as graph:
-            for _ in range(replays):
-                steps()
-        graph.launch()
+    bytes_step = sum(b_alg(*shapes[nm].shape) for nm in order)
     e0, e1 = d.Event(), d.Event()
-    graph.launch()
-    e0.record()
-    graph.launch()
-    e1.record()
-    e1.synchronize()
+    if GRAPHS:
+        with d.Graph() as graph:
+            steps()
+        graph.launch()
+        d.synchronize()
+        wall = timed(graph.launch)
+        # device time of the same K steps (HIP events; see batch_us), repeated
+        # in one graph until it holds >= 400 launches: each graph replay
+        # carries a fixed cost of its own (~20-30 us on these boxes), which
+        # 40 launches (--steps 20) would otherwise charge to their kernels
+        if replays > 1:
+            graph.destroy()
+            with d.Graph() as graph:
+                for _ in range(replays):
+                    steps()
+            graph.launch()
+        graph.launch()
+        e0.record()
+        graph.launch()
+        e1.record()
+        e1.synchronize()
+        graph.destroy()
+    else:
+        steps()
+        d.synchronize()
+        wall = timed(steps)
+        e0.record()
+        for _ in range(replays):
+            steps()
+        e1.record()
+        e1.synchronize()
+    value = bytes_step * a.steps / wall / 1e9
     ev_ms = e0.elapsed_ms(e1) / replays
-    graph.destroy()
     # the same K steps launched one call at a time (garbage collector paused)
     gc.disable()
     try:
@@ -325,7 +347,8 @@ def main(argv=None) -> int:
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": round(wall / a.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16w-f32acc",
-        "submission": "one HIP graph replay of the K timed steps (2K kernel launches)",
+        "submission": ("one HIP graph replay of the K timed steps (2K kernel launches)" if GRAPHS
+                       else "the K timed steps launched one call at a time (--no-graph)"),
         "eager": {"value": round(bytes_step * a.steps / eager_wall / 1e9, 1),
                   "note": "the same K steps launched one Python call at a time, host wall time"},
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) f32 activations (PCG64 seed 0)",
@@ -348,7 +371,9 @@ def main(argv=None) -> int:
     }
     if a.extended:
         result["extended"] = extended(d, W, a.steps)
-    if (a.extended and not a.no_c3) or a.c3:
+    if ((a.extended and not a.no_c3) or a.c3) and not GRAPHS:
+        log("C3 left out: its decode step is a captured graph (--no-graph)")
+    elif (a.extended and not a.no_c3) or a.c3:
         result["c3"] = c3(d, W)
     print(json.dumps(result), flush=True)
     return 0
