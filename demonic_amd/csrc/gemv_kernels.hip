@@ -1225,8 +1225,9 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
             if (live[t][r]) Y[(int64_t)(m0 + i16) * N + row0 + base[t] + g * 4 + r] = acc[t][r];
 }
 
-// Sixth MFMA layout ("gemm"), for prefill-sized M (> 16): the wide layout
-// with MB tiles of 16 activation rows per workgroup instead of one.  Every
+// Sixth MFMA layout ("gemm"), for 9 activation rows and up (prefill-sized M
+// among them): the wide layout with MB tiles of 16 activation rows per
+// workgroup instead of one.  Every
 // weight tile a wave stages in LDS meets all 16 * MB activation rows, so W
 // streams from HBM once per 16 * MB rows (the 16-row layouts stream it once
 // per 16).  x arrives already split: split_x_planes_kernel writes its three

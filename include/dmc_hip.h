@@ -228,9 +228,10 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
  * Row-dot layout: `vec` is the weight rows' alignment in bf16 elements (8 =
  * 16 bytes); `slices` > 0 is a streaming plan with that many 8-element k
  * windows per lane (with vec < 8, the variant that reads misaligned rows with
- * unaligned 128-bit loads), 0 the general kernel, -6 / -7 the MFMA layouts (256 rows
- * per workgroup / 16 rows per workgroup, mt activation rows); waves and
- * rows_per_group (weight rows per workgroup) describe the workgroup.
+ * unaligned 128-bit loads), 0 the general kernel, -6 / -7 / -8 the MFMA layouts
+ * (wide: 256 rows per workgroup; rows16: 16 rows per block; gemm: 256 rows
+ * against 16, 32 or 64 activation rows, k possibly split; mt activation rows);
+ * waves and rows_per_group (weight rows per workgroup) describe the workgroup.
  * Column-stream layout: `vec` is the row alignment as above; rows_or_rw 0 is
  * the streaming kernel (512 columns per workgroup, rows_per_group k rows per
  * slice; with vec < 8 it reads misaligned rows and the slice pass applies the
@@ -275,8 +276,8 @@ int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, i
 /* HIP graphs of the library stream.  Between capture_begin and capture_end,
  * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
  * workspace -- column-stream split-K partials, or x's bf16 planes and partial
- * sums for row-dot on the gemm layout (m > 16, or 9..16 where the wide layout
- * would leave CUs idle) -- is already large enough, i.e. after one uncaptured
+ * sums for row-dot on the gemm layout (from m = 9 on matrices above 80 MiB) --
+ * is already large enough, i.e. after one uncaptured
  * call of the same shape) are recorded instead of run; capture_end returns an
  * executable graph (0 on error: an entry that allocates or waits was called
  * while capturing) that graph_launch replays on the library stream.  While
