@@ -120,3 +120,38 @@ def test_consecutive_calls_see_each_new_x(hip):
         y = hip.matmul_bf16_gpu_t(xs[i % 3], w)
         assert np.array_equal(y.view(np.uint32), hip.matmul_bf16_gpu(xs[i % 3], wt).view(np.uint32)), i
         check(y, want[i % 3], what=f"call {i}")
+
+
+def test_calls_from_several_threads(hip):
+    """One process-wide context, its entries serialized by a mutex (the
+    reference keeps one context per thread, gpu.rs:186-189): four threads
+    issue synchronous bf16 and f32 calls on their own weights and
+    activations, interleaved; every result is its own call's."""
+    import threading
+
+    cases = []
+    for t in range(4):
+        x, w = data(1 + t % 2, 1024 + 8 * t, 300 + 17 * t, seed=700 + t)
+        wf = np.random.default_rng(800 + t).standard_normal((64 + t, 512)).astype(np.float32)
+        xf = np.random.default_rng(900 + t).standard_normal(512).astype(np.float32)
+        cases.append((x, w, oracle.matmul_bf16_t(x, w), wf, xf, oracle.matmul_f32(wf, xf)))
+    errors = []
+
+    def worker(t):
+        x, w, ref, wf, xf, ref_f = cases[t]
+        try:
+            for i in range(25):
+                if (i + t) % 3:
+                    check(hip.matmul_bf16_gpu_t(x, w), ref, what=f"thread {t} call {i}")
+                else:
+                    check(hip.matmul_f32_gpu(wf, xf), ref_f, what=f"thread {t} f32 call {i}")
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(t,)) for t in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in threads), "a thread did not finish"
+    assert not errors, errors[:2]
