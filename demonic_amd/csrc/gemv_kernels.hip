@@ -1539,7 +1539,7 @@ constexpr int kRows16Pitch = 144;
 template <int MC, int T>
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y,
-                           int N, int K, int M) {
+                           int N, int K, int M, int lpk, float *__restrict__ P) {
     static_assert(MC == 4 || MC == 8 || MC == 16, "activation rows per workgroup");
     static_assert(T == 1 || T == 2 || T == 4, "16-row blocks per workgroup");
     constexpr bool kCompact = MC < 16;
@@ -1550,7 +1550,10 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     const int g = lane >> 4;
     const int m0 = blockIdx.y * MC;
     const int mrows = min(MC, M - m0);
-    const int nlines = K >> 6;
+    // k slice blockIdx.z: lines [l0, l1) of 64 elements (lpk per slice; one
+    // slice unless P, the slices' partial sums, is given)
+    const int l0 = (int)blockIdx.z * lpk;
+    const int l1 = min(K >> 6, l0 + lpk);
 
     // LDS: the waves' weight tiles and x planes while streaming, then the
     // partial sums (T x 8 KiB) in the same bytes.
@@ -1596,7 +1599,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     };
     // Line L's loads; lines past the end read zeros from outside the buffers.
     auto load = [&](Line &r, int L) {
-        const bool live = L < nlines;
+        const bool live = L < l1;
         const uint32_t lw = (uint32_t)L * 128u, lx = (uint32_t)L * 256u;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -1614,7 +1617,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     };
 
     // A wave that owns no line adds -0, the identity that keeps a -0 sum.
-    const float z = wave < nlines ? 0.0f : -0.0f;
+    const float z = l0 + wave < l1 ? 0.0f : -0.0f;
     f32x4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4{z, z, z, z};
@@ -1701,11 +1704,11 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     };
 
     Line la, lb;
-    load(la, wave);
-    for (int L = wave; L < nlines; L += 16) {
+    load(la, l0 + wave);
+    for (int L = l0 + wave; L < l1; L += 16) {
         load(lb, L + 8);
         compute(la);
-        if (L + 8 >= nlines) break;
+        if (L + 8 >= l1) break;
         load(la, L + 16);
         compute(lb);
     }
@@ -1727,10 +1730,17 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             bool live[1][4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) live[0][r] = i16 < mrows && g * 4 + r < nrows;
-            settle_zeros(s, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
+            if (P) {  // a k slice: its partial sums, for gemm_sum_slices_kernel (which settles zeros)
+                float *ps = P + (int64_t)blockIdx.z * M * N + (int64_t)(m0 + i16) * N + row0 + g * 4;
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (live[0][r]) Y[(int64_t)(m0 + i16) * N + row0 + g * 4 + r] = s[0][r];
+                for (int r = 0; r < 4; ++r)
+                    if (live[0][r]) ps[r] = s[0][r];
+            } else {
+                settle_zeros(s, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (live[0][r]) Y[(int64_t)(m0 + i16) * N + row0 + g * 4 + r] = s[0][r];
+            }
         }
     }
 }
@@ -3025,9 +3035,26 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
             int tiles = env_int("DMC_HIP_RD_R16_TILES", mp.mt <= 8 ? 2 : 1);
             if (tiles != 1 && tiles != 2 && tiles != 4) tiles = 1;
+            const int want = tiles;
             const int64_t blocks16 = (p.n + 15) / 16;
             const int64_t min_wg = (int64_t)env_int("DMC_HIP_RD_R16_MIN_WG_PER_CU", 1) * cus;
             while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < min_wg) tiles >>= 1;
+            // Where the grid would take fewer blocks per workgroup than wanted
+            // (C2 down: 256 16-row blocks), keep them and split k in two
+            // instead: the same grid, half the x bytes per weight byte, and a
+            // slice-sum launch (gemm_sum_slices_kernel, which settles zeros).
+            // Measured: C2 down m = 3 / 4 / 6 / 8, 22.9 / 23.1 / 28.6 / 27.9 us
+            // -> 22.0 / 22.0 / 23.9 / 23.9; on a matrix of 32 MiB (C1) the
+            // extra launch costs more than the bytes save (8.3-10.3 us ->
+            // 10.9-11.7), so only from 64 MiB of weights.
+            const int64_t nl = p.k / 64;
+            if (tiles < want && nl >= 32 && wbytes >= ((int64_t)64 << 20) &&
+                env_int("DMC_HIP_RD_R16_SPLIT", 1) != 0 && (blocks16 + want - 1) / want * gy * 2 >= min_wg) {
+                tiles = want;
+                mp.kslices = 2;
+                mp.kchunks = (int)((nl + 1) / 2);
+                mp.workspace_bytes = (size_t)2 * p.m * p.n * 4;
+            }
             mp.rpw = 16 * tiles;
         }
         mp.grid_x = (p.n + mp.rpw - 1) / mp.rpw;
@@ -3245,16 +3272,24 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         }
         if (pl.mkind == 7) {
             const int tiles = pl.rpw / 16;
-#define DMC_R16(MC, T)                                                                                      \
-    if (pl.mt == MC && tiles == T) {                                                                        \
-        hipLaunchKernelGGL((gemv_rd_mfma_rows16_kernel<MC, T>), grid, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n, \
-                           (int)p.k, (int)p.m);                                                             \
-        return hipGetLastError();                                                                           \
-    }
+            const int ks = pl.kslices;
+            const int lpk = ks > 1 ? pl.kchunks : (int)(p.k / 64);
+            if (ks < 1 || ks > 2 || (ks > 1 && (!workspace || (int64_t)ks * lpk < p.k / 64)))
+                return hipErrorInvalidValue;
+            float *part = ks > 1 ? static_cast<float *>(workspace) : nullptr;
+            const dim3 grid3((unsigned)pl.grid_x, (unsigned)pl.grid_y, (unsigned)ks);
+#define DMC_R16(MC, T)                                                                                       \
+    if (pl.mt == MC && tiles == T) {                                                                         \
+        hipLaunchKernelGGL((gemv_rd_mfma_rows16_kernel<MC, T>), grid3, dim3(512), 0, s, p.w, p.x, p.y, (int)p.n, \
+                           (int)p.k, (int)p.m, lpk, part);                                                   \
+    } else
             DMC_R16(4, 1) DMC_R16(4, 2) DMC_R16(4, 4) DMC_R16(8, 1) DMC_R16(8, 2) DMC_R16(8, 4)
-            DMC_R16(16, 1) DMC_R16(16, 2) DMC_R16(16, 4)
+            DMC_R16(16, 1) DMC_R16(16, 2) DMC_R16(16, 4) return hipErrorInvalidValue;
 #undef DMC_R16
-            return hipErrorInvalidValue;
+            if (ks > 1)
+                hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,
+                                   s, part, ks, p.y, p.w, p.x, (int)p.m, (int)p.n, (int)p.k);
+            return hipGetLastError();
         }
         return hipErrorInvalidValue;
     }

@@ -184,11 +184,21 @@ def test_rowdot_mfma_layouts(monkeypatch):
     p = d.plan("rd", 12, 4096, 4096, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group) == (-7, 16, 16), p
     # blocks per workgroup shrink while the grid would fall under 1 per CU:
-    # C2 up/gate keeps two (448 workgroups), C2 down and C1 (256 blocks) one
+    # C2 up/gate keeps two (448 workgroups), C1 (256 blocks, 32 MiB) one;
+    # C2 down (256 blocks, 112 MiB) keeps two and splits k in two instead
+    # (256 workgroups, the slices' partials in the workspace)
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
-    assert (p.mt, p.rows_per_group, p.grid_x) == (8, 32, 448), p
+    assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (8, 32, 448, 0), p
+    p = d.plan("rd", 4, 4096, 4096, x_addr=256, w_addr=256)
+    assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
+    for m, mt in ((3, 4), (4, 4), (6, 8), (8, 8)):
+        p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
+            (-7, mt, 32, 128, 2 * m * 4096 * 4), (m, p)
+    monkeypatch.setenv("DMC_HIP_RD_R16_SPLIT", "0")
     p = d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256)
-    assert (p.mt, p.rows_per_group, p.grid_x) == (4, 16, 256), p
+    assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
+    monkeypatch.delenv("DMC_HIP_RD_R16_SPLIT")
     # the gemm layout splits k while the grid stays within one workgroup per
     # CU: C2 up at m = 64 has 56 tiles of 256 x 64, so 4 slices of 16 chunks;
     # its workspace holds x's three bf16 planes and the 4 partial sums
