@@ -2945,7 +2945,8 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     // layout, by measurement on MI355X: rows16 with compact x for M <= 8 (C4
     // m = 2..4: 155-167 us against 170-214 for the wide layout; m = 8: 164-165
     // against 166 on the gemm layout and 173-174 on the wide one); from 9
-    // rows the gemm layout (below).  The wide layout is kept for DMC_HIP_RD_MFMA_KIND=6.
+    // rows the gemm layout or, on matrices it streams fast enough, rows16
+    // (below).  The wide layout is kept for DMC_HIP_RD_MFMA_KIND=6.
     // (A third layout, 16-row tiles with k split over the waves, measured
     // 1.2-2.7x slower than rows16 on every shape and was removed.)
     // From 3 activation rows: at m = 2 the streaming kernel with 16 (or 8)
@@ -2965,20 +2966,26 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         const int64_t gy = (p.m + 15) / 16;
         // From 9 activation rows, the gemm layout (16 * MB rows per workgroup:
         // W streams once per 16, 32 or 64 rows; at 16-row tiles it splits x
-        // in the kernel): C2 up and down at m = 12 and 16, 34-38 us against
-        // 41-44 on rows16 (at m = 8 rows16 wins, 27-31 against 31-33); C4 at
-        // m = 12 / 16, 164.3 / 166.3 us against 177.0 / 177.4 on the wide
-        // layout (same box), k in one slice there.
-        // On a small matrix the gemm layout's two extra launches (x split,
-        // slice sum) outweigh its reuse: rows16, which streams the weights
-        // once per 16 activation rows, while that totals at most 80 MiB.
-        // Measured (rows16 / gemm, us): W [1024,4096] at m = 128 24 / 32;
-        // [4096,2048] at m = 64 25.6 / 31.5, at m = 128 48 / 34; C1 at
-        // m = 12 13.5 / 20.9, m = 32 25.5 / 25.9, m = 48 36 / 31; [8192,4096]
-        // at m = 12 22.9 / 24.5, m = 24 44 / 28; C2 at m = 12 38 / 32.
+        // in the kernel), except where rows16 (which streams W once per 16
+        // activation rows and needs no extra launch unless k is split) is
+        // faster.  Measured, rows16 / gemm in us:
+        // - up to 16 activation rows on matrices up to 112 MiB: [8192,4096]
+        //   at m = 9 / 12 / 16 16.8 / 16.8 / 18.1 against 21.5 / 21.8 / 22.5;
+        //   C2 up 27.1 / 27.8 / 29.3 against 29.1 / 30.7 / 31.6, down 25.9 /
+        //   26.8 / 28.2 against 29.5 / 30.2 / 31.6.  At 224 MiB they tie or
+        //   gemm wins ([28672,4096] m = 16: 54.7 / 48.5), at 392 MiB and C4
+        //   gemm wins ([14336,14336] m = 16: 97.7 / 72.8; C4 m = 16: 212-216
+        //   against 166-203).
+        // - small matrices while the weights streamed total at most 128 MiB
+        //   (matrix up to 32 MiB) or 80 MiB: C1 at m = 32 / 64 17.2 / 30.1
+        //   against 25.8 / 35.0 (m = 80, 160 MiB: 39.6 / 35.5); [4096,2048] at
+        //   m = 128 30.7 / 34.5 (m = 192: 41.7 / 40.3); [1024,4096] at m = 128
+        //   16.3 / 32.4; [8192,4096] at m = 24 (128 MiB) 29.6 / 27.9.
         const int64_t wbytes = (int64_t)2 * p.n * p.k;
-        const bool small = gy * wbytes <= ((int64_t)80 << 20);
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m <= 8 ? 7 : small ? 7 : 8);
+        const int64_t small_cap = wbytes <= ((int64_t)32 << 20) ? ((int64_t)128 << 20) : ((int64_t)80 << 20);
+        const bool small = gy * wbytes <= small_cap;
+        const bool r16_mid = p.m <= 16 && wbytes <= (int64_t)env_int("DMC_HIP_RD_R16_MID_MIB", 128) << 20;
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m <= 8 || small || r16_mid ? 7 : 8);
         const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
         const bool planes_fit = (int64_t)6 * p.m * p.k <= INT32_MAX;          // x planes' buffer range
         mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;
@@ -3026,34 +3033,44 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         } else {
             // rows16: T 16-row blocks per workgroup, gridDim.x apart, while
             // the grid keeps >= 1 workgroup per CU.  Two blocks share each x
-            // split at MC = 4 and 8 (C4 m = 8: 165 us against 195 with one
-            // block and 174 on the wide layout; C2 up m = 3 / 4 / 6 / 8: 20.4
-            // / 20.5 / 22.5 / 22.8 us against 21.2 / 21.7 / 26.4 / 26.4 with
-            // one; C2 down and C1, 256 blocks, keep one), at MC = 16 the
-            // registers of more blocks cost occupancy (205-217 us against 174
-            // on the wide layout).
+            // split (C4 m = 8: 165 us against 195 with one block and 174 on
+            // the wide layout; C2 up m = 3 / 4 / 6 / 8: 20.4 / 20.5 / 22.5 /
+            // 22.8 us against 21.2 / 21.7 / 26.4 / 26.4 with one, m = 12 / 16
+            // 27.9 / 29.5 against 38 and 30.1 / 31.8 on the gemm layout; C2
+            // down and C1, 256 blocks, keep one unless k is split, below).
             mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
-            int tiles = env_int("DMC_HIP_RD_R16_TILES", mp.mt <= 8 ? 2 : 1);
-            if (tiles != 1 && tiles != 2 && tiles != 4) tiles = 1;
-            const int want = tiles;
+            const int tenv = env_int("DMC_HIP_RD_R16_TILES", 0);
+            const int want = tenv == 1 || tenv == 2 || tenv == 4 ? tenv : 2;
+            int tiles = want;
             const int64_t blocks16 = (p.n + 15) / 16;
             const int64_t min_wg = (int64_t)env_int("DMC_HIP_RD_R16_MIN_WG_PER_CU", 1) * cus;
             while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < min_wg) tiles >>= 1;
             // Where the grid would take fewer blocks per workgroup than wanted
-            // (C2 down: 256 16-row blocks), keep them and split k in two
-            // instead: the same grid, half the x bytes per weight byte, and a
-            // slice-sum launch (gemm_sum_slices_kernel, which settles zeros).
-            // Measured: C2 down m = 3 / 4 / 6 / 8, 22.9 / 23.1 / 28.6 / 27.9 us
-            // -> 22.0 / 22.0 / 23.9 / 23.9; on a matrix of 32 MiB (C1) the
-            // extra launch costs more than the bytes save (8.3-10.3 us ->
-            // 10.9-11.7), so only from 64 MiB of weights.
+            // (C2 down: 256 16-row blocks), keep them (at MC = 16, four) and
+            // split k instead, into the fewest slices that fill the grid: the
+            // x bytes per weight byte stay those of the wanted blocks, and a
+            // slice-sum launch (gemm_sum_slices_kernel, which settles zeros)
+            // follows.  Measured on C2 down: m = 3 / 4 / 6 / 8, 22.9 / 23.1 /
+            // 28.6 / 27.9 us -> 22.0 / 22.0 / 23.9 / 23.9 on two blocks and two
+            // slices; m = 12 / 16, 26.7 / 27.7 us on four blocks and four slices
+            // (27.8 / 30.3 on two and two, 30.6 / 31.8 on the gemm layout).  On
+            // a matrix of 32 MiB (C1) the extra launch costs more than the
+            // bytes save (8.3-10.3 us -> 10.9-11.7), so only from 64 MiB of
+            // weights; and each slice keeps >= 48 lines of 64 k (C2 up, 64
+            // lines: four blocks on two or four slices ran 26-39 us against
+            // 21-29 on two blocks and one).
             const int64_t nl = p.k / 64;
-            if (tiles < want && nl >= 32 && wbytes >= ((int64_t)64 << 20) &&
-                env_int("DMC_HIP_RD_R16_SPLIT", 1) != 0 && (blocks16 + want - 1) / want * gy * 2 >= min_wg) {
-                tiles = want;
-                mp.kslices = 2;
-                mp.kchunks = (int)((nl + 1) / 2);
-                mp.workspace_bytes = (size_t)2 * p.m * p.n * 4;
+            const int ksenv = env_int("DMC_HIP_RD_R16_SPLIT", -1);  // k slices; 0 or 1: never split
+            const int st = tenv ? want : mp.mt == 16 ? 4 : 2;
+            int ks = ksenv;
+            if (ks < 0)
+                for (ks = 2; ks < 8 && (blocks16 + st - 1) / st * gy * ks < min_wg;) ks *= 2;
+            if (tiles < want && ks >= 2 && ks <= 8 && nl >= 48 * ks && wbytes >= ((int64_t)64 << 20) &&
+                (blocks16 + st - 1) / st * gy * ks >= min_wg) {
+                tiles = st;
+                mp.kchunks = (int)((nl + ks - 1) / ks);
+                mp.kslices = (int)((nl + mp.kchunks - 1) / mp.kchunks);
+                mp.workspace_bytes = (size_t)mp.kslices * p.m * p.n * 4;
             }
             mp.rpw = 16 * tiles;
         }
@@ -3274,7 +3291,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             const int tiles = pl.rpw / 16;
             const int ks = pl.kslices;
             const int lpk = ks > 1 ? pl.kchunks : (int)(p.k / 64);
-            if (ks < 1 || ks > 2 || (ks > 1 && (!workspace || (int64_t)ks * lpk < p.k / 64)))
+            if (ks < 1 || ks > 8 || (ks > 1 && (!workspace || lpk < 1 || (int64_t)ks * lpk < p.k / 64)))
                 return hipErrorInvalidValue;
             float *part = ks > 1 ? static_cast<float *>(workspace) : nullptr;
             const dim3 grid3((unsigned)pl.grid_x, (unsigned)pl.grid_y, (unsigned)ks);

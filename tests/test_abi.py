@@ -199,6 +199,26 @@ def test_rowdot_mfma_layouts(monkeypatch):
     p = d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
     monkeypatch.delenv("DMC_HIP_RD_R16_SPLIT")
+    # 9..16 activation rows on matrices up to 128 MiB: rows16 too, two blocks
+    # per workgroup (C2 up/gate, [8192,4096]), or on C2 down four blocks and
+    # k in four slices (64 x 4 workgroups); the gemm layout above 128 MiB
+    for m in (9, 12, 16):
+        p = d.plan("rd", m, 4096, 14336, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 16, 32, 448, 0), p
+        p = d.plan("rd", m, 4096, 8192, x_addr=256, w_addr=256)
+        assert (p.slices, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 32, 256, 0), p
+        p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
+            (-7, 16, 64, 64, 4 * m * 4096 * 4), p
+        assert d.plan("rd", m, 4096, 28672, x_addr=256, w_addr=256).slices == -8
+    # above 16 rows, rows16 while the weights streamed (once per 16 rows)
+    # total at most 128 MiB on a matrix up to 32 MiB, 80 MiB otherwise
+    assert d.plan("rd", 64, 4096, 4096, x_addr=256, w_addr=256).slices == -7     # C1, 128 MiB
+    assert d.plan("rd", 65, 4096, 4096, x_addr=256, w_addr=256).slices == -8     # 160 MiB
+    assert d.plan("rd", 128, 4096, 2048, x_addr=256, w_addr=256).slices == -7
+    assert d.plan("rd", 17, 4096, 8192, x_addr=256, w_addr=256).slices == -8     # 64 MiB matrix, 128 streamed
+    assert d.plan("rd", 16, 4096, 16384, x_addr=256, w_addr=256).slices == -7    # 128 MiB at 16 rows
+    assert d.plan("rd", 16, 4096, 16384 + 16, x_addr=256, w_addr=256).slices == -8
     # the gemm layout splits k while the grid stays within one workgroup per
     # CU: C2 up at m = 64 has 56 tiles of 256 x 64, so 4 slices of 16 chunks;
     # its workspace holds x's three bf16 planes and the 4 partial sums
@@ -229,7 +249,7 @@ def test_rowdot_mfma_layouts(monkeypatch):
     # either layout can be forced
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
-    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-7, 16, 16, 8016), p
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-7, 16, 32, 4008), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "6")
     p = d.plan("rd", 16, 4096, 1000, x_addr=256, w_addr=256)
     assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p

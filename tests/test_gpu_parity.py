@@ -490,16 +490,24 @@ def test_c2_sampled_rows(hip, which):
     check(y2[rows], y_ref, what=f"C2 {which} cs")
 
 
-@pytest.mark.parametrize("m", [3, 4, 6, 8])
-def test_rows16_split_k_on_c2_down(hip, m):
-    """C2 down at 3..8 activation rows: rows16 keeps two 16-row blocks per
-    workgroup and splits k in two (256 workgroups), the slices summed by a
-    second launch that settles zeros.  Activation row 1 is -1e-38 throughout,
-    so against the tiny weights planted in rows 0..3 (and the zero row 4)
-    every product underflows: exact zeros whose signs follow the chain.
+# (shape, m) -> rows16's plan: (blocks per workgroup, workgroups along N, k slices)
+R16_C2_PLANS = {("down", 3): (2, 128, 2), ("down", 4): (2, 128, 2), ("down", 6): (2, 128, 2),
+                ("down", 8): (2, 128, 2), ("down", 9): (4, 64, 4), ("down", 12): (4, 64, 4),
+                ("down", 16): (4, 64, 4), ("up", 12): (2, 448, 1), ("up", 16): (2, 448, 1)}
+
+
+@pytest.mark.parametrize("shape,m", list(R16_C2_PLANS))
+def test_rows16_split_k_on_c2(hip, shape, m):
+    """C2 at 3..16 activation rows on rows16.  Down (256 16-row blocks) keeps
+    two blocks per workgroup at 3..8 rows and splits k in two, four blocks at
+    9..16 rows and four k slices (256 workgroups either way), the slices summed
+    by a second launch that settles zeros; up/gate at 12 and 16 rows runs two
+    blocks per workgroup and k in one slice.  Activation row 1 is -1e-38
+    throughout, so against the tiny weights planted in rows 0..3 (and the zero
+    row 4) every product underflows: exact zeros whose signs follow the chain.
     Sampled rows (every block position, the planted ones, the last) against
     the oracle, within the norm and the elementwise bound."""
-    w, x1 = W.c2()["down"]
+    w, x1 = W.c2()[shape]
     w = w.copy()
     n, k = w.shape
     rng = np.random.default_rng(40 + m)
@@ -511,22 +519,24 @@ def test_rows16_split_k_on_c2_down(hip, m):
     w[4] = 0
     w[5, : k // 2] = 0x3F80   # +1 then -1 against row 1's constant x: a cancellation
     w[5, k // 2:] = 0xBF80
+    tiles, grid_x, ks = R16_C2_PLANS[(shape, m)]
     with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
             hip.DeviceBuffer(4 * m * n) as dy:
         p = hip.plan("rd", m, k, n, x_addr=dx.addr, w_addr=dw.addr)
-        assert (p.slices, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 32, 128, 2 * m * n * 4), p
+        assert (p.slices, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
+            (-7, 16 * tiles, grid_x, (ks * m * n * 4) if ks > 1 else 0), p
         hip.gemv_rd(dx, dw, dy, m, k, n)
         hip.synchronize()
         y = dy.download(np.float32, (m, n))
     rows = np.unique(np.r_[np.arange(0, 40), np.arange(n - 20, n), rng.integers(0, n, 300)])
     mi, ni = np.meshgrid(np.arange(m), rows, indexing="ij")
     y_ref = oracle.gemv_points(x, w, "rd", mi.reshape(-1), ni.reshape(-1)).reshape(m, -1)
-    check(y[:, rows], y_ref, what=f"rows16 split m={m}")
+    check(y[:, rows], y_ref, what=f"rows16 C2 {shape} m={m}")
     assert np.all(y_ref[1, :5] == 0)  # row 5 keeps a subnormal residue in the chain's order
     assert np.array_equal(y[1, :5].view(np.uint32), y_ref[1, :5].view(np.uint32)), (y[1, :5], y_ref[1, :5])
     wf = W.bf16_to_f32(w[rows])
     for r in range(m):
-        check_bound(y[r, rows], y_ref[r], x[r], wf, what=f"rows16 split m={m} row {r}")
+        check_bound(y[r, rows], y_ref[r], x[r], wf, what=f"rows16 C2 {shape} m={m} row {r}")
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 8, 16])
