@@ -3032,19 +3032,43 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             mp.rpw = kWideRows;
         } else {
             // rows16: T 16-row blocks per workgroup, gridDim.x apart, while
-            // the grid keeps >= 1 workgroup per CU.  Two blocks share each x
-            // split (C4 m = 8: 165 us against 195 with one block and 174 on
-            // the wide layout; C2 up m = 3 / 4 / 6 / 8: 20.4 / 20.5 / 22.5 /
-            // 22.8 us against 21.2 / 21.7 / 26.4 / 26.4 with one, m = 12 / 16
-            // 27.9 / 29.5 against 38 and 30.1 / 31.8 on the gemm layout; C2
+            // the grid keeps >= 1 workgroup per CU.  At MC = 4 and 8 two blocks
+            // share each x split (C4 m = 8: 165 us against 195 with one block
+            // and 174 on the wide layout; C2 up m = 3 / 4 / 6 / 8: 20.4 / 20.5
+            // / 22.5 / 22.8 us against 21.2 / 21.7 / 26.4 / 26.4 with one; C2
             // down and C1, 256 blocks, keep one unless k is split, below).
             mp.mt = p.m <= 4 ? 4 : p.m <= 8 ? 8 : 16;
+            // At MC = 16 the x split is as many values as one block's weights,
+            // so up to four blocks share it, on a grid of at least 7/8 of the
+            // CUs: C2 up/gate (896 blocks, 224 workgroups) m = 9 / 12 / 16 23.8
+            // / 24.8 / 26.2 us against 26.9 / 27.9 / 30.2 on two blocks (448);
+            // C1 at m = 64 22.3 against 28.8; [4096,2048] at m = 64 / 128 14.1 /
+            // 26.0 against 17.0 / 29.1.  At MC = 4 and 8 four blocks tie with
+            // two on C2 (m = 4 21.4 / 21.1, m = 8 23.2 / 23.8) and lose on C4.
+            // At MC = 16 (one workgroup per CU at four blocks: 148 VGPRs), among
+            // the block counts whose grid meets that floor, the one with the
+            // least rounds x (T + 1) (a workgroup's time: T blocks of weights
+            // and one x split as costly as one block): [2048,2048] at m = 160
+            // takes two blocks (640 workgroups, 21.6 us) over four (320: a
+            // second round a quarter full, 24.9 us).  At MC = 4 and 8, where
+            // several workgroups share a CU, the most blocks that meet it.
             const int tenv = env_int("DMC_HIP_RD_R16_TILES", 0);
-            const int want = tenv == 1 || tenv == 2 || tenv == 4 ? tenv : 2;
-            int tiles = want;
+            const int want = tenv == 1 || tenv == 2 || tenv == 4 ? tenv : mp.mt == 16 ? 4 : 2;
             const int64_t blocks16 = (p.n + 15) / 16;
-            const int64_t min_wg = (int64_t)env_int("DMC_HIP_RD_R16_MIN_WG_PER_CU", 1) * cus;
-            while (tiles > 1 && (blocks16 + tiles - 1) / tiles * gy < min_wg) tiles >>= 1;
+            const int mwenv = env_int("DMC_HIP_RD_R16_MIN_WG_PER_CU", -1);
+            const int64_t min_wg = mwenv >= 0 ? (int64_t)mwenv * cus : mp.mt == 16 ? cus * 7 / 8 : cus;
+            int tiles = 1;
+            double best = -1;
+            for (int t = want; t >= 1; t >>= 1) {  // ties keep the larger T
+                const int64_t wg = (blocks16 + t - 1) / t * gy;
+                if (t > 1 && wg < min_wg) continue;
+                if (mp.mt < 16) {
+                    tiles = t;
+                    break;
+                }
+                const double cost = (double)((wg + cus - 1) / cus) * (t + 1);
+                if (best < 0 || cost < best) best = cost, tiles = t;
+            }
             // Where the grid would take fewer blocks per workgroup than wanted
             // (C2 down: 256 16-row blocks), keep them (at MC = 16, four) and
             // split k instead, into the fewest slices that fill the grid: the
@@ -3061,12 +3085,12 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // 21-29 on two blocks and one).
             const int64_t nl = p.k / 64;
             const int ksenv = env_int("DMC_HIP_RD_R16_SPLIT", -1);  // k slices; 0 or 1: never split
-            const int st = tenv ? want : mp.mt == 16 ? 4 : 2;
+            const int st = want;
             int ks = ksenv;
             if (ks < 0)
                 for (ks = 2; ks < 8 && (blocks16 + st - 1) / st * gy * ks < min_wg;) ks *= 2;
-            if (tiles < want && ks >= 2 && ks <= 8 && nl >= 48 * ks && wbytes >= ((int64_t)64 << 20) &&
-                (blocks16 + st - 1) / st * gy * ks >= min_wg) {
+            if (tiles < want && ks >= 2 && ks <= 8 && nl >= (ksenv < 0 ? 48 : 1) * ks &&
+                wbytes >= ((int64_t)64 << 20) && (blocks16 + st - 1) / st * gy * ks >= min_wg) {
                 tiles = st;
                 mp.kchunks = (int)((nl + ks - 1) / ks);
                 mp.kslices = (int)((nl + mp.kchunks - 1) / mp.kchunks);

@@ -199,18 +199,27 @@ def test_rowdot_mfma_layouts(monkeypatch):
     p = d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
     monkeypatch.delenv("DMC_HIP_RD_R16_SPLIT")
-    # 9..16 activation rows on matrices up to 128 MiB: rows16 too, two blocks
-    # per workgroup (C2 up/gate, [8192,4096]), or on C2 down four blocks and
-    # k in four slices (64 x 4 workgroups); the gemm layout above 128 MiB
+    # 9..16 activation rows on matrices up to 128 MiB: rows16 too, four blocks
+    # per workgroup on a grid of >= 7/8 of the CUs (C2 up/gate: 224), two
+    # where four would leave fewer ([8192,4096]: 256), or on C2 down four
+    # blocks and k in four slices (64 x 4 workgroups); the gemm layout above
+    # 128 MiB
     for m in (9, 12, 16):
         p = d.plan("rd", m, 4096, 14336, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 16, 32, 448, 0), p
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 16, 64, 224, 0), p
         p = d.plan("rd", m, 4096, 8192, x_addr=256, w_addr=256)
         assert (p.slices, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 32, 256, 0), p
         p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
             (-7, 16, 64, 64, 4 * m * 4096 * 4), p
         assert d.plan("rd", m, 4096, 28672, x_addr=256, w_addr=256).slices == -8
+    # at 16-row activation tiles the block count weighs rounds against the
+    # x split: C1 at m = 64 takes four (256 workgroups, one round), [2048,2048]
+    # at m = 160 two (640 workgroups, 3 rounds of 3) over four (320, 2 rounds of 5)
+    p = d.plan("rd", 64, 4096, 4096, x_addr=256, w_addr=256)
+    assert (p.slices, p.rows_per_group, p.grid_x, p.grid_x * 4) == (-7, 64, 64, 256), p
+    p = d.plan("rd", 160, 2048, 2048, x_addr=256, w_addr=256)
+    assert (p.slices, p.rows_per_group, p.grid_x) == (-7, 32, 64), p
     # above 16 rows, rows16 while the weights streamed (once per 16 rows)
     # total at most 128 MiB on a matrix up to 32 MiB, 80 MiB otherwise
     assert d.plan("rd", 64, 4096, 4096, x_addr=256, w_addr=256).slices == -7     # C1, 128 MiB
@@ -249,7 +258,7 @@ def test_rowdot_mfma_layouts(monkeypatch):
     # either layout can be forced
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     p = d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256)
-    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-7, 16, 32, 4008), p
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-7, 16, 64, 2004), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "6")
     p = d.plan("rd", 16, 4096, 1000, x_addr=256, w_addr=256)
     assert (p.slices, p.rows_per_group, p.waves, p.grid_x) == (-6, 256, 8, 4), p

@@ -493,7 +493,7 @@ def test_c2_sampled_rows(hip, which):
 # (shape, m) -> rows16's plan: (blocks per workgroup, workgroups along N, k slices)
 R16_C2_PLANS = {("down", 3): (2, 128, 2), ("down", 4): (2, 128, 2), ("down", 6): (2, 128, 2),
                 ("down", 8): (2, 128, 2), ("down", 9): (4, 64, 4), ("down", 12): (4, 64, 4),
-                ("down", 16): (4, 64, 4), ("up", 12): (2, 448, 1), ("up", 16): (2, 448, 1)}
+                ("down", 16): (4, 64, 4), ("up", 12): (4, 224, 1), ("up", 16): (4, 224, 1)}
 
 
 @pytest.mark.parametrize("shape,m", list(R16_C2_PLANS))
@@ -501,8 +501,8 @@ def test_rows16_split_k_on_c2(hip, shape, m):
     """C2 at 3..16 activation rows on rows16.  Down (256 16-row blocks) keeps
     two blocks per workgroup at 3..8 rows and splits k in two, four blocks at
     9..16 rows and four k slices (256 workgroups either way), the slices summed
-    by a second launch that settles zeros; up/gate at 12 and 16 rows runs two
-    blocks per workgroup and k in one slice.  Activation row 1 is -1e-38
+    by a second launch that settles zeros; up/gate at 12 and 16 rows runs four
+    blocks per workgroup (224 workgroups) and k in one slice.  Activation row 1 is -1e-38
     throughout, so against the tiny weights planted in rows 0..3 (and the zero
     row 4) every product underflows: exact zeros whose signs follow the chain.
     Sampled rows (every block position, the planted ones, the last) against
