@@ -1241,12 +1241,16 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 // P[slice][m][n] for gemm_sum_slices_kernel.  Numerics, special values and
 // the zero rule are the wide layout's, tile by tile; with slices the zero
 // rule runs after the sum.
-template <int MB, bool FUSE>
-__global__ void __launch_bounds__(512)
+template <int MB, bool FUSE, int NWV>
+__global__ void __launch_bounds__(64 * NWV)
 gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, const uint16_t *__restrict__ XS,
                          float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy) {
-    static_assert(MB >= 1 && MB <= 4, "x staging covers at most 512 threads");
+    static_assert(MB >= 1 && MB <= 4, "16 to 64 activation rows per workgroup");
+    static_assert(NWV == 4 || NWV == 8, "32 weight rows per wave");
     static_assert(!FUSE || MB == 1, "the in-kernel split serves 16-row activation tiles");
+    constexpr int kRows = 32 * NWV;                  // weight rows per workgroup
+    constexpr int kXItems = 128 * MB;                // x staging items (tile, k-block, operand lane)
+    constexpr int kXPer = (kXItems + 64 * NWV - 1) / (64 * NWV);  // items per thread
     constexpr int D = 2;  // register sets of the chunk ring (3 and 4 measured no faster)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -1267,15 +1271,15 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     const int by = (int)(lin % (uint32_t)gy);
     const int bx = (int)(lin / (uint32_t)gy % (uint32_t)gx);
     const int bz = (int)(lin / (uint32_t)gy / (uint32_t)gx);
-    const int row0 = bx * kWideRows;
-    const int nrows = min(kWideRows, N - row0);
+    const int row0 = bx * kRows;
+    const int nrows = min(kRows, N - row0);
     const int m0 = by * 16 * MB;
     const int c0 = bz * kc;                              // this slice's chunks: [c0, c1)
     const int c1 = min(K / 64, c0 + kc);
     const int nchunks = max(0, c1 - c0);
 
-    __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 36 KiB
-    __shared__ u32x4 xpl[2][MB][2][3][64];                                       // MB x 12 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t wt[kRows * kWidePitch];  // 36 KiB at 8 waves
+    __shared__ u32x4 xpl[2][MB][2][3][64];                                   // MB x 12 KiB
     uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
 
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
@@ -1286,54 +1290,68 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         soff[j] = (uint32_t)min(wave * 32 + slr + 8 * j, nrows - 1) * (uint32_t)K * 2u + scol;
-    // x items: threads 0 .. 128*MB-1 = (tile xt = tid/128, k-block b = tid/64 % 2,
-    // operand lane): the lane's 8 elements of each of the three planes (FUSE:
-    // its 8 f32 values, split in `store`), by unconditional buffer loads (rows
-    // past M load from past the range: zeros).
-    const bool xthread = tid < 128 * MB;
-    const int xt = tid >> 7;
-    const int xb = (tid >> 6) & 1;
-    const int xm = m0 + xt * 16 + (lane & 15);
+    // x items it = tid + 64*NWV*j (j < kXPer), those below 128*MB: (tile xt =
+    // it/128, k-block b = it/64 % 2, operand lane = lane): the lane's 8
+    // elements of each of the three planes (FUSE: its 8 f32 values, split in
+    // `store`), by unconditional buffer loads (rows past M load from past the
+    // range: zeros).
+    bool xthread[kXPer];
+    int xt[kXPer], xb[kXPer];
+    uint32_t xoff[kXPer];
     const uint32_t plane_bytes = (uint32_t)M * (uint32_t)K * 2u;
     const __amdgpu_buffer_rsrc_t xrs = FUSE ? weight_rsrc(X, 2u * plane_bytes) : weight_rsrc(XS, 3u * plane_bytes);
-    const uint32_t xelem = (uint32_t)xm * (uint32_t)K + xb * 32 + (lane >> 4) * 8;
-    const uint32_t xoff = xthread && xm < M ? xelem * (FUSE ? 4u : 2u) : kOutOfRange;
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j) {
+        const int it = tid + 64 * NWV * j;
+        xthread[j] = it < kXItems;
+        xt[j] = xthread[j] ? it >> 7 : 0;
+        xb[j] = (it >> 6) & 1;
+        const int xm = m0 + xt[j] * 16 + (lane & 15);
+        const uint32_t xelem = (uint32_t)xm * (uint32_t)K + xb[j] * 32 + (lane >> 4) * 8;
+        xoff[j] = xthread[j] && xm < M ? xelem * (FUSE ? 4u : 2u) : kOutOfRange;
+    }
 
-    constexpr int XQ = FUSE ? 2 : 3;  // x registers per chunk: f32 halves, or the three planes
+    constexpr int XQ = FUSE ? 2 : 3;  // x registers per item and chunk: f32 halves, or the three planes
     struct Regs {
         u32x4 w[4];
-        u32x4 x[XQ];
+        u32x4 x[kXPer][XQ];
     };
     auto load = [&](int c, Regs &r) {
         const uint32_t cb = (uint32_t)(c0 + c) * 128u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + cb);
-        if constexpr (FUSE) {
 #pragma unroll
-            for (int q = 0; q < 2; ++q) r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, 2u * cb + 16u * q, 0);
-        } else {
+        for (int j = 0; j < kXPer; ++j) {
+            if constexpr (FUSE) {
 #pragma unroll
-            for (int q = 0; q < 3; ++q)
-                r.x[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff, q * plane_bytes + cb, 0);
+                for (int q = 0; q < 2; ++q)
+                    r.x[j][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[j], 2u * cb + 16u * q, 0);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 3; ++q)
+                    r.x[j][q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xoff[j], q * plane_bytes + cb, 0);
+            }
         }
     };
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
-        if (xthread) {
+#pragma unroll
+        for (int j = 0; j < kXPer; ++j) {
+            if (!xthread[j]) continue;
             if constexpr (FUSE) {
-                const float v[8] = {__uint_as_float(r.x[0][0]), __uint_as_float(r.x[0][1]),
-                                    __uint_as_float(r.x[0][2]), __uint_as_float(r.x[0][3]),
-                                    __uint_as_float(r.x[1][0]), __uint_as_float(r.x[1][1]),
-                                    __uint_as_float(r.x[1][2]), __uint_as_float(r.x[1][3])};
+                const float v[8] = {__uint_as_float(r.x[j][0][0]), __uint_as_float(r.x[j][0][1]),
+                                    __uint_as_float(r.x[j][0][2]), __uint_as_float(r.x[j][0][3]),
+                                    __uint_as_float(r.x[j][1][0]), __uint_as_float(r.x[j][1][1]),
+                                    __uint_as_float(r.x[j][1][2]), __uint_as_float(r.x[j][1][3])};
                 u32x4 hi, md, lo;
                 split8(v, hi, md, lo);
-                xpl[xbuf][xt][xb][0][lane] = hi;
-                xpl[xbuf][xt][xb][1][lane] = md;
-                xpl[xbuf][xt][xb][2][lane] = lo;
+                xpl[xbuf][xt[j]][xb[j]][0][lane] = hi;
+                xpl[xbuf][xt[j]][xb[j]][1][lane] = md;
+                xpl[xbuf][xt[j]][xb[j]][2][lane] = lo;
             } else {
 #pragma unroll
-                for (int q = 0; q < 3; ++q) xpl[xbuf][xt][xb][q][lane] = r.x[q];
+                for (int q = 0; q < 3; ++q) xpl[xbuf][xt[j]][xb[j]][q][lane] = r.x[j][q];
             }
         }
     };
@@ -2991,7 +3009,6 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;
         mp.waves = 8;
         if (mp.mkind == 8) {
-            mp.rpw = kWideRows;
             // 16 activation rows per workgroup up to m = 16 (no half-empty
             // MFMA tiles: C1 at m = 12 / 16, 20.0 / 21.3 us against 20.5 /
             // 22.5 with 32-row tiles, C2 within 0.5 us), 32 up to m = 32, 64
@@ -3000,6 +3017,20 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // against 152 / 158).
             const int gmt = env_int("DMC_HIP_GEMM_MT", p.m <= 16 ? 16 : p.m <= 32 ? 32 : 64);
             mp.mt = gmt == 16 ? 16 : gmt == 32 ? 32 : 64;
+            // 8 waves (256 weight rows) per workgroup, or 4 (128 rows, two
+            // workgroups per CU) with 32-row tiles where 256-row tiles would
+            // not fill the device without a k split.  Same box, 8 / 4 waves,
+            // us: C2 up m = 17 / 24 / 32 36.7 / 38.8 / 42.2 against 30.9 /
+            // 33.9 / 38.3, down 37.2 / 40.2 / 44.1 against 32.7 / 36.9 / 40.9;
+            // [28672,4096] m = 17 / 32 61.6 / 70.2 against 53.9 / 61.5.  C4
+            // (501 tiles of 256 rows) loses with 4 (m = 17 / 32 182 / 196
+            // against 206 / 225), and so do 64-row tiles everywhere (C2 up /
+            // down m = 64 55 / 57 against 61 / 61, m = 512 232 / 236 against
+            // 268 / 300: each workgroup stages x for half the rows).
+            const int64_t tiles8 = ((p.n + 255) / 256) * ((p.m + mp.mt - 1) / mp.mt);
+            const int gw = env_int("DMC_HIP_GEMM_WAVES", 0);
+            mp.waves = (gw == 4 || (gw != 8 && mp.mt == 32 && tiles8 < cus)) && mp.mt >= 32 ? 4 : 8;
+            mp.rpw = 32 * mp.waves;
             // Split k while the grid fits one workgroup per CU (16-row tiles:
             // two), kchunks chunks of 64 per slice; when that leaves a lone
             // round under 70% full, fill two rounds instead.  Measured on C2's
@@ -3008,9 +3039,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // m = 256: 124 / 125 against 140 / 135), except up at m = 192,
             // whose 168 tiles leave a third of the CUs idle (112 us on three
             // slices against 124 on one).
-            const int64_t tiles = ((p.n + kWideRows - 1) / kWideRows) * ((p.m + mp.mt - 1) / mp.mt);
+            const int64_t tiles = ((p.n + mp.rpw - 1) / mp.rpw) * ((p.m + mp.mt - 1) / mp.mt);
             const int64_t nchunks = p.k / 64;
-            const int64_t per_cu = std::max(1, env_int("DMC_HIP_GEMM_PER_CU", mp.mt == 16 ? 2 : 1));
+            const int64_t per_cu =
+                std::max(1, env_int("DMC_HIP_GEMM_PER_CU", mp.mt == 16 || mp.waves == 4 ? 2 : 1));
             int64_t want = std::max<int64_t>(1, per_cu * cus / tiles);
             if (tiles < cus && tiles * want * 10 < cus * 7) want = std::max<int64_t>(1, 2 * per_cu * cus / tiles);
             // A slice of fewer than 8 chunks pays its pipeline fill and output
@@ -3287,7 +3319,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             // single-slice plan needs none and may be given none.
             const bool needs_ws = !pl.xfuse || pl.kslices > 1;
             if ((needs_ws && !workspace) || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 ||
-                pl.kslices > 65535 || (int64_t)pl.kslices * pl.kchunks < p.k / 64)
+                pl.kslices > 65535 || (int64_t)pl.kslices * pl.kchunks < p.k / 64 || pl.rpw != 32 * pl.waves)
                 return hipErrorInvalidValue;
             if (pl.xfuse && pl.mt != 16) return hipErrorInvalidValue;
             uint16_t *xs = pl.xfuse ? nullptr : static_cast<uint16_t *>(workspace);
@@ -3299,12 +3331,14 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
                                    s, p.x, xs, count);
             const int64_t wgs = pl.grid_x * pl.grid_y * (int64_t)pl.kslices;
             if (wgs > INT32_MAX) return hipErrorInvalidValue;
-#define DMC_GEMM(MB, F)                                                                                      \
-    if (pl.mt == 16 * MB && pl.xfuse == F)                                                                   \
-        hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB, F>), dim3((unsigned)wgs), dim3(512), 0, s, p.w, p.x, xs,  \
-                           p.y, part, (int)p.n, (int)p.k, (int)p.m, pl.kchunks, (int)pl.grid_x, (int)pl.grid_y);  \
+#define DMC_GEMM(MB, F, NW)                                                                                  \
+    if (pl.mt == 16 * MB && pl.xfuse == F && pl.waves == NW)                                                 \
+        hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB, F, NW>), dim3((unsigned)wgs), dim3(64 * NW), 0, s, p.w,  \
+                           p.x, xs, p.y, part, (int)p.n, (int)p.k, (int)p.m, pl.kchunks, (int)pl.grid_x,          \
+                           (int)pl.grid_y);                                                                   \
     else
-            DMC_GEMM(1, true) DMC_GEMM(1, false) DMC_GEMM(2, false) DMC_GEMM(4, false) return hipErrorInvalidValue;
+            DMC_GEMM(1, true, 8) DMC_GEMM(1, false, 8) DMC_GEMM(2, false, 8) DMC_GEMM(4, false, 8)
+            DMC_GEMM(2, false, 4) DMC_GEMM(4, false, 4) return hipErrorInvalidValue;
 #undef DMC_GEMM
             if (pl.kslices > 1)
                 hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,

@@ -174,11 +174,19 @@ def test_rowdot_mfma_layouts(monkeypatch):
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
-    # from 9 activation rows where the wide layout does not fit, and above 16
-    # whatever N, the gemm layout (16 activation rows per workgroup up to 16, 32 up to 128)
-    for m, mt in ((9, 16), (16, 16), (20, 32)):
+    # from 9 activation rows on a matrix above 128 MiB, and above 16 (past the
+    # small-matrix rule) whatever N, the gemm layout (16 activation rows per
+    # workgroup up to 16, 32 up to 32); at 32-row tiles on 4-wave workgroups
+    # of 128 weight rows where 256-row tiles would number fewer than the CUs
+    for m, mt in ((9, 16), (16, 16)):
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, mt, 256, 8, 65), (m, p)
+    p = d.plan("rd", 20, 4096, 16387, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 128, 4, 129), p
+    p = d.plan("rd", 32, 4096, 128256, x_addr=256, w_addr=256)   # 501 tiles of 256 rows
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 256, 8, 501), p
+    p = d.plan("rd", 33, 4096, 16387, x_addr=256, w_addr=256)    # 64-row tiles: 8 waves
+    assert (p.slices, p.mt, p.rows_per_group, p.waves) == (-8, 64, 256, 8), p
     # ... except on a matrix under 64 MiB, where rows16 saves the gemm layout's
     # two extra launches (C1 at m = 12)
     p = d.plan("rd", 12, 4096, 4096, x_addr=256, w_addr=256)
@@ -267,7 +275,11 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-8, 16, 256, 4), p
     monkeypatch.setenv("DMC_HIP_GEMM_MT", "32")
     p = d.plan("rd", 4, 4096, 1000, x_addr=256, w_addr=256)
-    assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (-8, 32, 256, 4), p
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 128, 4, 8), p
+    monkeypatch.setenv("DMC_HIP_GEMM_WAVES", "8")
+    p = d.plan("rd", 4, 4096, 1000, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-8, 32, 256, 8, 4), p
+    monkeypatch.delenv("DMC_HIP_GEMM_WAVES")
     monkeypatch.delenv("DMC_HIP_GEMM_MT")
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "0")  # disabled: the FMA kernels
     assert d.plan("rd", 16, 4096, 128256, x_addr=256, w_addr=256).slices > 0

@@ -1025,6 +1025,33 @@ def test_prefill_gemm_within_bound(hip, m, k, n, monkeypatch):
         check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm m={m} k={k} n={n} row {r}")
 
 
+@pytest.mark.parametrize("waves,m,k,n", [(4, 17, 4096, 1000), (4, 33, 576, 257), (4, 64, 4096, 513),
+                                         (4, 100, 14336, 260), (4, 200, 128, 17), (4, 130, 1024, 600),
+                                         (8, 17, 4096, 1000), (8, 24, 1024, 700), (8, 32, 64, 300)])
+def test_prefill_gemm_four_and_eight_wave_workgroups(hip, waves, m, k, n, monkeypatch):
+    """The gemm layout on 4-wave workgroups (128 weight rows, two per CU;
+    DMC_HIP_GEMM_WAVES=4; the default at 32-row tiles on short grids), 32-
+    and 64-row activation tiles: at 64 each thread stages two x items; and
+    32-row tiles forced back onto 8-wave workgroups (C4's plan).  Partial
+    weight and activation tiles, k split or not, edge data; every element
+    within the rigorous bound, non-finite classes and exact zeros as the
+    reference."""
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")
+    monkeypatch.setenv("DMC_HIP_GEMM_WAVES", str(waves))
+    x, w = case(m, k, n, seed=9300 + m + k + n, edge=True)
+    w[min(3, n - 1)] = 0
+    p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
+    assert (p.slices, p.mt, p.waves, p.rows_per_group) == (-8, 32 if m <= 32 else 64, waves, 32 * waves), p
+    y = run_rd(hip, x, w)
+    rows = np.unique(np.r_[0, min(3, n - 1), n - 1, np.random.default_rng(m).integers(0, n, 160)])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    check(y[:, rows], y_ref, what=f"gemm {waves} waves m={m} k={k} n={n}")
+    wf = W.bf16_to_f32(w[rows])
+    fin = np.all(np.isfinite(wf), axis=1)
+    for r in range(0, m, 7):
+        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm {waves} waves m={m} k={k} n={n} row {r}")
+
+
 @pytest.mark.parametrize("m,k,n", [(9, 1024, 700), (16, 4096, 513)])
 def test_gemm_fused_single_slice_needs_no_workspace(hip, m, k, n, monkeypatch):
     """16-row activation tiles split x in the kernel, so with k in one slice
