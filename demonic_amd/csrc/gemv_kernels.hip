@@ -2990,10 +2990,11 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         // - up to 16 activation rows on matrices up to 112 MiB: [8192,4096]
         //   at m = 9 / 12 / 16 16.8 / 16.8 / 18.1 against 21.5 / 21.8 / 22.5;
         //   C2 up 27.1 / 27.8 / 29.3 against 29.1 / 30.7 / 31.6, down 25.9 /
-        //   26.8 / 28.2 against 29.5 / 30.2 / 31.6.  At 224 MiB they tie or
-        //   gemm wins ([28672,4096] m = 16: 54.7 / 48.5), at 392 MiB and C4
-        //   gemm wins ([14336,14336] m = 16: 97.7 / 72.8; C4 m = 16: 212-216
-        //   against 166-203).
+        //   26.8 / 28.2 against 29.5 / 30.2 / 31.6 (two blocks per workgroup
+        //   on up; four measured faster still).  At 224 MiB they tie
+        //   ([28672,4096] m = 16: 49.8 / 49.2 on four blocks), at 392 MiB
+        //   and C4 gemm wins ([14336,14336] m = 16: 83.1 / 73.3; C4 m = 12 /
+        //   16: 193.7 / 203.3 against 175.8 / 162.4).
         // - small matrices while the weights streamed total at most 128 MiB
         //   (matrix up to 32 MiB) or 80 MiB: C1 at m = 32 / 64 17.2 / 30.1
         //   against 25.8 / 35.0 (m = 80, 160 MiB: 39.6 / 35.5); [4096,2048] at
