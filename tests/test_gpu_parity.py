@@ -493,16 +493,18 @@ def test_c2_sampled_rows(hip, which):
 # (shape, m) -> rows16's plan: (blocks per workgroup, workgroups along N, k slices)
 R16_C2_PLANS = {("down", 3): (2, 128, 2), ("down", 4): (2, 128, 2), ("down", 6): (2, 128, 2),
                 ("down", 8): (2, 128, 2), ("down", 9): (4, 64, 4), ("down", 12): (4, 64, 4),
-                ("down", 16): (4, 64, 4), ("up", 12): (4, 224, 1), ("up", 16): (4, 224, 1)}
+                ("down", 16): (4, 64, 4), ("up", 12): (4, 224, 1), ("up", 16): (4, 224, 1),
+                ("down", 24): (4, 64, 2)}  # forced onto rows16: two activation tiles, each k-split
 
 
 @pytest.mark.parametrize("shape,m", list(R16_C2_PLANS))
-def test_rows16_split_k_on_c2(hip, shape, m):
+def test_rows16_split_k_on_c2(hip, shape, m, monkeypatch):
     """C2 at 3..16 activation rows on rows16.  Down (256 16-row blocks) keeps
     two blocks per workgroup at 3..8 rows and splits k in two, four blocks at
     9..16 rows and four k slices (256 workgroups either way), the slices summed
     by a second launch that settles zeros; up/gate at 12 and 16 rows runs four
-    blocks per workgroup (224 workgroups) and k in one slice.  Activation row 1 is -1e-38
+    blocks per workgroup (224 workgroups) and k in one slice; down at 24 rows
+    forced onto rows16 has two 16-row activation tiles, each on two k slices.  Activation row 1 is -1e-38
     throughout, so against the tiny weights planted in rows 0..3 (and the zero
     row 4) every product underflows: exact zeros whose signs follow the chain.
     Sampled rows (every block position, the planted ones, the last) against
@@ -514,12 +516,16 @@ def test_rows16_split_k_on_c2(hip, shape, m):
     x = rng.standard_normal((m, k)).astype(np.float32)
     x[0] = x1
     x[1] = np.float32(-1e-38)
+    zrows = [1] + ([17] if m > 17 else [])  # one in each activation tile
+    x[zrows] = np.float32(-1e-38)
     w[0:2] = 0x0001
     w[2:4] = 0x8001
     w[4] = 0
     w[5, : k // 2] = 0x3F80   # +1 then -1 against row 1's constant x: a cancellation
     w[5, k // 2:] = 0xBF80
     tiles, grid_x, ks = R16_C2_PLANS[(shape, m)]
+    if m > 16:
+        monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
             hip.DeviceBuffer(4 * m * n) as dy:
         p = hip.plan("rd", m, k, n, x_addr=dx.addr, w_addr=dw.addr)
@@ -532,8 +538,10 @@ def test_rows16_split_k_on_c2(hip, shape, m):
     mi, ni = np.meshgrid(np.arange(m), rows, indexing="ij")
     y_ref = oracle.gemv_points(x, w, "rd", mi.reshape(-1), ni.reshape(-1)).reshape(m, -1)
     check(y[:, rows], y_ref, what=f"rows16 C2 {shape} m={m}")
-    assert np.all(y_ref[1, :5] == 0)  # row 5 keeps a subnormal residue in the chain's order
-    assert np.array_equal(y[1, :5].view(np.uint32), y_ref[1, :5].view(np.uint32)), (y[1, :5], y_ref[1, :5])
+    for zr in zrows:
+        assert np.all(y_ref[zr, :5] == 0)  # row 5 keeps a subnormal residue in the chain's order
+        assert np.array_equal(y[zr, :5].view(np.uint32), y_ref[zr, :5].view(np.uint32)), \
+            (zr, y[zr, :5], y_ref[zr, :5])
     wf = W.bf16_to_f32(w[rows])
     for r in range(m):
         check_bound(y[r, rows], y_ref[r], x[r], wf, what=f"rows16 C2 {shape} m={m} row {r}")
