@@ -2967,11 +2967,17 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     // (below).  The wide layout is kept for DMC_HIP_RD_MFMA_KIND=6.
     // (A third layout, 16-row tiles with k split over the waves, measured
     // 1.2-2.7x slower than rows16 on every shape and was removed.)
-    // From 3 activation rows: at m = 2 the streaming kernel with 16 (or 8)
-    // weight rows per workgroup is as fast or faster (C2 up 19.6 us against
-    // 21.7, down 21.5-22.2 against 22.2, C4 146.6 against 154.5, C1 equal);
-    // at m = 3 and 4 it is 7-80% slower.
-    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", 3);
+    // From 3 activation rows, or from 2 where the streaming kernel does not
+    // take both in one pass (rows too long for its registers at m = 2: it
+    // would stream W once per activation row; [32768,28672] 521 us against
+    // 269 on rows16).  Elsewhere at m = 2 the streaming kernel is as fast or
+    // faster (same box, streaming / rows16, us: C2 up 20.6 / 20.5, down 22.3 /
+    // 22.0, [1024,4096] 4.4 / 7.1, [4096,11008] 17.9 / 21.3, [11008,4096]
+    // 17.4 / 18.7, C4 147.1 / 154.0; C1 9.3 / 8.4 the one loss); at m = 3 and
+    // 4 it is 7-80% slower everywhere.
+    RdPlan sfit{};
+    const bool stream_fits = plan_stream(p.m, p.k, &p.n, 1, num_cus > 0 ? num_cus : 256, sfit) && sfit.mt >= p.m;
+    const int mfma_min_m = env_int("DMC_HIP_RD_MFMA_MIN_M", stream_fits ? 3 : 2);
     if (mfma_min_m > 0 && p.m >= mfma_min_m && p.k >= 64 && p.k % 64 == 0 && p.k <= INT32_MAX / 2 &&
         aligned(p.w, 16) && aligned(p.x, 16) && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n &&
         (int64_t)16 * 4 * p.k <= INT32_MAX && (p.m + 15) / 16 <= 65535) {  // rows16: 16 x rows of f32

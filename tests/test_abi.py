@@ -113,11 +113,17 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
     assert p.mt == 1 and p.slices >= 1, p
     # M = 2: the streaming kernel, 16 weight rows per workgroup where the grid
-    # keeps 4 workgroups per CU (8 on C2 up/gate)
+    # keeps 4 workgroups per CU (8 on C2 up/gate); rows16 where rows too long
+    # for the streaming kernel's registers would take one activation row per pass
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 16, 8016), p
     p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
+    assert d.plan("rd", 2, 28672, 32768, x_addr=256, w_addr=256).slices == -7
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "3")
+    p = d.plan("rd", 2, 28672, 32768, x_addr=256, w_addr=256)
+    assert (p.slices, p.mt) == (7, 1), p   # the streaming kernel, one activation row per pass
+    monkeypatch.delenv("DMC_HIP_RD_MFMA_MIN_M")
     # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
     # (two 16-row blocks per workgroup, 4 activation rows); 9..16 rows on the LM
     # head: the gemm layout with 16-row tiles, x split in the kernel, k in one

@@ -195,13 +195,35 @@ def test_shapes(hip, m, k, n, layout):
     check(y, ref(x, w), what=f"{layout} m={m} k={k} n={n}")
 
 
+@pytest.mark.parametrize("k,n", [(28672, 600), (28672, 4099), (20480, 1000)])
+def test_two_activation_rows_long_rows_on_rows16(hip, k, n):
+    """M = 2 on rows too long for the streaming kernel to take both activation
+    rows in one pass (k > 16384): rows16 by default (4099 rows: two blocks per
+    workgroup and k in two slices).  Edge data; sampled rows within the
+    rigorous bound, special classes and zero signs as the reference."""
+    x, w = case(2, k, n, seed=8200 + k + n, edge=True)
+    p = hip.plan("rd", 2, k, n, x_addr=256, w_addr=256)
+    assert p.slices == -7 and p.mt == 4, p
+    y = run_rd(hip, x, w)
+    rows = np.unique(np.r_[np.arange(0, min(40, n)), np.arange(max(0, n - 40), n),
+                           np.random.default_rng(k + n).integers(0, n, 200)])
+    y_ref = oracle.matmul_bf16_t(x, w[rows])
+    check(y[:, rows], y_ref, what=f"m=2 rows16 k={k} n={n}")
+    wf = W.bf16_to_f32(w[rows])
+    fin = np.all(np.isfinite(wf), axis=1)
+    for r in range(2):
+        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"m=2 rows16 k={k} n={n} row {r}")
+
+
 @pytest.mark.parametrize("k,n", [(4096, 14336), (4096, 16387), (14336, 4096), (4096, 40003), (1024, 33), (64, 70)])
-def test_two_activation_rows_stream(hip, k, n):
-    """M = 2 runs the streaming kernel with 16 (or, where the grid would fall
+def test_two_activation_rows_stream(hip, k, n, monkeypatch):
+    """M = 2 on the streaming kernel (its default from 32768 rows; forced here
+    with the matrix cores from m = 3) with 16 (or, where the grid would fall
     under 4 workgroups per CU, 8 or 4) weight rows per workgroup: C2's shapes,
     a partial last workgroup (n = 16387, 40003), short rows.  Edge data; every
     element within the rigorous bound, special classes and zero signs as the
     reference."""
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "3")
     x, w = case(2, k, n, seed=8100 + k + n, edge=True)
     p = hip.plan("rd", 2, k, n, x_addr=256, w_addr=256)  # device regions are 256-byte aligned
     assert p.slices > 0 and p.mt == 2, p
