@@ -1247,7 +1247,6 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
                          float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy) {
     static_assert(MB >= 1 && MB <= 4, "16 to 64 activation rows per workgroup");
     static_assert(NWV == 4 || NWV == 8, "32 weight rows per wave");
-    static_assert(!FUSE || MB == 1, "the in-kernel split serves 16-row activation tiles");
     constexpr int kRows = 32 * NWV;                  // weight rows per workgroup
     constexpr int kXItems = 128 * MB;                // x staging items (tile, k-block, operand lane)
     constexpr int kXPer = (kXItems + 64 * NWV - 1) / (64 * NWV);  // items per thread
@@ -3062,9 +3061,18 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             want = std::max<int64_t>(want, 1);
             mp.kchunks = (int)((nchunks + want - 1) / want);
             mp.kslices = (int)((nchunks + mp.kchunks - 1) / mp.kchunks);
-            // 16-row activation tiles split x in the kernel (no planes; C2 down
-            // at m = 16: the split launch cost 3-4 us of 37).
-            mp.xfuse = mp.mt == 16 && env_int("DMC_HIP_GEMM_FUSE", 1) != 0;
+            // Workgroups split their own chunks of x (no planes, no split
+            // launch) at 16-row tiles (C2 down at m = 16: the split launch cost
+            // 3-4 us of 37), and at 32 and 64 while the repeated split stays
+            // small: each of the gx column blocks splits all of x, so while gx
+            // * m <= 8192.  Same box, planes / fused, us: C2 down m = 32 / 64 /
+            // 128 / 256 / 512 41.0 / 56.6 / 79.3 / 125.7 / 235.8 against 35.5 /
+            // 50.7 / 75.1 / 120.1 / 218.7 (16 column blocks); up m = 32 / 64 /
+            // 128 37.9 / 55.4 / 80.0 against 36.2 / 51.1 / 79.4, but m = 256 /
+            // 512 122.2 / 230.8 against 126.0 / 248.0 (56 column blocks).
+            const int fenv = env_int("DMC_HIP_GEMM_FUSE", 1);  // 0: never; 2: always
+            const int64_t gx = (p.n + mp.rpw - 1) / mp.rpw;
+            mp.xfuse = fenv == 2 || (fenv == 1 && (mp.mt == 16 || gx * p.m <= 8192));
             const size_t planes = mp.xfuse ? 0 : ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
             mp.workspace_bytes = planes + (mp.kslices > 1 ? (size_t)mp.kslices * p.m * p.n * 4 : 0);
         } else if (mp.mkind == 6) {
@@ -3328,7 +3336,6 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             if ((needs_ws && !workspace) || (pl.mt != 16 && pl.mt != 32 && pl.mt != 64) || pl.kslices < 1 ||
                 pl.kslices > 65535 || (int64_t)pl.kslices * pl.kchunks < p.k / 64 || pl.rpw != 32 * pl.waves)
                 return hipErrorInvalidValue;
-            if (pl.xfuse && pl.mt != 16) return hipErrorInvalidValue;
             uint16_t *xs = pl.xfuse ? nullptr : static_cast<uint16_t *>(workspace);
             const size_t planes = pl.xfuse ? 0 : ((size_t)3 * p.m * p.k * 2 + 255) / 256 * 256;
             float *part = pl.kslices > 1 ? reinterpret_cast<float *>(static_cast<char *>(workspace) + planes) : nullptr;
@@ -3345,7 +3352,8 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
                            (int)pl.grid_y);                                                                   \
     else
             DMC_GEMM(1, true, 8) DMC_GEMM(1, false, 8) DMC_GEMM(2, false, 8) DMC_GEMM(4, false, 8)
-            DMC_GEMM(2, false, 4) DMC_GEMM(4, false, 4) return hipErrorInvalidValue;
+            DMC_GEMM(2, false, 4) DMC_GEMM(4, false, 4) DMC_GEMM(2, true, 8) DMC_GEMM(4, true, 8)
+            DMC_GEMM(2, true, 4) DMC_GEMM(4, true, 4) return hipErrorInvalidValue;
 #undef DMC_GEMM
             if (pl.kslices > 1)
                 hipLaunchKernelGGL(gemm_sum_slices_kernel, dim3(stride_grid((p.m * p.n + 255) / 256)), dim3(256), 0,

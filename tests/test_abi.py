@@ -244,17 +244,25 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert d.plan("rd", 16, 4096, 16384 + 16, x_addr=256, w_addr=256).slices == -8
     # the gemm layout splits k while the grid stays within one workgroup per
     # CU: C2 up at m = 64 has 56 tiles of 256 x 64, so 4 slices of 16 chunks;
-    # its workspace holds x's three bf16 planes and the 4 partial sums
+    # its 56 column blocks x 64 rows stay under 8192, so each workgroup
+    # splits its own x and the workspace holds only the 4 partial sums
     p = d.plan("rd", 64, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.grid_x) == (-8, 64, 56), p
-    assert p.workspace_bytes == 3 * 64 * 4096 * 2 + 4 * 64 * 14336 * 4, p
+    assert p.workspace_bytes == 4 * 64 * 14336 * 4, p
     # up at m = 192: 168 tiles would leave a lone round a third empty, so
-    # k splits to fill two rounds (3 slices)
+    # k splits to fill two rounds (3 slices); 56 x 192 > 8192, so x is split
+    # once, by a launch, into three bf16 planes in the workspace
     p = d.plan("rd", 192, 4096, 14336, x_addr=256, w_addr=256)
     assert p.workspace_bytes == 3 * 192 * 4096 * 2 + 3 * 192 * 14336 * 4, p
-    # down at m = 32: 16 tiles of 256 x 32, 16 slices of 14 chunks
+    monkeypatch.setenv("DMC_HIP_GEMM_FUSE", "2")   # always split in the kernel
+    assert d.plan("rd", 192, 4096, 14336, x_addr=256, w_addr=256).workspace_bytes == 3 * 192 * 14336 * 4
+    monkeypatch.setenv("DMC_HIP_GEMM_FUSE", "0")   # never (planes even at 16-row tiles)
+    assert d.plan("rd", 64, 4096, 14336, x_addr=256, w_addr=256).workspace_bytes == \
+        3 * 64 * 4096 * 2 + 4 * 64 * 14336 * 4
+    monkeypatch.delenv("DMC_HIP_GEMM_FUSE")
+    # down at m = 32: 32 tiles of 128 x 32 (4-wave workgroups), 16 slices of 14 chunks
     p = d.plan("rd", 32, 14336, 4096, x_addr=256, w_addr=256)
-    assert (p.mt, p.workspace_bytes) == (32, 3 * 32 * 14336 * 2 + 16 * 32 * 4096 * 4), p
+    assert (p.mt, p.waves, p.workspace_bytes) == (32, 4, 16 * 32 * 4096 * 4), p
     p = d.plan("rd", 512, 4096, 128256, x_addr=256, w_addr=256)   # 4008 tiles: no split
     assert p.workspace_bytes == 3 * 512 * 4096 * 2, p
     # x's three bf16 planes must stay inside one buffer range (6 m k < 2^31):

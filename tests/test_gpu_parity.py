@@ -1030,29 +1030,32 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
 
 # ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
 
+@pytest.mark.parametrize("fuse", [0, 2])
 @pytest.mark.parametrize("m,k,n", [(9, 512, 300), (16, 4096, 1000), (13, 64, 17),
                                    (17, 4096, 1000), (32, 64, 300), (33, 576, 257), (64, 4096, 513),
                                    (65, 1024, 700), (100, 14336, 260), (128, 4096, 4096), (200, 128, 17),
                                    (130, 1024, 600)])
-def test_prefill_gemm_within_bound(hip, m, k, n, monkeypatch):
-    """M > 16 runs the gemm layout by default, and M = 9..16 where the wide
-    layout does not fill the device: 16, 32 or 64 activation rows per
-    workgroup, partial activation tiles (m = 9, 13, 17, 33, 65, 100, 130, 200), partial
-    256-row weight blocks, K from one chunk to 224; edge data (subnormals,
+def test_prefill_gemm_within_bound(hip, m, k, n, fuse, monkeypatch):
+    """The gemm layout (the default from 17 rows on larger matrices, and at
+    9..16 above 128 MiB): 16, 32 or 64 activation rows per workgroup, partial
+    activation tiles (m = 9, 13, 17, 33, 65, 100, 130, 200), partial weight
+    blocks, K from one chunk to 224, x split into planes by a launch
+    (DMC_HIP_GEMM_FUSE=0) or by each workgroup (=2); edge data (subnormals,
     +-0, +-1e-38, inf/NaN weights).  Every element within the rigorous bound,
     non-finite classes and exact zeros as the reference."""
     x, w = case(m, k, n, seed=9000 + m + k + n, edge=True)
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")  # small matrices run rows16 by default
+    monkeypatch.setenv("DMC_HIP_GEMM_FUSE", str(fuse))
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
     assert (p.slices, p.mt) == (-8, 16 if m <= 16 else 32 if m <= 32 else 64), p
     y = run_rd(hip, x, w)
     rows = np.unique(np.r_[0, n - 1, np.random.default_rng(m).integers(0, n, 160)])
     y_ref = oracle.matmul_bf16_t(x, w[rows])
-    check(y[:, rows], y_ref, what=f"gemm m={m} k={k} n={n}")
+    check(y[:, rows], y_ref, what=f"gemm fuse={fuse} m={m} k={k} n={n}")
     wf = W.bf16_to_f32(w[rows])
     fin = np.all(np.isfinite(wf), axis=1)
     for r in range(0, m, 7):
-        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm m={m} k={k} n={n} row {r}")
+        check_bound(y[r, rows[fin]], y_ref[r, fin], x[r], wf[fin], what=f"gemm fuse={fuse} m={m} k={k} n={n} row {r}")
 
 
 @pytest.mark.parametrize("waves,m,k,n", [(4, 17, 4096, 1000), (4, 33, 576, 257), (4, 64, 4096, 513),
@@ -1102,13 +1105,17 @@ def test_gemm_fused_single_slice_needs_no_workspace(hip, m, k, n, monkeypatch):
         check(dy.download(np.float32, (m, n)), y_ref, what=f"gemm fused unsplit device m={m} k={k} n={n}")
 
 
+@pytest.mark.parametrize("fuse", [0, 2])
 @pytest.mark.parametrize("m,k,n", [(17, 4096, 1000), (64, 576, 513), (100, 1024, 260)])
-def test_prefill_gemm_unsplit(hip, m, k, n, monkeypatch):
+def test_prefill_gemm_unsplit(hip, m, k, n, fuse, monkeypatch):
     """The gemm layout with k in one slice (DMC_HIP_GEMM_MAX_SLICES=1: what it
     runs when the tiles alone fill the device, as on the LM head), where the
-    zero rule runs inside the kernel: edge data, an all-zero weight row, and
-    rows whose underflowing products end at -0.0 and +0.0."""
+    zero rule runs inside the kernel, with x split into planes by a launch
+    (DMC_HIP_GEMM_FUSE=0) or by each workgroup (=2: no workspace at all):
+    edge data, an all-zero weight row, and rows whose underflowing products
+    end at -0.0 and +0.0."""
     monkeypatch.setenv("DMC_HIP_GEMM_MAX_SLICES", "1")
+    monkeypatch.setenv("DMC_HIP_GEMM_FUSE", str(fuse))
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "8")  # small matrices run rows16 by default
     x, w = case(m, k, n, seed=9500 + m + k + n, edge=True)
     w[3] = 0
@@ -1116,9 +1123,9 @@ def test_prefill_gemm_unsplit(hip, m, k, n, monkeypatch):
     w[6] = 0x8001
     x[1] = np.float32(-1e-38)
     p = hip.plan("rd", m, k, n, x_addr=x.ctypes.data, w_addr=w.ctypes.data)
-    assert p.slices == -8 and p.workspace_bytes == 3 * m * k * 2, p
+    assert p.slices == -8 and p.workspace_bytes == (0 if fuse else 3 * m * k * 2), p
     y = run_rd(hip, x, w)
     y_ref = ref(x, w)
-    check(y, y_ref, what=f"gemm unsplit m={m} k={k} n={n}")
+    check(y, y_ref, what=f"gemm unsplit fuse={fuse} m={m} k={k} n={n}")
     assert np.signbit(y_ref[1, 5]) and np.signbit(y[1, 5]) and y[1, 5] == 0
     assert not np.signbit(y[1, 6]) and y[1, 6] == 0
