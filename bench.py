@@ -435,6 +435,26 @@ def extended(d, W, reps: int) -> dict:
             f(0)
             record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
             s.free()
+    # Batched per-head projections, one launch over every head: the
+    # reference's [B,1,S,K] @ [H,K,N] collapse (jit.rs:19914-19933) on device
+    # regions, W [H,K,N] bf16.  q heads with one broadcast x (ls = 0), k/v
+    # heads, and per-head inputs (ls = K); enough rotating copies that the
+    # weights exceed the 256 MB cache.
+    rng = np.random.default_rng(7)
+    for label, heads, k, n, ls in (("batched q heads [32,4096,128]", 32, 4096, 128, 0),
+                                   ("batched kv heads [8,4096,128]", 8, 4096, 128, 0),
+                                   ("batched per-head x [32,128,4096]", 32, 128, 4096, 128)):
+        wb = W_bf16(rng, heads * k, n)
+        xb = rng.standard_normal(heads * k if ls else k).astype(np.float32)
+        copies = max(3, -(-300_000_000 // wb.nbytes))
+        s = Rotating(d, wb, xb, copies, n_out=heads * n)
+        f = lambda i: d.gemv_cs(s.x, s.w[i % copies], s.y, 1, k, n, heads, ls, k * n)  # noqa: E731
+        f(0)
+        us = batch_us(d, f, 20)
+        gbs = (wb.nbytes + xb.nbytes + 4 * heads * n) / (us * 1e-6) / 1e9
+        out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+        log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
+        s.free()
     # C2's shapes at a few activation rows (MFMA kernels)
     for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
         n, k = w.shape

@@ -1982,17 +1982,29 @@ gemv_cs_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restri
 // the next row's first elements and are never stored.
 constexpr int kCsCols = 512;
 
-template <int NW, int MT, bool UN>
+//
+// G > 1 (narrow N, e.g. per-head projections with N = 64..256): the wave's
+// lanes form G row groups of 64/G lanes; group g walks rows r0 + g, r0 + g +
+// G, ... of the wave's range over 512/G columns, so one load instruction still
+// covers 1 KiB (G rows of 1024/G bytes) where at G = 1 most lanes would sit
+// past N.  x is then per lane (its row's value), loaded with the weights.  The
+// groups' folded partials meet in LDS with the waves', in a fixed order.
+template <int NW, int MT, bool UN, int G>
 __global__ void __launch_bounds__(64 * NW)
 gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *__restrict__ X, int64_t ls,
                       float *__restrict__ Y, float *__restrict__ P, int64_t z_stride, int64_t p_slice, int N,
                       int K, int M, int kslice, int slices) {
+    static_assert(G == 1 || G == 2 || G == 4 || G == 8, "row groups per wave");
+    static_assert(G == 1 || !UN, "row groups serve aligned rows");
+    constexpr int CB = kCsCols / G;  // columns per workgroup
+    constexpr int CL = 64 / G;       // lanes per row group
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = lane / CL;        // this lane's row group
     const int cb = blockIdx.x;
     const int s = blockIdx.y;
     const int64_t z = blockIdx.z;
-    const int col = cb * kCsCols + lane * 8;
+    const int col = cb * CB + (lane % CL) * 8;
     const bool live = col < N;
 
     const int kb = s * kslice;
@@ -2007,11 +2019,11 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     const uint32_t range = (uint32_t)((int64_t)(r1 - r0) * N * 2) + (UN ? (delta + 2 + 3) & ~3u : 0);
     const __amdgpu_buffer_rsrc_t rsw = weight_rsrc(reinterpret_cast<const char *>(w0) - delta, range);
     const uint32_t row_bytes = (uint32_t)N * 2;
-    const uint32_t lane_off = delta + (uint32_t)col * 2;
+    const uint32_t lane_off = delta + (uint32_t)col * 2 + (uint32_t)rg * row_bytes;
 
     // +0.0f when this lane sums at least one product (or K == 0, which must
     // write +0.0f), -0.0f, the additive identity, otherwise.
-    const float init = ((r0 < r1 && live) || K == 0) ? 0.0f : -0.0f;
+    const float init = ((r0 + rg < r1 && live) || K == 0) ? 0.0f : -0.0f;
     float acc[MT][8];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
@@ -2021,10 +2033,11 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     // nz: the bf16 halves of the lane's columns that met a nonzero weight
     // where x is nonzero (any product with two nonzero factors; zero_fold).
     uint32_t nz[MT][4] = {};
-    auto consume = [&](const u32x4 &wv, int k) {
+    // xg: at G > 1 the lane's own x values, loaded with its rows' weights.
+    auto consume = [&](const u32x4 &wv, int k, const float *xg) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-            const float xv = xz[(int64_t)min(m, M - 1) * K + k];
+            const float xv = G == 1 ? xz[(int64_t)min(m, M - 1) * K + k] : xg[m];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const uint32_t d = wv[e >> 1];
@@ -2043,52 +2056,64 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     // buffer it sums; the row guard sits on the arithmetic, which also keeps
     // x[k] in range.
     constexpr int U = MT <= 2 ? 8 : 4;
+    constexpr int XU = G == 1 ? 1 : U;  // per-lane x registers (G > 1)
     const uint32_t loff = live ? lane_off : kOutOfRange;
     u32x4 ba[U], bb[U];
-    auto load = [&](u32x4 (&b)[U], int r) {
+    float xa[XU][MT], xb[XU][MT];
+    // Buffer u holds row r + u*G + rg of each lane.
+    auto load = [&](u32x4 (&b)[U], float (&xv)[XU][MT], int r) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) b[u] = load_w16(rsw, loff, (uint32_t)(r - r0 + u) * row_bytes);
+        for (int u = 0; u < U; ++u) b[u] = load_w16(rsw, loff, (uint32_t)(r - r0 + u * G) * row_bytes);
+        if constexpr (G > 1) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = r + u * G + rg;
+#pragma unroll
+                for (int m = 0; m < MT; ++m) xv[u][m] = k < r1 ? xz[(int64_t)min(m, M - 1) * K + k] : 0.0f;
+            }
+        }
     };
-    auto sum_rows = [&](const u32x4 (&b)[U], int r) {
-        if (r + U <= r1) {
+    auto sum_rows = [&](const u32x4 (&b)[U], const float (&xv)[XU][MT], int r) {
+        if (r + U * G <= r1) {
 #pragma unroll
-            for (int u = 0; u < U; ++u) consume(b[u], r + u);
+            for (int u = 0; u < U; ++u) consume(b[u], r + u * G + rg, xv[G == 1 ? 0 : u]);
         } else {
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                if (r + u < r1) consume(b[u], r + u);
+                if (r + u * G + rg < r1) consume(b[u], r + u * G + rg, xv[G == 1 ? 0 : u]);
         }
     };
-    load(ba, r0);
-    for (int r = r0; r < r1; r += 2 * U) {
-        load(bb, r + U);
-        sum_rows(ba, r);
-        if (r + U >= r1) break;
-        load(ba, r + 2 * U);
-        sum_rows(bb, r + U);
+    load(ba, xa, r0);
+    for (int r = r0; r < r1; r += 2 * U * G) {
+        load(bb, xb, r + U * G);
+        sum_rows(ba, xa, r);
+        if (r + U * G >= r1) break;
+        load(ba, xa, r + 2 * U * G);
+        sum_rows(bb, xb, r + U * G);
     }
 
-    __shared__ float red[NW][MT][kCsCols];
+    __shared__ float red[NW * G][MT][CB];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-            red[wave][m][lane * 8 + e] = zero_fold(acc[m][e], ((nz[m][e >> 1] >> (16 * (e & 1))) & 0x7fffu) != 0);
+            red[wave * G + rg][m][(lane % CL) * 8 + e] =
+                zero_fold(acc[m][e], ((nz[m][e >> 1] >> (16 * (e & 1))) & 0x7fffu) != 0);
     __syncthreads();
 
-    const int c0 = cb * kCsCols;
-    const int ncol = min(kCsCols, N - c0);
+    const int c0 = cb * CB;
+    const int ncol = min(CB, N - c0);
     // With one k slice (and every row in it) the workgroup writes y and the
     // zero rule applies here; otherwise the folded partial goes to P and
     // sum_slices_stream_kernel applies it.
     const bool final_out = slices == 1 && !UN;
     float *out = final_out ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
-    for (int t = threadIdx.x; t < MT * kCsCols; t += 64 * NW) {
-        const int m = t / kCsCols, c = t - m * kCsCols;
+    for (int t = threadIdx.x; t < MT * CB; t += 64 * NW) {
+        const int m = t / CB, c = t - m * CB;
         const bool store = m < M && c < ncol;
         float v = red[0][m][c];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) v += red[w][m][c];
+        for (int w = 1; w < NW * G; ++w) v += red[w][m][c];
         if (final_out)
             v = zero_unfold(v, store, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? c0 + c : 0), N, K);
         if (store) out[(int64_t)m * N + c0 + c] = v;
@@ -2797,36 +2822,43 @@ hipError_t cs_mt(const CsProblem &p, const CsPlan &pl, float *P, int64_t ps, int
     return hipErrorInvalidValue;
 }
 
-template <int NW, int MT>
+template <int NW, int MT, int G>
 hipError_t css_go(const CsProblem &p, const CsPlan &pl, float *P, int64_t z0, int64_t nz, int64_t m0,
                   int64_t mc, hipStream_t s) {
     const int64_t zs = p.m * p.n;
     const dim3 grid((unsigned)pl.grid_x, (unsigned)pl.slices, (unsigned)nz);
-    if (pl.unaligned)
-        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, true>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs, p.rs,
-                           p.x + z0 * p.ls + m0 * p.k, p.ls, p.y + z0 * zs + m0 * p.n, P + z0 * zs + m0 * p.n, zs,
-                           p.batch * zs, (int)p.n, (int)p.k, (int)mc, (int)pl.kslice, (int)pl.slices);
-    else
-        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, false>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs,
+    if (pl.cb != kCsCols / G || pl.grid_x * pl.cb < p.n) return hipErrorInvalidValue;
+    if (pl.unaligned) {
+        if (G != 1) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, true, 1>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs,
+                           p.rs, p.x + z0 * p.ls + m0 * p.k, p.ls, p.y + z0 * zs + m0 * p.n, P + z0 * zs + m0 * p.n,
+                           zs, p.batch * zs, (int)p.n, (int)p.k, (int)mc, (int)pl.kslice, (int)pl.slices);
+    } else {
+        hipLaunchKernelGGL((gemv_cs_stream_kernel<NW, MT, false, G>), grid, dim3(64 * NW), 0, s, p.w + z0 * p.rs,
                            p.rs, p.x + z0 * p.ls + m0 * p.k, p.ls, p.y + z0 * zs + m0 * p.n,
                            P ? P + z0 * zs + m0 * p.n : nullptr, zs, p.batch * zs, (int)p.n, (int)p.k, (int)mc,
                            (int)pl.kslice, (int)pl.slices);
+    }
     return hipGetLastError();
 }
 
 hipError_t css_dispatch(const CsProblem &p, const CsPlan &pl, float *P, int64_t z0, int64_t nz, int64_t m0,
                         int64_t mc, hipStream_t s) {
-#define DMC_CSS(NW)                                                 \
-    switch (pl.mt) {                                                \
-    case 1: return css_go<NW, 1>(p, pl, P, z0, nz, m0, mc, s);      \
-    case 2: return css_go<NW, 2>(p, pl, P, z0, nz, m0, mc, s);      \
-    case 4: return css_go<NW, 4>(p, pl, P, z0, nz, m0, mc, s);      \
-    }                                                               \
+#define DMC_CSS(NW, G)                                                 \
+    switch (pl.mt) {                                                   \
+    case 1: return css_go<NW, 1, G>(p, pl, P, z0, nz, m0, mc, s);      \
+    case 2: return css_go<NW, 2, G>(p, pl, P, z0, nz, m0, mc, s);      \
+    case 4: return css_go<NW, 4, G>(p, pl, P, z0, nz, m0, mc, s);      \
+    }                                                                  \
     return hipErrorInvalidValue;
+    if (pl.waves == 4 && pl.rw == 2) { DMC_CSS(4, 2) }
+    if (pl.waves == 4 && pl.rw == 4) { DMC_CSS(4, 4) }
+    if (pl.waves == 4 && pl.rw == 8) { DMC_CSS(4, 8) }
+    if (pl.rw > 1) return hipErrorInvalidValue;
     switch (pl.waves) {
-    case 2: DMC_CSS(2)
-    case 4: DMC_CSS(4)
-    case 8: DMC_CSS(8)
+    case 2: DMC_CSS(2, 1)
+    case 4: DMC_CSS(4, 1)
+    case 8: DMC_CSS(8, 1)
     }
 #undef DMC_CSS
     return hipErrorInvalidValue;
@@ -3235,8 +3267,21 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         pl.waves = nw;
         pl.rw = 0;
         pl.mt = std::min(mt_for(p.m), 4);
-        pl.cb = kCsCols;
-        pl.grid_x = (p.n + kCsCols - 1) / kCsCols;
+        // Row groups per wave: 512/G columns per workgroup, as few as still
+        // cover N (N = 128: 4 groups of 16 lanes), on aligned rows with 4
+        // waves.  Batched per-head W [32,4096,128], one broadcast x: 12.5 us
+        // with one group (three quarters of the lanes past N).
+        int g = 1;
+        if (!un && nw == 4) {
+            const int genv = env_int("DMC_HIP_CS_ROW_GROUPS", 0);
+            if (genv == 1 || genv == 2 || genv == 4 || genv == 8)
+                g = genv;
+            else
+                while (g < 8 && (int64_t)(kCsCols / (2 * g)) >= p.n) g *= 2;
+        }
+        pl.rw = g > 1 ? g : 0;  // 0: one group (the plan's long-standing value)
+        pl.cb = kCsCols / g;
+        pl.grid_x = (p.n + pl.cb - 1) / pl.cb;
         // Split k so the launch has ~4 workgroups per CU; 2 with at most 16
         // column blocks, 3 with at most 24 (env-tunable); each wave with at
         // least 8 rows.  Measured with one activation row (shapes as the
@@ -3259,7 +3304,7 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         // A wave's rows, plus the 16 rows its last loads run past them, must
         // fit a 31-bit buffer offset; the grid's y extent is limited to 65535.
         const int64_t per_wave = (kslice + nw - 1) / nw;
-        if (pl.slices <= 65535 && (per_wave + 16) * p.n * 2 <= INT32_MAX) {
+        if (pl.slices <= 65535 && (per_wave + 16 * g) * p.n * 2 <= INT32_MAX) {
             pl.workspace_bytes = pl.slices > 1 || un ? (size_t)pl.slices * batch * p.m * p.n * 4 : 0;
             return pl;
         }

@@ -93,7 +93,7 @@ struct RdPlan {
 // the slice partials in slice order.
 struct CsPlan {
     int vec;        // bf16 columns per lane per load
-    int rw;         // k-rows covered by one wave-wide load
+    int rw;         // k-rows covered by one wave-wide load (streaming kernel: its row groups, 0 for one)
     int mt;         // activation rows per workgroup
     int cb;         // output columns per workgroup
     int waves;      // waves per workgroup

@@ -327,6 +327,52 @@ def test_column_stream_batched_slices_at_odd_strides(hip):
     check(y, oracle.matmul_bf16_batched(x, w, k, n, batch, ls, rs), what="cs batched odd strides")
 
 
+@pytest.mark.parametrize("k,n,batch,per_head,m,groups", [
+    (4096, 128, 32, False, 1, 0), (4096, 64, 8, True, 1, 0), (300, 256, 3, True, 3, 0),
+    (1001, 136, 4, False, 2, 0), (2048, 1024, 2, True, 1, 8), (7, 128, 5, True, 1, 0), (4096, 8, 16, False, 1, 0)])
+def test_column_stream_row_groups(hip, k, n, batch, per_head, m, groups, monkeypatch):
+    """Batched column-stream calls on narrow N (per-head projections): the
+    streaming kernel's wave splits into G row groups of 64/G lanes over
+    512/G columns (N = 8, 64 -> G = 8, 128 -> 4, 136 and 256 -> 2), with one
+    broadcast x (ls = 0) or one per head, 1..3 activation rows, k shorter
+    than one group step, and G = 8 forced on N = 1024 (16 column blocks).
+    Edge data, and planted columns whose products all underflow (signs from
+    the chain) or are exact zeros; sampled against the oracle within the
+    norm and the elementwise bound, zeros bitwise."""
+    if groups:
+        monkeypatch.setenv("DMC_HIP_CS_ROW_GROUPS", str(groups))
+    rng = np.random.default_rng(k * 7 + n + batch)
+    x = rng.standard_normal((batch if per_head else 1, m, k)).astype(np.float32)
+    w = W.bf16_rne(rng.standard_normal((batch, k, n), dtype=np.float32))
+    flat = w.reshape(-1)
+    pos = rng.integers(0, flat.size, size=max(1, flat.size // 500))
+    flat[pos] = (rng.integers(0, 2, size=pos.size, dtype=np.uint16) << 15) | rng.integers(1, 128, size=pos.size, dtype=np.uint16)
+    x[0, 0, :] = np.float32(-1e-38)          # head 0, row 0: tiny x ...
+    w[0, :, 0] = 0x0001                      # ... against tiny weights: -0.0
+    w[0, :, 1] = 0x8001                      # +0.0
+    w[0, :, 2] = 0                           # exact zeros: +0.0
+    ls = m * k if per_head else 0
+    want_g = groups or next(g for g in (8, 4, 2, 1) if 512 // g >= n)
+    p = hip.plan("cs", m, k, n, batch=batch, rs=k * n, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.grid_x) == (want_g if want_g > 1 else 0, -(-n // (512 // want_g))), p
+    with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * batch * m * n) as dy:
+        hip.gemv_cs(dx, dw, dy, m, k, n, batch, ls, k * n)
+        hip.synchronize()
+        y = dy.download(np.float32, (batch, m, n))
+    heads = np.unique(np.r_[0, batch - 1, rng.integers(0, batch, 3)])
+    for z in heads:
+        xz = x[z if per_head else 0]
+        y_ref = oracle.matmul_bf16_t(xz, np.ascontiguousarray(w[z].T))
+        check(y[z], y_ref, what=f"cs row groups head {z} k={k} n={n} m={m}")
+        wf = W.bf16_to_f32(np.ascontiguousarray(w[z].T))
+        fin = np.all(np.isfinite(wf), axis=1)
+        for r in range(m):
+            check_bound(y[z, r, fin], y_ref[r, fin], xz[r], wf[fin], what=f"cs row groups head {z} row {r}")
+        if z == 0:
+            assert np.array_equal(y[0, 0, :3].view(np.uint32), y_ref[0, :3].view(np.uint32)), (y[0, 0, :3], y_ref[0, :3])
+
+
 def zero_rows(k, n=8):
     """Activation rows x [4, k] and weight rows w [n, k] (bf16 bits) whose
     products are all exact zeros or underflow -- so every device sum is
