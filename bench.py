@@ -628,6 +628,26 @@ def dropin(d, W, reps: int) -> dict:
         out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         log(f"{label}: {us:.2f} us/call  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%} (PCIe-inclusive)")
         assert np.all(np.isfinite(y)), label
+    # The reference's deferred protocol (gpu.rs:439-474), as its JIT issues
+    # consecutive GEMVs: eight deferred x @ W calls, then one flush that waits
+    # once and copies the eight y's out.  Host wall time per call.
+    dfr, flush = lib.dmc_matmul_bf16_gpu_batched_deferred, lib.dmc_matmul_bf16_gpu_flush
+    wts = [np.ascontiguousarray(w.T) for w in mats]
+    ptrs = [w.ctypes.data for w in wts]
+    ys = [np.empty(n, np.float32) for _ in range(8)]
+    groups = max(1, reps // 8)
+    for g in range(groups + 1):  # the first group untimed
+        if g == 1:
+            t0 = time.perf_counter()
+        for j in range(8):
+            dfr(x.ctypes.data, ptrs[(8 * g + j) % 3], ys[j].ctypes.data, 1, k, n, 1, 0, 0)
+        flush()
+    us = (time.perf_counter() - t0) / (8 * groups) * 1e6
+    gbs = b_alg(n, k) / (us * 1e-6) / 1e9
+    label = "drop-in cs x@W deferred x8 + flush"
+    out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    log(f"{label}: {us:.2f} us/call  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%} (PCIe-inclusive)")
+    assert all(np.all(np.isfinite(v)) for v in ys), label
     d.release_weights()
     return out
 
