@@ -392,7 +392,8 @@ class Event:
 @dataclass
 class Plan:
     vec: int
-    rows_or_rw: int
+    rows_or_rw: int        # rd: weight rows per register buffer; cs: the general kernel's k rows
+                           # per wave-wide load (> 0), or the streaming kernel's -row groups (<= 0)
     mt: int
     grid_x: int
     slices: int            # cs: k slices; rd: 8-element k vectors per lane (0 = general kernel)

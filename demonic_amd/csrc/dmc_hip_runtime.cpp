@@ -1354,8 +1354,8 @@ int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t 
         dmc::CsProblem p{reinterpret_cast<const uint16_t *>(w_addr), reinterpret_cast<const float *>(x_addr),
                          nullptr, m, k, n, batch, 0, rs};
         const dmc::CsPlan pl = dmc::plan_cs(p, cus);
-        const int64_t v[8] = {pl.vec, pl.rw, pl.mt, pl.grid_x, pl.slices, (int64_t)pl.workspace_bytes,
-                              pl.waves, pl.stream ? pl.kslice : pl.cb};
+        const int64_t v[8] = {pl.vec, pl.stream ? -(int64_t)pl.rw : pl.rw, pl.mt, pl.grid_x, pl.slices,
+                              (int64_t)pl.workspace_bytes, pl.waves, pl.stream ? pl.kslice : pl.cb};
         memcpy(out8, v, sizeof v);
     }
     return DMC_HIP_OK;

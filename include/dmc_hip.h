@@ -232,10 +232,11 @@ int32_t dmc_hip_gemv_rd_grouped(int64_t count, const int64_t *x_devs, const int6
  * (wide: 256 rows per workgroup; rows16: 16 rows per block; gemm: 256 rows
  * against 16, 32 or 64 activation rows, k possibly split; mt activation rows);
  * waves and rows_per_group (weight rows per workgroup) describe the workgroup.
- * Column-stream layout: `vec` is the row alignment as above; rows_or_rw 0 is
- * the streaming kernel (512 columns per workgroup, rows_per_group k rows per
- * slice; with vec < 8 it reads misaligned rows and the slice pass applies the
- * last k row), > 0 the general kernel's k rows per wave-wide load
+ * Column-stream layout: `vec` is the row alignment as above; rows_or_rw <= 0 is
+ * the streaming kernel (512 columns per workgroup, or with -G row groups per
+ * wave 512/G, rows_per_group k rows per slice; with vec < 8 it reads
+ * misaligned rows and the slice pass applies the last k row), > 0 the
+ * general kernel's k rows per wave-wide load
  * (rows_per_group columns per workgroup); `slices` k slices, summed by a
  * second launch into `workspace_bytes` of partials. */
 int32_t dmc_hip_plan(int32_t layout_rd, int64_t x_addr, int64_t w_addr, int64_t m, int64_t k,

@@ -392,6 +392,25 @@ def test_column_stream_plans_split_k_and_size_workspace():
     assert zero_k.slices == 1
 
 
+def test_column_stream_row_groups_for_narrow_n(monkeypatch):
+    """Narrow N on the streaming kernel (batched per-head projections): G row
+    groups per wave over 512/G columns, the fewest groups whose columns cover
+    N, reported as rows_or_rw = -G (0 for one group; > 0 is the general
+    kernel); 4 waves only, aligned rows."""
+    for n, g in ((8, 8), (64, 8), (72, 4), (128, 4), (136, 2), (256, 2), (264, 0), (512, 0), (4096, 0)):
+        p = d.plan("cs", 1, 4096, n, batch=32, rs=4096 * n, x_addr=256, w_addr=256)
+        assert (p.vec, p.waves, p.rows_or_rw, p.grid_x) == (8, 4, -g, -(-n // (512 // max(g, 1)))), (n, p)
+        assert p.workspace_bytes == (p.slices * 32 * n * 4 if p.slices > 1 else 0), (n, p)
+    monkeypatch.setenv("DMC_HIP_CS_WAVES", "8")        # row groups only at 4 waves
+    assert d.plan("cs", 1, 4096, 128, batch=32, rs=4096 * 128, x_addr=256, w_addr=256).rows_or_rw == 0
+    monkeypatch.delenv("DMC_HIP_CS_WAVES")
+    monkeypatch.setenv("DMC_HIP_CS_ROW_GROUPS", "8")   # forced on a wide N: 64 columns per workgroup
+    p = d.plan("cs", 1, 2048, 1024, batch=2, rs=2048 * 1024, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.grid_x) == (-8, 16), p
+    p = d.plan("cs", 1, 4096, 4097, x_addr=256, w_addr=256)  # odd N: misaligned rows, one group
+    assert (p.vec, p.rows_or_rw) == (1, 0), p
+
+
 # ---- errors without a device ------------------------------------------------------------------
 
 def test_int_entries_reject_bad_shapes_before_touching_a_device():

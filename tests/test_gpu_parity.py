@@ -354,7 +354,7 @@ def test_column_stream_row_groups(hip, k, n, batch, per_head, m, groups, monkeyp
     ls = m * k if per_head else 0
     want_g = groups or next(g for g in (8, 4, 2, 1) if 512 // g >= n)
     p = hip.plan("cs", m, k, n, batch=batch, rs=k * n, x_addr=256, w_addr=256)
-    assert (p.rows_or_rw, p.grid_x) == (want_g if want_g > 1 else 0, -(-n // (512 // want_g))), p
+    assert (p.rows_or_rw, p.grid_x) == (-want_g if want_g > 1 else 0, -(-n // (512 // want_g))), p
     with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
             hip.DeviceBuffer(4 * batch * m * n) as dy:
         hip.gemv_cs(dx, dw, dy, m, k, n, batch, ls, k * n)
