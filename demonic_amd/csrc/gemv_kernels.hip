@@ -1026,6 +1026,24 @@ __device__ float reference_chain(const uint16_t *__restrict__ w, const float *__
     return acc;
 }
 
+// Tiny activation rows.  split3 is exact for |x| >= 2^-110: below that the
+// third term falls under bf16's least subnormal (2^-133) and x loses its low
+// bits.  That matters only when a whole activation row is that small -- then
+// every product loses up to 2^-133 / |x| of itself (a row of |x| ~ 1e-37
+// would be off by ~2^-10) -- while in a row with larger entries the lost
+// bits are below 2^-33 of the largest one.  So each MFMA kernel keeps, per
+// lane, the largest bf16 magnitude of the hi terms it split (hi keeps the
+// order of |x| against 2^-100, and is nonzero for every nonzero x), takes
+// the maximum per activation row over its workgroup's k range, and gives a
+// row whose maximum is nonzero but below 2^-100 (bf16 0x0d80) the reference
+// chain over that k range instead of its MFMA sums: bit for bit the
+// reference's value when k is not split, else the slice's part of it.  Rare
+// path: no real activation row is this small.
+constexpr uint32_t kTinyHiBits = 0x0d80u;
+
+__device__ __forceinline__ uint32_t hi_max(uint32_t mx) { return max(mx & 0xffffu, mx >> 16); }
+__device__ __forceinline__ bool tiny_row(uint32_t mx) { return mx != 0 && mx < kTinyHiBits; }
+
 // Wave-uniform: does the row hold an element other than +-0?  (bytes: 16 * n16)
 __device__ bool wave_row_nonzero(const void *row, int n16, uint32_t mask) {
     const u32x4 *p = reinterpret_cast<const u32x4 *>(row);
@@ -1119,7 +1137,9 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 
     __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 36 KiB
     __shared__ u32x4 xpl[2][2][3][64];                                           // 2 x 6 KiB
+    __shared__ uint32_t xmax_s[16];  // per activation row: the largest hi-term magnitude (tiny rows)
     uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
+    if (tid < 16) xmax_s[tid] = 0;
 
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
     // Staging: load j (0..3) covers the wave's rows 8j + lane/8, bytes 16*(lane%8) of the chunk.
@@ -1152,12 +1172,15 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
             for (int e = 0; e < 8; ++e) r.x[e] = 0.0f;
         }
     };
+    uint32_t xmx = 0;
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
         if (xthread) {
             u32x4 hi, md, lo;
             split8(r.x, hi, md, lo);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xmx = max_mag(xmx, hi[v]);
             xpl[xbuf][tid >> 6][0][lane] = hi;
             xpl[xbuf][tid >> 6][1][lane] = md;
             xpl[xbuf][tid >> 6][2][lane] = lo;
@@ -1211,12 +1234,24 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
         step(c + 1, ra, rb);
     }
 
+    if (xthread) atomicMax(&xmax_s[lane & 15], hi_max(xmx));
+    __syncthreads();
     const int base[2] = {wave * 32, wave * 32 + 16};
     bool live[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) live[t][r] = m0 + i16 < M && base[t] + g * 4 + r < nrows;
+    const bool tiny = m0 + i16 < M && tiny_row(xmax_s[i16]);
+    if (__builtin_amdgcn_ballot_w64(tiny) != 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (tiny && live[t][r])
+                    acc[t][r] = reference_chain(W + (int64_t)(row0 + base[t] + g * 4 + r) * K,
+                                                X + (int64_t)(m0 + i16) * K, K);
+    }
     settle_zeros(acc, live, base, W + (int64_t)row0 * K, X + (int64_t)m0 * K, K, i16);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -1279,7 +1314,9 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
 
     __shared__ __attribute__((aligned(16))) uint8_t wt[kRows * kWidePitch];  // 36 KiB at 8 waves
     __shared__ u32x4 xpl[2][MB][2][3][64];                                   // MB x 12 KiB
+    __shared__ uint32_t xmax_s[16 * MB];  // per activation row: the largest hi-term magnitude (tiny rows)
     uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
+    if (tid < 16 * MB) xmax_s[tid] = 0;
 
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)row0 * K, (uint32_t)((int64_t)nrows * K * 2));
     // Staging: load j (0..3) covers the wave's rows 8j + lane/8, bytes 16*(lane%8) of the chunk.
@@ -1332,6 +1369,9 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
             }
         }
     };
+    uint32_t xmx[kXPer];
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j) xmx[j] = 0;
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
@@ -1345,10 +1385,14 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
                                     __uint_as_float(r.x[j][1][2]), __uint_as_float(r.x[j][1][3])};
                 u32x4 hi, md, lo;
                 split8(v, hi, md, lo);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xmx[j] = max_mag(xmx[j], hi[e]);
                 xpl[xbuf][xt[j]][xb[j]][0][lane] = hi;
                 xpl[xbuf][xt[j]][xb[j]][1][lane] = md;
                 xpl[xbuf][xt[j]][xb[j]][2][lane] = lo;
             } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xmx[j] = max_mag(xmx[j], r.x[j][0][e]);
 #pragma unroll
                 for (int q = 0; q < 3; ++q) xpl[xbuf][xt[j]][xb[j]][q][lane] = r.x[j][q];
             }
@@ -1463,6 +1507,10 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
         }
     }
 
+#pragma unroll
+    for (int j = 0; j < kXPer; ++j)
+        if (xthread[j]) atomicMax(&xmax_s[xt[j] * 16 + (lane & 15)], hi_max(xmx[j]));
+    __syncthreads();
     const int base[2] = {wave * 32, wave * 32 + 16};
 #pragma unroll
     for (int mt = 0; mt < MB; ++mt) {
@@ -1472,6 +1520,16 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) live[t][rr] = m < M && base[t] + g * 4 + rr < nrows;
+        const bool tiny = m < M && tiny_row(xmax_s[mt * 16 + i16]);
+        if (__builtin_amdgcn_ballot_w64(tiny) != 0) {  // this slice's chain (all of k without slices)
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr)
+                    if (tiny && live[t][rr])
+                        acc[mt][t][rr] = reference_chain(W + (int64_t)(row0 + base[t] + g * 4 + rr) * K + 64 * c0,
+                                                         X + (int64_t)m * K + 64 * c0, 64 * nchunks);
+        }
         if (P) {  // a k slice: the partial sums, for gemm_sum_slices_kernel
             float *ps = P + (int64_t)bz * M * N + (int64_t)m * N + row0;
 #pragma unroll
@@ -1580,9 +1638,11 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     constexpr int kStreamBytes = 8 * (kTileBytes + kXBytes);
     constexpr int kRedBytes = 8 * T * 64 * 16;
     __shared__ __attribute__((aligned(16))) uint8_t lds[kStreamBytes > kRedBytes ? kStreamBytes : kRedBytes];
+    __shared__ uint32_t xmax_s[16];  // per activation row: the largest hi-term magnitude (tiny rows)
     uint8_t *const tile = lds + wave * kTileBytes;
     uint8_t *const xt = lds + 8 * kTileBytes + wave * kXBytes;  // [3][kXRows][pitch]
     f32x4 *const red = reinterpret_cast<f32x4 *>(lds);         // [8][T][64]
+    if (threadIdx.x < 16) xmax_s[threadIdx.x] = 0;
 
     // Block t of this workgroup: weight rows 16 (blockIdx.x + t gridDim.x) + 0..15.
     __amdgpu_buffer_rsrc_t rs[T];
@@ -1638,6 +1698,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     f32x4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4{z, z, z, z};
+    uint32_t xmx = 0;  // the largest hi-term magnitude this lane split (its activation row xm, or i16)
     auto compute = [&](const Line &r) {
         // x: the three bf16 terms in the B operand layout.
         u32x4 h0, md0, lo0, h1, md1, lo1;
@@ -1651,6 +1712,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
                 hq[q] = ha | (hb << 16);
                 mq[q] = ma | (mb << 16);
                 lq[q] = la | (lb << 16);
+                xmx = max_mag(xmx, hq[q]);
             }
             uint8_t *const xr = xt + xm * kRows16Pitch + xq * 8;
             *reinterpret_cast<uint2 *>(xr) = uint2{hq[0], hq[1]};
@@ -1665,6 +1727,8 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             }
             u32x4 hq, mq, lq;
             split8(xv, hq, mq, lq);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xmx = max_mag(xmx, hq[v]);
             uint8_t *const xr = xt + xm * kRows16Pitch + xq * 16;
             *reinterpret_cast<u32x4 *>(xr) = hq;
             *reinterpret_cast<u32x4 *>(xr + kXRows * kRows16Pitch) = mq;
@@ -1688,6 +1752,8 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
                 for (int e = 0; e < 4; ++e) xv[4 * q + e] = __uint_as_float(xs[q][e]);
             split8(xv, h0, md0, lo0);
             split8(xv + 8, h1, md1, lo1);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xmx = max_mag(max_mag(xmx, h0[v]), h1[v]);
         }
         // Weights: each block through the wave's tile in turn.
 #pragma unroll
@@ -1734,6 +1800,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
     __syncthreads();  // every wave is done with its tile and x planes
 #pragma unroll
     for (int t = 0; t < T; ++t) red[(wave * T + t) * 64 + lane] = acc[t];
+    atomicMax(&xmax_s[kCompact ? xm : i16], hi_max(xmx));
     __syncthreads();
     if (wave < T) {
         const int t = wave;
@@ -1747,6 +1814,14 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             bool live[1][4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) live[0][r] = i16 < mrows && g * 4 + r < nrows;
+            const bool tiny = i16 < mrows && tiny_row(xmax_s[i16]);
+            if (__builtin_amdgcn_ballot_w64(tiny) != 0) {  // this slice's chain (all of k without slices)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (tiny && live[0][r])
+                        s[0][r] = reference_chain(W + (int64_t)(row0 + g * 4 + r) * K + 64 * l0,
+                                                  X + (int64_t)(m0 + i16) * K + 64 * l0, 64 * max(0, l1 - l0));
+            }
             if (P) {  // a k slice: its partial sums, for gemm_sum_slices_kernel (which settles zeros)
                 float *ps = P + (int64_t)blockIdx.z * M * N + (int64_t)(m0 + i16) * N + row0 + g * 4;
 #pragma unroll

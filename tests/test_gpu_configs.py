@@ -63,6 +63,30 @@ def test_c4_full_lm_head(hip, c4_weight, m):
     print(f"C4 m={m} plan={p} rows={rows.size} rel={rel:.3e}")
 
 
+@pytest.mark.parametrize("m", [4, 8, 16])
+def test_c4_tiny_activation_rows(hip, c4_weight, m):
+    """C4 at the MFMA plans its real shape takes (rows16 at M = 4 and 8, the
+    gemm layout at 16) with activation rows of N(0,1) * 1e-36 and * 1e-37
+    beside ordinary rows (tests/test_gpu_tiny_rows.py: the rows the three-term
+    split alone cannot carry): every row within the 1e-5 normwise rule on
+    its own, and the tiny rows bit for bit the reference chain (k is not
+    split on these plans)."""
+    from test_gpu_tiny_rows import check_rows, tiny_rows_x
+    n, k = W.LM_HEAD
+    x = tiny_rows_x(m, k, seed=500 + m)
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer(4 * m * n) as dy:
+        p = hip.plan("rd", m, k, n, x_addr=dx.addr, w_addr=c4_weight.addr)
+        assert (p.slices, p.rows_per_group) == C4_PLANS[m] and p.workspace_bytes == 0, p
+        dy.upload(np.full(m * n, np.nan, np.float32))
+        hip.gemv_rd(dx, c4_weight, dy, m, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (m, n))
+    rows = np.unique(np.r_[0, n - 1, np.random.default_rng(m).integers(0, n, 256), np.arange(255, n, 4096)])
+    wr = W.counter_rows(0, W.C4_TENSOR, rows, k, 0.02)
+    check_rows(y[:, rows], oracle.matmul_bf16_t(x, wr), m, f"C4 tiny rows m={m}", exact=True)
+    assert np.all(y[-1] == 0) and not np.any(np.signbit(y[-1]))
+
+
 def test_c3_every_layer(hip):
     """One decode token of C3 as bench.py runs it (all 32 layers resident;
     q/k/v and gate/up grouped, o and down single; captured in a HIP graph and
