@@ -156,6 +156,7 @@ struct Ctx {
     hipStream_t stream = nullptr;
     dmc::Residency *weights = nullptr;  // resident weights by content key (created at init)
     Buf dx, dy, ws;         // device scratch (reuse is stream-ordered)
+    Buf dwf, dwt;           // f32 route: a weight staged for one call, and its transpose
     int live_graphs = 0;    // executable graphs not yet destroyed
     std::vector<void *> retired_ws;  // outgrown workspaces a live graph may still use
     Buf hx, hy;             // pinned staging
@@ -369,7 +370,7 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
                       (elem == 4 ? 0x6633320000000000ULL : 0));
     auto t1 = std::chrono::steady_clock::now();
     c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
-    if (void *hit = c.weights->find(key, pin)) {
+    if (void *hit = c.weights->find(key, pin, pin ? host : nullptr)) {
         *dev = hit;
         return DMC_HIP_OK;
     }
@@ -394,7 +395,7 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
         (void)hipFree(d);
         return hip_fail(e, "weight upload");
     }
-    c.weights->insert(key, d, bytes, pin);
+    c.weights->insert(key, d, bytes, pin, pin ? host : nullptr);
     c.st.uploads++;
     c.st.upload_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
                           std::chrono::steady_clock::now() - t1)
@@ -617,8 +618,14 @@ void run_host_or_die(const char *entry, bool rd, int64_t l, int64_t r, int64_t o
 //   x @ W (m <= kF32MaxAct activation rows): r [k,n] is the weight, kept
 //     resident as its transpose [n,k] (one transpose at first use).
 // Other shapes are GEMMs this route does not take (dmc_hip_f32_selected says
-// so up front).  As for bf16, x and y pass through pinned staging and the
-// weight stays resident, keyed by content.
+// so up front).  As for bf16, x and y pass through pinned staging.  The
+// weight side is another matter: the reference's f32 `@` keeps nothing
+// between calls, and either operand may be an activation the program
+// updates in place, so a sampled content key is no proof that the bytes are
+// unchanged.  The weight side therefore stays resident only when the caller
+// registered those bytes at that address (dmc_hip_register_weight: its
+// promise that they stay unchanged); otherwise it is uploaded on every call
+// (and, for x @ W, transposed on the device into a second scratch buffer).
 constexpr int64_t kF32MaxAct = 16;
 
 bool f32_weight_left(int64_t m, int64_t n) { return n <= kF32MaxAct && (n <= m || m > kF32MaxAct); }
@@ -663,8 +670,24 @@ int run_host_f32(const float *l, const float *r, float *out, int64_t m, int64_t 
     if (!x_direct) HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
     c.st.stage_ns += ns_since(t0);
     void *dw = nullptr;
-    if ((rc = w_left ? resident(l, (int64_t)w_bytes, &dw) : resident(r, (int64_t)w_bytes, &dw, k, n, false, 4)))
-        return rc;
+    const void *const wsrc = w_left ? static_cast<const void *>(l) : static_cast<const void *>(r);
+    if (w_bytes && c.weights->registered(content_key(wsrc, (int64_t)w_bytes), wsrc)) {
+        if ((rc = w_left ? resident(l, (int64_t)w_bytes, &dw) : resident(r, (int64_t)w_bytes, &dw, k, n, false, 4)))
+            return rc;
+    } else if (w_bytes) {
+        if ((rc = ensure_dev(c.dwf, w_bytes + dmc::kWeightSlack))) return rc;
+        HIP_TRY(hipMemcpyAsync(c.dwf.p, wsrc, w_bytes, hipMemcpyHostToDevice, c.stream), "f32 weight upload");
+        dw = c.dwf.p;
+        if (!w_left) {  // r [k,n] -> [n,k], the row-dot layout
+            if ((rc = ensure_dev(c.dwt, w_bytes + dmc::kWeightSlack))) return rc;
+            HIP_TRY(dmc::launch_transpose_f32(static_cast<const float *>(c.dwf.p), static_cast<float *>(c.dwt.p), k,
+                                              n, c.stream),
+                    "f32 weight transpose");
+            dw = c.dwt.p;
+        }
+    } else {
+        dw = c.dummy;
+    }
     auto t1 = std::chrono::steady_clock::now();
     // Output (activation a, weight row i) is out[i][a] for W @ x, out[a][i] for x @ W.
     const dmc::F32Problem p{static_cast<const float *>(dw), k, xsrc, k, ydst,

@@ -10,7 +10,9 @@
 //   * pinned: made resident by dmc_hip_register_weight, which hands its
 //     device address to the caller; an eviction never frees it, only
 //     release_all (dmc_hip_release_weights) does, so that address stays valid
-//     until the caller releases it.
+//     until the caller releases it.  A pinned entry remembers the host
+//     addresses it was registered from (`registered`), for callers that may
+//     keep only registered operands resident (the f32 route).
 // No HIP here: device allocation and freeing come in as callbacks, so the
 // policy is tested on the CPU (tests/residency_test.cpp).
 #pragma once
@@ -19,6 +21,7 @@
 #include <cstdint>
 #include <functional>
 #include <unordered_map>
+#include <vector>
 
 namespace dmc {
 
@@ -45,16 +48,31 @@ class Residency {
     Residency(size_t max_entries, AllocFn alloc, FreeFn free_fn, DrainFn drain)
         : max_entries_(max_entries), alloc_(std::move(alloc)), free_(std::move(free_fn)), drain_(std::move(drain)) {}
 
-    // The device copy of `key`, or nullptr.  A pinned lookup pins the entry.
-    void *find(const WeightKey &key, bool pin = false) {
+    // The device copy of `key`, or nullptr.  A pinned lookup pins the entry
+    // and records `host` as an address it was registered from.
+    void *find(const WeightKey &key, bool pin = false, const void *host = nullptr) {
         auto it = map_.find(key);
         if (it == map_.end()) return nullptr;
-        if (pin && !it->second.pinned) {
-            it->second.pinned = true;
-            pinned_bytes_ += it->second.bytes;
-            ++pinned_count_;
+        if (pin) {
+            if (!it->second.pinned) {
+                it->second.pinned = true;
+                pinned_bytes_ += it->second.bytes;
+                ++pinned_count_;
+            }
+            note_host(it->second, host);
         }
         return it->second.p;
+    }
+
+    // Was `key` pinned by a registration from host address `host`?  (A
+    // registration is the caller's promise that those bytes stay unchanged
+    // while resident; content alone, sampled, is no such promise.)
+    bool registered(const WeightKey &key, const void *host) const {
+        auto it = map_.find(key);
+        if (it == map_.end() || !it->second.pinned || !host) return false;
+        for (const void *h : it->second.hosts)
+            if (h == host) return true;
+        return false;
     }
 
     // Device memory for a new entry of `bytes` (plus `slack` bytes that are
@@ -97,8 +115,9 @@ class Residency {
         return rc;
     }
 
-    void insert(const WeightKey &key, void *p, int64_t bytes, bool pinned) {
-        map_[key] = Entry{p, bytes, pinned};
+    void insert(const WeightKey &key, void *p, int64_t bytes, bool pinned, const void *host = nullptr) {
+        Entry &e = map_[key] = Entry{p, bytes, pinned, {}};
+        if (pinned) note_host(e, host);
         bytes_ += bytes;
         if (pinned) {
             pinned_bytes_ += bytes;
@@ -134,7 +153,15 @@ class Residency {
         void *p;
         int64_t bytes;
         bool pinned;
+        std::vector<const void *> hosts;  // addresses a registration pinned it from
     };
+
+    static void note_host(Entry &e, const void *host) {
+        if (!host) return;
+        for (const void *h : e.hosts)
+            if (h == host) return;
+        e.hosts.push_back(host);
+    }
 
     bool over_cap(int64_t bytes, int64_t cap) const { return cap > 0 && bytes_ + bytes > cap; }
 

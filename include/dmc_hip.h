@@ -115,10 +115,14 @@ void dmc_matmul_bf16_gpu_t(int64_t l, int64_t r, int64_t out, int64_t m, int64_t
  * summation order as for bf16 (normwise <= 1e-5, NaN/+-inf classes and zero
  * signs kept).  It replaces the single-threaded scalar_matmul that an f32
  * `W @ x` takes (emit_2d_matmul_at, jit.rs:20806-20831: W [m,k] @ x [k,1],
- * n = 1).  Served shapes: n <= 16 (W @ x: l is the weight, kept resident by
- * content) and m <= 16 (x @ W: r is the weight, kept resident as its
- * transpose); any other shape is DMC_HIP_EINVAL (the void form aborts) --
- * ask dmc_hip_f32_selected first.  m == 0 or n == 0 returns without touching
+ * n = 1).  Served shapes: n <= 16 (W @ x: l is the weight) and m <= 16
+ * (x @ W: r is the weight, run as its transpose); any other shape is
+ * DMC_HIP_EINVAL (the void form aborts) -- ask dmc_hip_f32_selected first.
+ * The weight side is uploaded on every call, as the reference keeps nothing
+ * between f32 calls and either operand may be updated in place; only bytes
+ * registered at that address (dmc_hip_register_weight, the caller's promise
+ * that they stay unchanged) stay resident, x @ W's as a transpose built once.
+ * m == 0 or n == 0 returns without touching
  * out (jit.rs:29419); k == 0 writes +0.0.  Synchronous; pending deferred bf16
  * calls are materialized first.  The _try form returns DMC_HIP_E* with out
  * untouched instead of aborting. */

@@ -125,6 +125,22 @@ int main() {
         CHECK(t.find(key(2, 1000)) == nullptr && t.find(key(1, 1000)) == pinned);
         dev.release(s);
     }
+    {  // registered(): pinned entries only, and only from the addresses that pinned them
+        FakeDevice dev{1 << 30};
+        auto t = table(dev, 2048);
+        int h1 = 0, h2 = 0, h3 = 0;
+        void *p = nullptr;
+        CHECK(t.reserve(100, 16, 0, &p) == 0);
+        t.insert(key(1, 100), p, 100, true, &h1);
+        CHECK(t.registered(key(1, 100), &h1));
+        CHECK(!t.registered(key(1, 100), &h2) && !t.registered(key(1, 100), nullptr));
+        CHECK(t.find(key(1, 100), true, &h2) == p);  // the same bytes registered from a second address
+        CHECK(t.registered(key(1, 100), &h1) && t.registered(key(1, 100), &h2));
+        CHECK(add(t, 2, 100, false));  // cached: found by content, never "registered"
+        CHECK(t.find(key(2, 100)) != nullptr && !t.registered(key(2, 100), &h3));
+        CHECK(t.find(key(2, 100), false, &h3) != nullptr && !t.registered(key(2, 100), &h3));
+        CHECK(!t.registered(key(9, 100), &h1));
+    }
     if (failures) return 1;
     std::printf("ok\n");
     return 0;

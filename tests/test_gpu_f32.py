@@ -48,7 +48,7 @@ def test_w_at_x_matches_the_oracle(hip, m, k, n):
     check(hip.matmul_f32_gpu(l, r), oracle.matmul_f32(l, r), what=f"f32 W@x m={m} k={k} n={n}")
 
 
-# x @ W: r is the weight [k, n], m activation rows (resident transposed copy).
+# x @ W: r is the weight [k, n], m activation rows (transposed on the device).
 X_AT_W = [(1, 4096, 1024), (1, 1001, 333), (2, 4096, 4096), (5, 2048, 1500), (16, 1000, 64), (1, 14336, 4096)]
 
 
@@ -115,22 +115,55 @@ def test_gemm_shape_is_refused_and_out_untouched(hip):
     assert rc == -2 and np.all(out == 0)
 
 
-def test_weight_stays_resident_and_new_weights_are_seen(hip):
+def test_unregistered_operand_updated_in_place_is_seen(hip):
+    """The reference's f32 `@` keeps nothing between calls, so an operand
+    that the program updates in place -- here one element that the sampled
+    content key does not read (word 1 of the buffer; the samples start at
+    words 0, q, 2q, ...) -- must give the new result, in both layouts, and no
+    unregistered operand may stay resident."""
     rng = np.random.default_rng(5)
-    w = rng.standard_normal((2048, 4096)).astype(np.float32)
+    count = hip.resident_count()
+    w = rng.standard_normal((2048, 4096)).astype(np.float32)      # W @ x: l is the weight
     x = rng.standard_normal(4096).astype(np.float32)
     hip.matmul_f32_gpu(w, x)
-    count = hip.resident_count()
+    w[0, 3] = 1.0e4
     y = hip.matmul_f32_gpu(w, x)
+    check(y, oracle.matmul_f32(w, x), what="f32 W@x after an in-place update")
+    a = rng.standard_normal((2, 4096)).astype(np.float32)         # x @ W: r is the weight
+    r = rng.standard_normal((4096, 1024)).astype(np.float32)
+    hip.matmul_f32_gpu(a, r)
+    r[0, 3] = -1.0e4
+    y = hip.matmul_f32_gpu(a, r)
+    check(y, oracle.matmul_f32(a, r), what="f32 x@W after an in-place update")
     assert hip.resident_count() == count
-    check(y, oracle.matmul_f32(w, x), what="f32 resident hit")
-    # another weight of the same size is another resident copy (residency is
-    # keyed by sampled content, as the reference's fingerprint is, gpu.rs:334-358:
-    # weights are immutable while resident)
-    w2 = rng.standard_normal((2048, 4096)).astype(np.float32)
-    y2 = hip.matmul_f32_gpu(w2, x)
+
+
+def test_registered_weight_stays_resident(hip):
+    """Bytes registered at an address stay resident for the f32 route (the
+    caller's promise that they do not change): no new entry on W @ x, one
+    transposed copy for x @ W, built once; another address with the same
+    bytes is staged per call."""
+    rng = np.random.default_rng(6)
+    w = rng.standard_normal((2048, 4096)).astype(np.float32)
+    x = rng.standard_normal(4096).astype(np.float32)
+    hip.register_weight(w)
+    count = hip.resident_count()
+    for _ in range(2):
+        y = hip.matmul_f32_gpu(w, x)
+        check(y, oracle.matmul_f32(w, x), what="f32 registered W@x")
+    assert hip.resident_count() == count
+    r = rng.standard_normal((4096, 1024)).astype(np.float32)
+    a = rng.standard_normal((3, 4096)).astype(np.float32)
+    hip.register_weight(r)
+    count = hip.resident_count()
+    for _ in range(2):
+        y = hip.matmul_f32_gpu(a, r)
+        check(y, oracle.matmul_f32(a, r), what="f32 registered x@W")
     assert hip.resident_count() == count + 1
-    check(y2, oracle.matmul_f32(w2, x), what="f32 another weight")
+    r2 = r.copy()  # same bytes, another address: not registered
+    y = hip.matmul_f32_gpu(a, r2)
+    check(y, oracle.matmul_f32(a, r2), what="f32 copy of a registered weight")
+    assert hip.resident_count() == count + 1
 
 
 @pytest.mark.parametrize("m,k,n,stream", [(1, 4096, 14336, True), (4, 4096, 1000, True), (3, 14336, 4096, True),
