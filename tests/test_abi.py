@@ -60,6 +60,61 @@ def test_library_is_gfx950_code_only(tmp_path):
     assert targets == ["hipv4-amdgcn-amd-amdhsa--gfx950"], out.stdout
 
 
+def _kernel_descriptors(tmp_path):
+    """The AMDGPU metadata of every kernel in our own build's gfx950 code
+    object (llvm-readelf --notes), or None when the tools are missing."""
+    import yaml
+    fb, co = tmp_path / "fatbin.bin", tmp_path / "k.co"
+    steps = (["objcopy", "-O", "binary", "--only-section=.hip_fatbin", str(_lib.LIB_PATH), str(fb)],
+             ["/opt/rocm/llvm/bin/clang-offload-bundler", "--unbundle", "--type=o", f"--input={fb}",
+              "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"])
+    for cmd in steps:
+        if subprocess.run(cmd, capture_output=True).returncode != 0:
+            return None
+    r = subprocess.run(["/opt/rocm/llvm/bin/llvm-readelf", "--notes", str(co)], capture_output=True, text=True)
+    if r.returncode != 0 or "amdhsa.kernels" not in r.stdout:
+        return None
+    t = r.stdout
+    a = t.index("\n", t.index("---")) + 1
+    return yaml.safe_load(t[a:t.index("\n...", a)])["amdhsa.kernels"]
+
+
+def test_kernel_descriptors_within_dispatch_limits(tmp_path):
+    """Every kernel's dispatch needs stay inside what an AQL dispatch packet
+    and a gfx950 CU allow: static LDS <= 160 KiB, no scratch (private
+    segment 0, no dynamic stack), at most 1024 work-items, kernel arguments
+    well under HIP's 4 KiB.  (The check behind the finding that the queue
+    aborts seen with HIP-graph replays under rocprofv3 have no cause in the
+    launch parameters: every node of those graphs is one of these kernels,
+    launched with a grid whose work-item count fits 32 bits,
+    test_decode_step_grids_fit_a_dispatch_packet.)"""
+    ks = _kernel_descriptors(tmp_path)
+    if ks is None:
+        pytest.skip("offload bundle tools unavailable")
+    assert len(ks) > 100
+    for k in ks:
+        name = k[".name"]
+        assert k[".group_segment_fixed_size"] <= 160 * 1024, name
+        assert k[".private_segment_fixed_size"] == 0 and not k[".uses_dynamic_stack"], name
+        assert k[".max_flat_workgroup_size"] <= 1024, name
+        assert k[".kernarg_segment_size"] <= 1024, name
+        assert k[".vgpr_spill_count"] == 0, name
+        assert k[".wavefront_size"] == 64, name
+
+
+def test_decode_step_grids_fit_a_dispatch_packet():
+    """The launches of a C3 decode step (single and grouped, as bench.py
+    captures them into HIP graphs): each plan has a nonzero grid whose
+    work-item count fits the packet's 32-bit grid size, and a workgroup of
+    at most 1024 work-items."""
+    from demonic_amd import workloads as W
+    for nm, n, k in W.LLAMA3_8B_LAYER:
+        p = d.plan("rd", 1, k, n, x_addr=256, w_addr=256)
+        threads = 64 * p.waves
+        assert 0 < p.grid_x and 0 < threads <= 1024, (nm, p)
+        assert p.grid_x * threads < 2 ** 32, (nm, p)
+
+
 # ---- the route predicate (shape of jit.rs:39087-39113) ----------------------------------
 
 def test_selection_predicate():
