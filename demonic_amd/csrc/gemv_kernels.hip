@@ -718,6 +718,130 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
         [&](int t, float v) { Y[(int)blockIdx.x * rpw + t] = v; });
 }
 
+// ---- RD streaming, shared x over 14 waves (M = 1, long rows) ----------------
+//
+// The shared-x layout with one group of NS = 14 waves splitting k instead of
+// two halves of 8: lane l of wave w owns the KV windows (j*NS + w)*64 + l,
+// so at K = 14336 (KV = 2) every load instruction carries data (the halves'
+// fourth window is past K for half their lanes).  The workgroup's 16 rows
+// stream 4 at a time through two register buffers with unconditional loads
+// and no barrier until the end, where wave 0 sums each row's 14 partials
+// in wave order and rd_finish settles exact zeros.
+constexpr int kX14Waves = 14;
+
+template <int KV>
+__global__ void __launch_bounds__(64 * kX14Waves)
+gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                          int K) {
+    constexpr int NS = kX14Waves, ROWS = 4, NT = 64 * NS, RPW = 16;
+    static_assert(KV * NS * 64 * 8 <= kXldsMaxK * 7 / 8, "x windows must lie inside the LDS copy");
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = (int)blockIdx.x * RPW;
+    const int nr = max(0, min(N, rb + RPW) - rb);
+
+    __shared__ __attribute__((aligned(16))) float xs[kXldsMaxK];
+    constexpr int kHi = kXldsMaxK / 2;
+    __shared__ float red[NS][RPW];
+
+    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4);
+    u32x4 xp[6];
+#pragma unroll
+    for (int i = 0; i < 6; ++i)  // windows t, t + NT, t + 2 NT (1792 < 3 * 896)
+        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + (i >> 1) * NT) * 32u + (i & 1) * 16u, 0, 0);
+    uint32_t eoff[KV];
+    bool has[KV];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int e = ((j * NS + wave) * 64 + lane) * 8;
+        has[j] = e < K;
+        eoff[j] = has[j] ? (uint32_t)e * 2 : kOutOfRange;
+    }
+    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
+    const uint32_t row_bytes = (uint32_t)K * 2;
+    const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * K, (uint32_t)nr * row_bytes);
+    u32x4 ba[ROWS][KV], bb[ROWS][KV];
+    auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q)
+#pragma unroll
+            for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], (uint32_t)(i0 + q) * row_bytes);
+    };
+    load(ba, 0);
+    load(bb, ROWS);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+        const uint32_t w = threadIdx.x + (i >> 1) * NT;
+        if (w < kHi / 4) *reinterpret_cast<u32x4 *>(&xs[(i & 1) * kHi + w * 4u]) = xp[i];
+    }
+    __syncthreads();
+    float xr[KV][8];
+#pragma unroll
+    for (int j = 0; j < KV; ++j) {
+        const int w = (j * NS + wave) * 64 + lane;
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
+        const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
+        const uint32_t sgn = has[j] ? 0u : 0x80000000u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            xr[j][q] = __uint_as_float(a[q] | sgn);
+            xr[j][q + 4] = __uint_as_float(b[q] | sgn);
+        }
+    }
+    auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
+        float acc[ROWS];
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) acc[q] = init;
+#pragma unroll
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int q = 0; q < ROWS; ++q) {
+                    const uint32_t d = wv[q][j][e >> 1];
+                    acc[q] = fmaf(xr[j][e], (e & 1) ? widen_hi(d) : widen_lo(d), acc[q]);
+                }
+#pragma unroll
+        for (int q = 0; q < ROWS; ++q) {
+            const float s = wave_sum_dpp(acc[q]);
+            if (lane == 0) red[wave][i0 + q] = s;
+        }
+    };
+    sum_rows(ba, 0);
+    load(ba, 2 * ROWS);
+    sum_rows(bb, ROWS);
+    load(bb, 3 * ROWS);
+    sum_rows(ba, 2 * ROWS);
+    sum_rows(bb, 3 * ROWS);
+    __syncthreads();
+    __shared__ uint64_t hits[NS + 1];
+    rd_finish<NS>(
+        nr, hits,
+        [&](int t) {
+            float s = red[0][t];
+#pragma unroll
+            for (int w = 1; w < NS; ++w) s += red[w][t];
+            return s;
+        },
+        [&](int t) {
+            bool hit = false;
+#pragma unroll
+            for (int j = 0; j < KV; ++j) {
+                const int w = (j * NS + wave) * 64 + lane;
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
+                const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
+                const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
+                                     __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
+                                     __uint_as_float(b[2]), __uint_as_float(b[3])};
+                hit |= window_hit(xw, load_w16(rs, eoff[j], (uint32_t)t * row_bytes));
+            }
+            return hit;
+        },
+        [&](int t) { return chain_strided(W + (int64_t)(rb + t) * K, 1, X, K); },
+        [&](int t, float v) { Y[rb + t] = v; });
+}
+
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
 //
 // The layout of gemv_rd_stream_kernel (NW waves split k; lane l of wave w
@@ -3261,16 +3385,29 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     if (pl.vec == 8 && p.ldw == p.k && p.ldx == p.k && p.ldy == p.n) {
         RdPlan sp{};
         if (plan_stream(p.m, p.k, &p.n, 1, cus, sp)) {
-            // Long rows at M = 1 (2 to 4 windows per lane): 16-wave workgroups
-            // of 16 rows whose two halves share one LDS copy of x.  One fills
-            // a CU, so only when they come in whole rounds of one per CU (or
-            // enough rounds that a partial last one costs little): C5's
-            // N = 4097 would leave a 257th workgroup to start after the others
-            // (17.3 us against 15.7 on 8-wave workgroups).
+            // Long rows at M = 1 (2 to 4 windows per lane): workgroups of 16
+            // rows that share one LDS copy of x.  One fills a CU, so only when
+            // they come in whole rounds of one per CU (or enough rounds that
+            // a partial last one costs little): C5's N = 4097 would leave a
+            // 257th workgroup to start after the others (17.3 us against 15.7
+            // on 8-wave workgroups).  K up to 14336 takes one group of 14
+            // waves splitting k (every load carries data at K = 14336: C2 down
+            // 19.10 -> 18.97 us, same box), longer rows two 8-wave halves
+            // (DMC_HIP_RD_X14=0 keeps the halves everywhere).
             const int64_t g16 = (p.n + 15) / 16;
             const int xl = env_int("DMC_HIP_RD_XLDS", 1);  // 0: never; 2: wherever the kernel applies
+            const bool x14 = env_int("DMC_HIP_RD_X14", 1) != 0 && p.k <= 2 * kX14Waves * 512;
             if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
-                p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) && xl != 0) {
+                p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) && xl != 0 &&
+                x14) {
+                sp.waves = kX14Waves;
+                sp.kvec = (int)((p.k + kX14Waves * 512 - 1) / (kX14Waves * 512));
+                sp.rows = 4;
+                sp.rpw = 16;
+                sp.grid_x = (p.n + 15) / 16;
+            } else if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
+                       p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) &&
+                       xl != 0) {
                 int rpw = env_int("DMC_HIP_RD_XLDS_RPW", 16);
                 if (rpw != 8 && rpw != 16 && rpw != 32) rpw = 16;
                 sp.waves = 16;
@@ -3504,6 +3641,18 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         return hipErrorInvalidValue;
     }
     if (pl.kvec > 0 && pl.any_align) return rd_unaligned_dispatch(p, pl, s);
+    if (pl.kvec > 0 && pl.waves == kX14Waves && pl.rows == 4) {
+        if (pl.rpw != 16 || p.m != 1 || pl.kvec < 1 || pl.kvec > 2 || (int64_t)pl.kvec * kX14Waves * 512 < p.k ||
+            (int64_t)16 * p.k * 2 > INT32_MAX)
+            return hipErrorInvalidValue;
+        if (pl.kvec == 1)
+            hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<1>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s,
+                               p.w, p.x, p.y, (int)p.n, (int)p.k);
+        else
+            hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<2>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s,
+                               p.w, p.x, p.y, (int)p.n, (int)p.k);
+        return hipGetLastError();
+    }
     if (pl.kvec > 0 && pl.waves == 16) {
         if (pl.rows != 2 || (pl.rpw != 8 && pl.rpw != 16 && pl.rpw != 32) || p.m != 1 || p.k > kXldsMaxK)
             return hipErrorInvalidValue;
@@ -3727,6 +3876,7 @@ hipError_t noalloc_scratch_resolve(void **device_address) {
     *device_address = nullptr;
     return hipGetSymbolAddress(device_address, HIP_SYMBOL(scratch));
 }
+
 
 hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t s) {
     if (bytes <= 0) return hipSuccess;

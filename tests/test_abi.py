@@ -147,10 +147,16 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     up = d.plan("rd", 1, 4096, 14336, x_addr=256, w_addr=256)
     assert (up.vec, up.waves, up.slices, up.rows_per_group, up.rows_or_rw, up.mt, up.grid_x) == \
         (8, 8, 1, 4, 2, 1, 3584)
-    # long rows: ceil(14336 / 4096) vectors per lane; 16-wave workgroups of 16
-    # rows whose two 8-wave halves share one LDS copy of x (one per CU) ...
+    # long rows: workgroups of 16 rows sharing one LDS copy of x (one per CU):
+    # up to K = 14336 one group of 14 waves, 2 vectors per lane ...
+    down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
+    assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (14, 2, 16, 256)
+    # ... beyond it (or with DMC_HIP_RD_X14=0) two 8-wave halves, ceil(K / 4096) vectors per lane ...
+    assert d.plan("rd", 1, 16384, 4096, x_addr=256, w_addr=256).waves == 16
+    monkeypatch.setenv("DMC_HIP_RD_X14", "0")
     down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
     assert (down.waves, down.slices, down.rows_per_group, down.grid_x) == (16, 4, 16, 256)
+    monkeypatch.delenv("DMC_HIP_RD_X14")
     # ... or, switched off, 8-wave workgroups of 8 rows, each with x in registers
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "0")
     down = d.plan("rd", 1, 14336, 4096, x_addr=256, w_addr=256)
@@ -160,8 +166,8 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # them (one 16-wave workgroup fills a CU): the 8-wave layout
     assert d.plan("rd", 1, 14336, 1024, x_addr=256, w_addr=256).waves == 8
     assert d.plan("rd", 1, 11008, 4097, x_addr=256, w_addr=256).waves == 8
-    assert d.plan("rd", 1, 8192, 8192, x_addr=256, w_addr=256).waves == 16      # two whole rounds
-    assert d.plan("rd", 1, 8192, 28672, x_addr=256, w_addr=256).waves == 16     # seven
+    assert d.plan("rd", 1, 8192, 8192, x_addr=256, w_addr=256).waves == 14      # two whole rounds
+    assert d.plan("rd", 1, 8192, 28672, x_addr=256, w_addr=256).waves == 14     # seven
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
     assert small.grid_x >= 512
     # M = 1: the streaming kernel

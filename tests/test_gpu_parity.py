@@ -14,7 +14,7 @@ import pytest
 
 import oracle
 from demonic_amd import workloads as W
-from parity import check, check_bound
+from parity import check, check_bound, check_or_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -1042,10 +1042,12 @@ XLDS_SHAPES = [(4096, 14336), (4096, 4112), (8192, 8192), (4096, 16384), (16380,
 @pytest.mark.parametrize("n,k", XLDS_SHAPES)
 def test_shared_x_workgroups(hip, n, k, monkeypatch):
     """Long rows at M = 1 on 16-wave workgroups whose halves share one LDS
-    copy of x: a last block of two windows (k = 4112), the largest K it
+    copy of x (the layout for K above 14336; DMC_HIP_RD_X14=0 keeps it for
+    shorter rows): a last block of two windows (k = 4112), the largest K it
     takes, two rounds (n = 8192), and a partial last workgroup whose second
     half holds 4 rows (n = 16380, four rounds)."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
+    monkeypatch.setenv("DMC_HIP_RD_X14", "0")
     assert hip.plan("rd", 1, k, n).waves == 16
     x, w = case(1, k, n, seed=7000 + n + k, edge=True)
     check(run_rd(hip, x, w), ref(x, w), what=f"xlds n={n} k={k}")
@@ -1056,6 +1058,7 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     """The zero-sign rule of test_underflowing_products_keep_their_zero_sign on
     the shared-x layout: even rows end at -0.0, odd rows at +0.0."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "1")
+    monkeypatch.setenv("DMC_HIP_RD_X14", "0")
     n = 4096
     assert hip.plan("rd", 1, k, n).waves == 16
     x = np.full((1, k), np.float32(-1e-38), np.float32)
@@ -1072,6 +1075,62 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     y_ref = ref(xm, w)
     y = run_rd(hip, xm, w)
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
+
+
+X14_SHAPES = [(4096, 14336), (4097, 14336), (8190, 12288), (4096, 4112), (1030, 14336), (6, 9000), (16384, 12288)]
+
+
+def _rd_dev(hip, x, w, y_init=np.nan):
+    m, k = x.shape
+    n = w.shape[0]
+    with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        dy.upload(np.full(m * n, y_init, np.float32))
+        hip.gemv_rd(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        return dy.download(np.float32, (m, n))
+
+
+@pytest.mark.parametrize("n,k", X14_SHAPES)
+def test_shared_x_fourteen_waves(hip, n, k, monkeypatch):
+    """The shared-x layout on one group of 14 waves splitting k (the default
+    for K <= 14336; DMC_HIP_RD_XLDS=2 takes it wherever it applies): C2 down
+    (two windows per lane, all carrying data), a partial last workgroup
+    (n = 4097: one row of 16), one window per lane (k = 4112, its last block
+    holding 16 elements), fewer rows than one workgroup (n = 6), and 1024
+    workgroups.  Edge data; the oracle's result within the parity rule and,
+    row by row, the elementwise bound; two launches bit for bit alike."""
+    x, w = case(1, k, n, seed=7100 + n + k, edge=True)
+    monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
+    p = hip.plan("rd", 1, k, n, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_per_group, p.slices) == (14, 16, 1 if k <= 7168 else 2), p
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
+    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"x14 n={n} k={k}")
+
+
+@pytest.mark.parametrize("k", [4112, 14336])
+def test_shared_x_fourteen_waves_zero_rule(hip, k, monkeypatch):
+    """Exact zeros on the 14-wave kernel: underflowing products of one sign
+    (zero signs from the chain) and the rows of zero_rows' patterns
+    (order-dependent zeros, exact-zero products) -- bit for bit the
+    reference."""
+    monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
+    n = 4096
+    assert hip.plan("rd", 1, k, n, x_addr=256, w_addr=256).waves == 14
+    x = np.full((1, k), np.float32(-1e-38), np.float32)
+    w = np.full((n, k), 0x0001, np.uint16)
+    w[1::2, :] = 0x8001
+    y_ref = ref(x, w)
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+    xm, wz = zero_rows(k, 9)
+    w = np.ascontiguousarray(wz[np.arange(n) % 9])
+    xm = np.ascontiguousarray(xm[2:3])
+    y_ref = ref(xm, w)
+    y = _rd_dev(hip, xm, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
+        np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
 
 
 # ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
