@@ -5,9 +5,9 @@ Workload (one "step"): the two Llama-3-8B FFN decode GEMVs of config C2 in the
 row-dot layout -- up/gate W [14336,4096] @ x[4096] and down W [4096,14336] @
 x[14336] -- bf16 weights ~N(0,0.02), f32 activations ~N(0,1), seed 0, weights
 and activations resident in HBM before the timed region starts.  Cold cache:
-each weight has COPIES distinct device copies and consecutive steps rotate
-through them, so >= 1 GiB of other weights streams between two reads of the
-same bytes (MI355X's Infinity Cache is 256 MB).
+each weight has COPIES (6) distinct device copies and consecutive steps
+rotate through them, so 11 other weights (1.29 GB, 1.2 GiB) stream between
+two reads of the same bytes (MI355X's Infinity Cache is 256 MB).
 
 value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
               of the K timed steps over their host wall time, synchronized on
@@ -179,7 +179,7 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--copies", type=int, default=5, help="distinct device copies per weight")
+    ap.add_argument("--copies", type=int, default=6, help="distinct device copies per weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extended", action="store_true",
@@ -334,7 +334,7 @@ def main(argv=None) -> int:
         "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_from_profile(),
         "kernel": "row-dot streaming GEMVs: gemv_rd_stream_kernel (up/gate), "
-                  "gemv_rd_stream_xlds_kernel (down, x shared through LDS)",
+                  "gemv_rd_stream_x14_kernel (down, 14 waves sharing x through LDS)",
         "bytes_per_launch": {"up": b_up, "down": b_down},
         "avg_launch_us": round(launch_us, 3),
         "us_per_launch": {nm: round(u, 3) for nm, u in us.items()},
