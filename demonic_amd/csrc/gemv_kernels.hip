@@ -1237,14 +1237,23 @@ __device__ void settle_zeros(f32x4 (&s)[T], const bool (&live)[T][4], const int 
 // 256 weight rows per workgroup (8 waves x 2 tiles, each wave owning its
 // tiles: no cross-wave reduction), k in chunks of 64 so each row's chunk is
 // one 128-byte line, weights loaded 8 whole lines per instruction into a
-// 144-byte-pitch LDS tile (operand reads conflict-free), x's chunk (16 x 64)
+// swizzled LDS tile (writes and operand reads conflict-free), x's chunk (16 x 64)
 // split once per workgroup into LDS planes.  x bytes are 1/8 of weight bytes.
 // Each wave stages and consumes only its own 32 rows, so its tile needs only
 // the wave's own program order (LDS executes a wave's operations in order);
 // the shared x planes are double-buffered behind one barrier per chunk.
 // Loads run two chunks ahead in registers.
 constexpr int kWideRows = 256;
-constexpr int kWidePitch = 144;
+constexpr int kWidePitch = 128;
+
+// Weight and x tiles in LDS hold rows of 128 bytes, 8 pieces of 16, back to
+// back, with piece p of row r stored at position p ^ ((r / 2) mod 8).  A
+// tile is written 8 rows x 128 bytes per instruction (each pair of rows then
+// covers the 64 banks once) and read 16 rows x one piece (the rows' pieces
+// land on 16 different groups of 4 banks).  The earlier 144-byte pitch kept
+// the reads apart but let each pair of rows written together meet on 4 banks
+// (11-24% of the MFMA kernels' LDS cycles lost to conflicts).
+__device__ __forceinline__ int swz(int r, int p) { return r * 128 + ((p ^ ((r >> 1) & 7)) << 4); }
 
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
@@ -1259,7 +1268,7 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
     const int m0 = blockIdx.y * 16;
     const int nchunks = K / 64;
 
-    __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 36 KiB
+    __shared__ __attribute__((aligned(16))) uint8_t wt[kWideRows * kWidePitch];  // 32 KiB
     __shared__ u32x4 xpl[2][2][3][64];                                           // 2 x 6 KiB
     __shared__ uint32_t xmax_s[16];  // per activation row: the largest hi-term magnitude (tiny rows)
     uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
@@ -1299,7 +1308,7 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
     uint32_t xmx = 0;
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + swz(slr + 8 * j, lane & 7)) = r.w[j];
         if (xthread) {
             u32x4 hi, md, lo;
             split8(r.x, hi, md, lo);
@@ -1320,7 +1329,7 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
             uint32_t mx = 0;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+                a[t] = *reinterpret_cast<const u32x4 *>(wtw + swz(t * 16 + i16, b * 4 + g));
 #pragma unroll
                 for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
             }
@@ -1436,7 +1445,7 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     const int c1 = min(K / 64, c0 + kc);
     const int nchunks = max(0, c1 - c0);
 
-    __shared__ __attribute__((aligned(16))) uint8_t wt[kRows * kWidePitch];  // 36 KiB at 8 waves
+    __shared__ __attribute__((aligned(16))) uint8_t wt[kRows * kWidePitch];  // 32 KiB at 8 waves
     __shared__ u32x4 xpl[2][MB][2][3][64];                                   // MB x 12 KiB
     __shared__ uint32_t xmax_s[16 * MB];  // per activation row: the largest hi-term magnitude (tiny rows)
     uint8_t *const wtw = wt + wave * 32 * kWidePitch;                            // this wave's 32 rows
@@ -1498,7 +1507,7 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     for (int j = 0; j < kXPer; ++j) xmx[j] = 0;
     auto store = [&](const Regs &r, int xbuf) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + (slr + 8 * j) * kWidePitch + scol) = r.w[j];
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4 *>(wtw + swz(slr + 8 * j, lane & 7)) = r.w[j];
 #pragma unroll
         for (int j = 0; j < kXPer; ++j) {
             if (!xthread[j]) continue;
@@ -1556,7 +1565,7 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     auto read_ops = [&](int xbuf, int b, u32x4 (&a)[2], u32x4 (&xo)[MB][3]) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
-            a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+            a[t] = *reinterpret_cast<const u32x4 *>(wtw + swz(t * 16 + i16, b * 4 + g));
 #pragma unroll
         for (int mt = 0; mt < MB; ++mt)
 #pragma unroll
@@ -1582,7 +1591,7 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
                 uint32_t mx = 0;
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    a[t] = *reinterpret_cast<const u32x4 *>(wtw + (t * 16 + i16) * kWidePitch + b * 64 + g * 16);
+                    a[t] = *reinterpret_cast<const u32x4 *>(wtw + swz(t * 16 + i16, b * 4 + g));
 #pragma unroll
                     for (int v = 0; v < 4; ++v) mx = max_mag(mx, a[t][v]);
                 }
@@ -1733,7 +1742,7 @@ gemm_sum_slices_kernel(const float *__restrict__ P, int slices, float *__restric
 // outside the buffer: zeros, no traffic) and splits 16 values.  The waves' partial sums meet once, at the
 // end, in LDS in wave order.  Loads run one line ahead (two register sets);
 // lines past the last load from outside the buffers.
-constexpr int kRows16Pitch = 144;
+constexpr int kRows16Pitch = 128;
 
 template <int MC, int T>
 __global__ void __launch_bounds__(512)
@@ -1791,7 +1800,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
 #pragma unroll
         for (int p = 0; p < 3; ++p)
             if (lane < kRows16Pitch / 16)
-                *reinterpret_cast<u32x4 *>(xt + (p * kXRows + MC) * kRows16Pitch + lane * 16) = u32x4{0, 0, 0, 0};
+                *reinterpret_cast<u32x4 *>(xt + p * kXRows * kRows16Pitch + swz(MC, lane)) = u32x4{0, 0, 0, 0};
     }
 
     struct Line {
@@ -1838,7 +1847,7 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
                 lq[q] = la | (lb << 16);
                 xmx = max_mag(xmx, hq[q]);
             }
-            uint8_t *const xr = xt + xm * kRows16Pitch + xq * 8;
+            uint8_t *const xr = xt + swz(xm, xq >> 1) + (xq & 1) * 8;
             *reinterpret_cast<uint2 *>(xr) = uint2{hq[0], hq[1]};
             *reinterpret_cast<uint2 *>(xr + kXRows * kRows16Pitch) = uint2{mq[0], mq[1]};
             *reinterpret_cast<uint2 *>(xr + 2 * kXRows * kRows16Pitch) = uint2{lq[0], lq[1]};
@@ -1853,20 +1862,21 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
             split8(xv, hq, mq, lq);
 #pragma unroll
             for (int v = 0; v < 4; ++v) xmx = max_mag(xmx, hq[v]);
-            uint8_t *const xr = xt + xm * kRows16Pitch + xq * 16;
+            uint8_t *const xr = xt + swz(xm, xq);
             *reinterpret_cast<u32x4 *>(xr) = hq;
             *reinterpret_cast<u32x4 *>(xr + kXRows * kRows16Pitch) = mq;
             *reinterpret_cast<u32x4 *>(xr + 2 * kXRows * kRows16Pitch) = lq;
         }
         if (kCompact) {
             __builtin_amdgcn_wave_barrier();
-            const uint8_t *const xr = xt + (i16 < MC ? i16 : MC) * kRows16Pitch + g * 16;
-            h0 = *reinterpret_cast<const u32x4 *>(xr);
-            md0 = *reinterpret_cast<const u32x4 *>(xr + kXRows * kRows16Pitch);
-            lo0 = *reinterpret_cast<const u32x4 *>(xr + 2 * kXRows * kRows16Pitch);
-            h1 = *reinterpret_cast<const u32x4 *>(xr + 64);
-            md1 = *reinterpret_cast<const u32x4 *>(xr + kXRows * kRows16Pitch + 64);
-            lo1 = *reinterpret_cast<const u32x4 *>(xr + 2 * kXRows * kRows16Pitch + 64);
+            const int xrow = i16 < MC ? i16 : MC;
+            const uint8_t *const xr0 = xt + swz(xrow, g), *const xr1 = xt + swz(xrow, 4 + g);
+            h0 = *reinterpret_cast<const u32x4 *>(xr0);
+            md0 = *reinterpret_cast<const u32x4 *>(xr0 + kXRows * kRows16Pitch);
+            lo0 = *reinterpret_cast<const u32x4 *>(xr0 + 2 * kXRows * kRows16Pitch);
+            h1 = *reinterpret_cast<const u32x4 *>(xr1);
+            md1 = *reinterpret_cast<const u32x4 *>(xr1 + kXRows * kRows16Pitch);
+            lo1 = *reinterpret_cast<const u32x4 *>(xr1 + 2 * kXRows * kRows16Pitch);
         } else {
             float xv[16];
             const u32x4 xs[4] = {r.x0, r.x1, r.x2, r.x3};
@@ -1883,11 +1893,11 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             __builtin_amdgcn_wave_barrier();
-            *reinterpret_cast<u32x4 *>(tile + srow * kRows16Pitch + scol) = r.w0[t];
-            *reinterpret_cast<u32x4 *>(tile + (srow + 8) * kRows16Pitch + scol) = r.w1[t];
+            *reinterpret_cast<u32x4 *>(tile + swz(srow, lane & 7)) = r.w0[t];
+            *reinterpret_cast<u32x4 *>(tile + swz(srow + 8, lane & 7)) = r.w1[t];
             __builtin_amdgcn_wave_barrier();
-            const u32x4 a0 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + g * 16);
-            const u32x4 a1 = *reinterpret_cast<const u32x4 *>(tile + i16 * kRows16Pitch + 64 + g * 16);
+            const u32x4 a0 = *reinterpret_cast<const u32x4 *>(tile + swz(i16, g));
+            const u32x4 a1 = *reinterpret_cast<const u32x4 *>(tile + swz(i16, 4 + g));
             uint32_t mx = 0;
 #pragma unroll
             for (int v = 0; v < 4; ++v) mx = max_mag(max_mag(mx, a0[v]), a1[v]);
@@ -2291,13 +2301,29 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
         sum_rows(bb, xb, r + U * G);
     }
 
-    __shared__ float red[NW * G][MT][CB];
+    // The partials in LDS as two half-planes: a lane's columns 8l .. 8l+3 go
+    // to the first at words 4l .. 4l+3, columns 8l+4 .. 8l+7 to the second,
+    // so each 16-byte write covers consecutive words across the lanes; they
+    // are read back in address order (word a of a half-plane row is column
+    // (a % 4CL) / 4 * 8 + (a / 4CL) * 4 + a % 4).  Every LDS access here
+    // moves consecutive words (32-byte windows written at a 32-byte stride
+    // lost a third of the LDS cycles to conflicts); the price is y's stores in
+    // 16-byte runs 32 bytes apart within a wave, once per workgroup.  Rows
+    // are 16 words longer than their data, so two waves' words of one column
+    // never share a bank (reads that fetch both at once stay whole).
+    constexpr int kRow = MT * CB + 16;
+    __shared__ __attribute__((aligned(16))) float red[NW * G][kRow];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-            red[wave * G + rg][m][(lane % CL) * 8 + e] =
-                zero_fold(acc[m][e], ((nz[m][e >> 1] >> (16 * (e & 1))) & 0x7fffu) != 0);
+        for (int h = 0; h < 2; ++h) {
+            float4 f;
+            f.x = zero_fold(acc[m][4 * h + 0], ((nz[m][2 * h] >> 0) & 0x7fffu) != 0);
+            f.y = zero_fold(acc[m][4 * h + 1], ((nz[m][2 * h] >> 16) & 0x7fffu) != 0);
+            f.z = zero_fold(acc[m][4 * h + 2], ((nz[m][2 * h + 1] >> 0) & 0x7fffu) != 0);
+            f.w = zero_fold(acc[m][4 * h + 3], ((nz[m][2 * h + 1] >> 16) & 0x7fffu) != 0);
+            *reinterpret_cast<float4 *>(&red[wave * G + rg][m * CB + h * 4 * CL + (lane % CL) * 4]) = f;
+        }
     __syncthreads();
 
     const int c0 = cb * CB;
@@ -2308,11 +2334,12 @@ gemv_cs_stream_kernel(const uint16_t *__restrict__ W, int64_t rs, const float *_
     const bool final_out = slices == 1 && !UN;
     float *out = final_out ? Y + z * z_stride : P + z * z_stride + (int64_t)s * p_slice;
     for (int t = threadIdx.x; t < MT * CB; t += 64 * NW) {
-        const int m = t / CB, c = t - m * CB;
+        const int m = t / CB, a = t - m * CB;
+        const int c = (a % (4 * CL)) / 4 * 8 + (a / (4 * CL)) * 4 + a % 4;
         const bool store = m < M && c < ncol;
-        float v = red[0][m][c];
+        float v = red[0][t];
 #pragma unroll
-        for (int w = 1; w < NW * G; ++w) v += red[w][m][c];
+        for (int w = 1; w < NW * G; ++w) v += red[w][t];
         if (final_out)
             v = zero_unfold(v, store, xz + (int64_t)(store ? m : 0) * K, W + z * rs + (store ? c0 + c : 0), N, K);
         if (store) out[(int64_t)m * N + c0 + c] = v;
