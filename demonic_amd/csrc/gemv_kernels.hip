@@ -1412,7 +1412,8 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
 template <int MB, bool FUSE, int NWV>
 __global__ void __launch_bounds__(64 * NWV)
 gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, const uint16_t *__restrict__ XS,
-                         float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy) {
+                         float *__restrict__ Y, float *__restrict__ P, int N, int K, int M, int kc, int gx, int gy,
+                         int xcd) {
     static_assert(MB >= 1 && MB <= 4, "16 to 64 activation rows per workgroup");
     static_assert(NWV == 4 || NWV == 8, "32 weight rows per wave");
     constexpr int kRows = 32 * NWV;                  // weight rows per workgroup
@@ -1425,13 +1426,15 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
     const int i16 = lane & 15;
     const int g = lane >> 4;
     // The tile from the linear workgroup id (a 1-D grid of gx * gy * slices).
-    // Workgroup L runs on XCD L % 8 (the dispatcher deals workgroups to the 8
-    // XCDs in turn) and takes the L / 8-th tile of that XCD's contiguous
-    // share, activation tiles fastest, so the workgroups an XCD runs together
-    // share weight blocks through its L2 (C2 shapes: 2-3% faster than weight
-    // blocks fastest).
+    // With `xcd` set, workgroup L, which runs on XCD L % 8 (the dispatcher
+    // deals workgroups to the 8 XCDs in turn), takes the L / 8-th tile of
+    // that XCD's contiguous share, activation tiles fastest, so the
+    // workgroups an XCD runs together share weight blocks through its L2
+    // (C2 shapes at several activation tiles: 2-3% faster than weight blocks
+    // fastest); otherwise tiles go in launch order, consecutive weight
+    // blocks to different XCDs.
     uint32_t lin = blockIdx.x;
-    {
+    if (xcd) {
         const uint32_t x = lin & 7u, q = gridDim.x >> 3, r = gridDim.x & 7u;
         lin = x * q + min(x, r) + (lin >> 3);
     }
@@ -3629,11 +3632,15 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
                                    s, p.x, xs, count);
             const int64_t wgs = pl.grid_x * pl.grid_y * (int64_t)pl.kslices;
             if (wgs > INT32_MAX) return hipErrorInvalidValue;
+            // The XCD-grouped tile order where activation tiles share weight
+            // blocks (DMC_HIP_GEMM_XCD: 0 never, 2 always).
+            const int xenv = env_int("DMC_HIP_GEMM_XCD", 1);
+            const int xcd = xenv == 2 || (xenv == 1 && pl.grid_y > 1) ? 1 : 0;
 #define DMC_GEMM(MB, F, NW)                                                                                  \
     if (pl.mt == 16 * MB && pl.xfuse == F && pl.waves == NW)                                                 \
         hipLaunchKernelGGL((gemv_rd_mfma_gemm_kernel<MB, F, NW>), dim3((unsigned)wgs), dim3(64 * NW), 0, s, p.w,  \
                            p.x, xs, p.y, part, (int)p.n, (int)p.k, (int)p.m, pl.kchunks, (int)pl.grid_x,          \
-                           (int)pl.grid_y);                                                                   \
+                           (int)pl.grid_y, xcd);                                                              \
     else
             DMC_GEMM(1, true, 8) DMC_GEMM(1, false, 8) DMC_GEMM(2, false, 8) DMC_GEMM(4, false, 8)
             DMC_GEMM(2, false, 4) DMC_GEMM(4, false, 4) DMC_GEMM(2, true, 8) DMC_GEMM(4, true, 8)
