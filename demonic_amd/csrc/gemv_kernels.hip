@@ -1255,6 +1255,20 @@ constexpr int kWidePitch = 128;
 // (11-24% of the MFMA kernels' LDS cycles lost to conflicts).
 __device__ __forceinline__ int swz(int r, int p) { return r * 128 + ((p ^ ((r >> 1) & 7)) << 4); }
 
+// Chunk order of the MFMA layouts.  A workgroup streams its weight rows
+// one 128-byte column of lines (64 k) at a time; with every workgroup at
+// the same k the whole device reads addresses that differ only above the
+// row pitch, which for power-of-two rows (K = 4096: 8 KiB) meets a few HBM
+// channels at a time.  Workgroup b therefore starts at chunk 5b mod n and
+// wraps: on C4's W [128256, 4096] the read pattern alone streams in 150 us
+// rotated against 178 in step (a plain read of the same bytes: 145).  The
+// MFMA sums are taken in that order; the zero rule and the tiny-row chains
+// recompute in k order, so only rounding inside the bound changes.
+__device__ __forceinline__ int chunk_rotation(uint32_t b, int n) {
+    return n > 0 ? (int)((b * 5u) % (uint32_t)n) : 0;
+}
+__device__ __forceinline__ int rotate_chunk(int c, int s0, int n) { return c + s0 >= n ? c + s0 - n : c + s0; }
+
 __global__ void __launch_bounds__(512)
 gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                          int K, int M) {
@@ -1292,7 +1306,9 @@ gemv_rd_mfma_wide_kernel(const uint16_t *__restrict__ W, const float *__restrict
         u32x4 w[4];
         float x[8];
     };
+    const int s0 = chunk_rotation(blockIdx.x, nchunks);
     auto load = [&](int c, Regs &r) {
+        c = rotate_chunk(c, s0, nchunks);
 #pragma unroll
         for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + (uint32_t)c * 128u);
         if (xlive) {
@@ -1488,8 +1504,9 @@ gemv_rd_mfma_gemm_kernel(const uint16_t *__restrict__ W, const float *__restrict
         u32x4 w[4];
         u32x4 x[kXPer][XQ];
     };
+    const int s0 = chunk_rotation(bx, nchunks);
     auto load = [&](int c, Regs &r) {
-        const uint32_t cb = (uint32_t)(c0 + c) * 128u;
+        const uint32_t cb = (uint32_t)(c0 + rotate_chunk(c, s0, nchunks)) * 128u;
 #pragma unroll
         for (int j = 0; j < 4; ++j) r.w[j] = load_w16(rs, soff[j] + cb);
 #pragma unroll
@@ -3220,11 +3237,11 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
     // MFMA kernels for skinny M >= 2: packed rows, k a multiple of 64.  The
-    // layout, by measurement on MI355X: rows16 with compact x for M <= 8 (C4
-    // m = 2..4: 155-167 us against 170-214 for the wide layout; m = 8: 164-165
-    // against 166 on the gemm layout and 173-174 on the wide one); from 9
-    // rows the gemm layout or, on matrices it streams fast enough, rows16
-    // (below).  The wide layout is kept for DMC_HIP_RD_MFMA_KIND=6.
+    // layout, by measurement on MI355X: rows16 with compact x for M <= 5 (C4
+    // m = 2..4: 152-156 us against 158-160 for the gemm and wide layouts) and
+    // up to M = 8 on matrices up to 256 MiB; from there the gemm layout or,
+    // on matrices it streams fast enough, rows16 (below).  The wide layout is
+    // kept for DMC_HIP_RD_MFMA_KIND=6.
     // (A third layout, 16-row tiles with k split over the waves, measured
     // 1.2-2.7x slower than rows16 on every shape and was removed.)
     // From 3 activation rows, or from 2 where the streaming kernel does not
@@ -3270,7 +3287,15 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         const int64_t small_cap = wbytes <= ((int64_t)32 << 20) ? ((int64_t)128 << 20) : ((int64_t)80 << 20);
         const bool small = gy * wbytes <= small_cap;
         const bool r16_mid = p.m <= 16 && wbytes <= (int64_t)env_int("DMC_HIP_RD_R16_MID_MIB", 128) << 20;
-        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m <= 8 || small || r16_mid ? 7 : 8);
+        // From 6 activation rows on matrices above 256 MiB the gemm layout
+        // (its k order rotated per workgroup, chunk_rotation) beats rows16
+        // (same box, rows16 / gemm, us: C4 m = 6 / 8 160.8 / 165.3 against
+        // 159.7 / 160.5; [14336,14336] m = 6 / 8 75.2 / 77.6 against 67.6 /
+        // 68.3); at 224 MiB it does not ([28672,4096] m = 6 / 8 41.1 / 41.6
+        // against 47.1 / 48.0: 112 row blocks, so the gemm layout splits k),
+        // nor at m = 4 / 5 on C4 (156.5 / 158.0 against 160.1 / 159.2).
+        const int gemm_min_m = env_int("DMC_HIP_RD_GEMM_MIN_M", wbytes > ((int64_t)256 << 20) ? 6 : 9);
+        const int kind = env_int("DMC_HIP_RD_MFMA_KIND", p.m < gemm_min_m || small || r16_mid ? 7 : 8);
         const bool rows256_fit = (int64_t)kWideRows * p.k * 2 <= INT32_MAX;  // 256-row buffer range
         const bool planes_fit = (int64_t)6 * p.m * p.k <= INT32_MAX;          // x planes' buffer range
         mp.mkind = (kind == 6 || (kind == 8 && planes_fit)) && rows256_fit ? kind : 7;

@@ -186,7 +186,7 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     assert (p.slices, p.mt) == (7, 1), p   # the streaming kernel, one activation row per pass
     monkeypatch.delenv("DMC_HIP_RD_MFMA_MIN_M")
     # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
-    # (two 16-row blocks per workgroup, 4 activation rows); 9..16 rows on the LM
+    # (two 16-row blocks per workgroup, 4 activation rows); 6..16 rows on the LM
     # head: the gemm layout with 16-row tiles, x split in the kernel, k in one
     # slice (no workspace)
     for m in (3, 4):
@@ -196,10 +196,12 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
     monkeypatch.delenv("DMC_HIP_RD_MFMA_MIN_M")
-    for m in (5, 8):  # two 16-row blocks per workgroup
-        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
-        assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
-    for m in (9, 16):
+    p = d.plan("rd", 5, 4096, 128256, x_addr=256, w_addr=256)  # two 16-row blocks per workgroup
+    assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 8, 32, 8, 4008), p
+    # 6..8 rows: the gemm layout on matrices above 256 MiB, rows16 up to 256 MiB
+    assert d.plan("rd", 8, 4096, 28672, x_addr=256, w_addr=256).slices == -7
+    assert d.plan("rd", 6, 14336, 14336, x_addr=256, w_addr=256).slices == -8
+    for m in (6, 8, 9, 16):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x, p.workspace_bytes) == \
             (-8, 16, 256, 8, 501, 0), p

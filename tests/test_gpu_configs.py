@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 
 # M -> (kind, rows per workgroup) the real C4 shape must plan: kind is the
 # streaming kernel's windows per lane (> 0) or -(MFMA layout) (7 rows16, 8 gemm)
-C4_PLANS = {1: (1, 4), 2: (1, 16), 4: (-7, 32), 8: (-7, 32), 12: (-8, 256), 16: (-8, 256)}
+C4_PLANS = {1: (1, 4), 2: (1, 16), 4: (-7, 32), 6: (-8, 256), 8: (-8, 256), 12: (-8, 256), 16: (-8, 256)}
 
 
 @pytest.fixture(scope="module")
