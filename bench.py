@@ -455,6 +455,28 @@ def extended(d, W, reps: int) -> dict:
         out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
         s.free()
+    # One GPU's share of C2 under 8-way tensor parallelism (rows of gate/up,
+    # k of down split eight ways): W[1792,4096] and W[4096,1792], 14.7 MB
+    # each, 20 rotating copies (294 MB between reuses, above the 256 MB
+    # cache).  Against the time 8 TB/s would take (`ideal_us`) and an empty
+    # launch (`floor_us`): at this size a launch is mostly dispatch.
+    floor_us = batch_us(d, lambda i: d.probe_read(None, 0), 200)
+    rng = np.random.default_rng(8)
+    for label, n, k in (("TP8 gate/up rd W[1792,4096]", 1792, 4096), ("TP8 down rd W[4096,1792]", 4096, 1792)):
+        w = W_bf16(rng, n, k)
+        x = rng.standard_normal(k).astype(np.float32)
+        s = Rotating(d, w, x, 20, n_out=n)
+        f = lambda i: d.gemv_rd(s.x, s.w[i % 20], s.y, 1, k, n)  # noqa: E731
+        f(0)
+        us = batch_us(d, f, 200)
+        read_us = batch_us(d, lambda i: d.probe_read(s.w[i % 20]), 200)
+        gbs = b_alg(n, k) / (us * 1e-6) / 1e9
+        out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                      "ideal_us": round(b_alg(n, k) / PEAK_GBS / 1e3, 3), "floor_us": round(floor_us, 3),
+                      "read_probe_us": round(read_us, 3)}
+        log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}  (ideal {out[label]['ideal_us']:.2f}, "
+            f"empty launch {floor_us:.2f}, read probe {read_us:.2f})")
+        s.free()
     # C2's shapes at a few activation rows (MFMA kernels)
     for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
         n, k = w.shape

@@ -279,11 +279,12 @@ int32_t dmc_hip_f32_to_bf16(int64_t src_dev, int64_t dst_dev, int64_t n);
 int32_t dmc_hip_bf16_transpose_2d(int64_t src_dev, int64_t dst_dev, int64_t m, int64_t n);
 
 /* HIP graphs of the library stream.  Between capture_begin and capture_end,
- * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs whose
- * workspace -- column-stream split-K partials, or x's bf16 planes and partial
- * sums for row-dot on the gemm layout (from m = 9 on matrices above 80 MiB) --
- * is already large enough, i.e. after one uncaptured
- * call of the same shape) are recorded instead of run; capture_end returns an
+ * device-pointer GEMVs (dmc_hip_gemv_rd, _gemv_rd_grouped, _gemv_cs) are
+ * recorded instead of run, provided that any plan whose dmc_hip_plan
+ * workspace_bytes > 0 (column-stream split-K partials; row-dot k-slice
+ * partials on the rows16 and gemm layouts, or x's bf16 planes) already fits
+ * the library workspace, i.e. after one uncaptured call of the same shape;
+ * capture_end returns an
  * executable graph (0 on error: an entry that allocates or waits was called
  * while capturing) that graph_launch replays on the library stream.  While
  * any graph is alive, a workspace outgrown by a later call stays allocated

@@ -928,6 +928,42 @@ def test_graph_replay_after_workspace_growth(hip, monkeypatch):
             b.free()
 
 
+def test_graph_replay_rows16_k_split(hip):
+    """A rows16 plan that splits k (C2 down at m = 4: partial sums in the
+    library workspace, then the slice-sum launch), captured after one
+    uncaptured call of the same shape, replayed three times with new
+    activations uploaded eagerly in between: every replay must match the
+    reference (sampled rows, every activation row)."""
+    n, k, m = 4096, 14336, 4
+    p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
+    assert p.slices == -7 and p.workspace_bytes > 0, p
+    rng = np.random.default_rng(77)
+    w = W.bf16_rne(np.float32(0.02) * rng.standard_normal((n, k)).astype(np.float32))
+    rows = np.unique(np.r_[0, n - 1, rng.integers(0, n, 96), np.arange(15, n, 512)])
+    dw, dx, dy = hip.DeviceBuffer.from_numpy(w), hip.DeviceBuffer(4 * m * k), hip.DeviceBuffer(4 * m * n)
+    try:
+        dx.upload(rng.standard_normal((m, k)).astype(np.float32))
+        hip.gemv_rd(dx, dw, dy, m, k, n)  # sizes the workspace for this shape
+        hip.synchronize()
+        g = hip.Graph()
+        with g:
+            hip.gemv_rd(dx, dw, dy, m, k, n)
+        try:
+            for rep in range(3):
+                x = rng.standard_normal((m, k)).astype(np.float32)
+                dx.upload(x)
+                dy.upload(np.full(m * n, np.nan, np.float32))
+                g.launch()
+                hip.synchronize()
+                y = dy.download(np.float32, (m, n))
+                check(y[:, rows], ref(x, w[rows]), what=f"rows16 k-split replay {rep}")
+        finally:
+            g.destroy()
+    finally:
+        for b in (dw, dx, dy):
+            b.free()
+
+
 def test_c3_layer_schedule(hip):
     """One layer of the C3 decode sweep as the bench runs it: weights filled in
     HBM by the counter generator, q/k/v and gate/up as grouped launches, o and
