@@ -3560,10 +3560,15 @@ CsPlan plan_cs(const CsProblem &p, int num_cus) {
         const int64_t groups = pl.grid_x * std::min<int64_t>(batch, 32768) * ((p.m + pl.mt - 1) / pl.mt);
         const int gpc = pl.grid_x <= 16 ? 2 : pl.grid_x <= 24 ? 3 : 4;
         const int64_t target = (int64_t)env_int("DMC_HIP_CS_GROUPS_PER_CU", gpc) * cus;
-        const int64_t want = std::max<int64_t>(1, (target + groups - 1) / groups);
+        // No split where the column blocks alone give every CU a workgroup:
+        // the slice pass's launch costs more than the balance it buys
+        // (per-head x, W [32,128,4096]: 10.1 us on 2 slices, 7.2 on one).
+        // Row groups (narrow N) keep >= 128 k rows per slice (k/v heads
+        // W [8,4096,128]: 6.9 us on 64 slices of 64 rows, 6.6 on 32).
+        const int64_t want = groups >= cus ? 1 : std::max<int64_t>(1, (target + groups - 1) / groups);
         const int64_t krows = un ? kmax - 1 : kmax;  // rows the streaming kernel covers
         int64_t kslice = (krows + want - 1) / want;
-        kslice = std::max<int64_t>(kslice, 8 * nw);
+        kslice = std::max<int64_t>(kslice, g > 1 ? 128 : 8 * nw);
         kslice = (kslice + nw - 1) / nw * nw;
         kslice = std::max<int64_t>(nw, env_int("DMC_HIP_CS_KSLICE", (int)std::min<int64_t>(kslice, INT32_MAX)));
         pl.kslice = kslice;

@@ -329,7 +329,8 @@ def test_column_stream_batched_slices_at_odd_strides(hip):
 
 @pytest.mark.parametrize("k,n,batch,per_head,m,groups", [
     (4096, 128, 32, False, 1, 0), (4096, 64, 8, True, 1, 0), (300, 256, 3, True, 3, 0),
-    (1001, 136, 4, False, 2, 0), (2048, 1024, 2, True, 1, 8), (7, 128, 5, True, 1, 0), (4096, 8, 16, False, 1, 0)])
+    (1001, 136, 4, False, 2, 0), (2048, 1024, 2, True, 1, 8), (7, 128, 5, True, 1, 0), (4096, 8, 16, False, 1, 0),
+    (1024, 128, 256, False, 1, 0), (128, 4096, 32, True, 1, 0)])  # k unsplit: a workgroup per CU without it
 def test_column_stream_row_groups(hip, k, n, batch, per_head, m, groups, monkeypatch):
     """Batched column-stream calls on narrow N (per-head projections): the
     streaming kernel's wave splits into G row groups of 64/G lanes over
@@ -352,7 +353,7 @@ def test_column_stream_row_groups(hip, k, n, batch, per_head, m, groups, monkeyp
     w[0, :, 1] = 0x8001                      # +0.0
     w[0, :, 2] = 0                           # exact zeros: +0.0
     ls = m * k if per_head else 0
-    want_g = groups or next(g for g in (8, 4, 2, 1) if 512 // g >= n)
+    want_g = groups or next((g for g in (8, 4, 2) if 512 // g >= n), 1)
     p = hip.plan("cs", m, k, n, batch=batch, rs=k * n, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.grid_x) == (-want_g if want_g > 1 else 0, -(-n // (512 // want_g))), p
     with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
