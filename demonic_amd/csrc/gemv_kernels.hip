@@ -1120,15 +1120,56 @@ __device__ __forceinline__ void split3(float v, uint32_t &h, uint32_t &m, uint32
     l = __float_as_uint(r2) >> 16;
 }
 
-__device__ __forceinline__ void split8(const float *v, u32x4 &hi, u32x4 &mid, u32x4 &lo) {
+// Four values at once, two per dword of each plane.  Where all four are
+// finite with |x| = 0 or |x| >= 2^-133 (bf16's least subnormal), split3's
+// rule is truncation alone (no NaN quieting, no kept tiny bit, no inf
+// residual), taken here without its selects: 4 operations a value and the
+// packing instead of about 15.  The test is two reductions over the
+// magnitudes (|x| - 1 wraps 0 to the top); a lane that fails it (an inf, a
+// NaN or a tiny value among its four) takes split3.
+__device__ __forceinline__ void split4(const float *v, uint32_t *hi, uint32_t *mid, uint32_t *lo) {
+    uint32_t amax = 0, amin1 = 0xffffffffu;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int e = 0; e < 4; ++e) {
+        const uint32_t a = __float_as_uint(v[e]) & 0x7fffffffu;
+        amax = max(amax, a);
+        amin1 = min(amin1, a - 1u);
+    }
+    if (amax < 0x7f800000u && amin1 >= 0x0000ffffu) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t u0 = __float_as_uint(v[2 * q]), u1 = __float_as_uint(v[2 * q + 1]);
+            const float r10 = v[2 * q] - __uint_as_float(u0 & 0xffff0000u);
+            const float r11 = v[2 * q + 1] - __uint_as_float(u1 & 0xffff0000u);
+            const uint32_t b10 = __float_as_uint(r10), b11 = __float_as_uint(r11);
+            const uint32_t b20 = __float_as_uint(r10 - __uint_as_float(b10 & 0xffff0000u));
+            const uint32_t b21 = __float_as_uint(r11 - __uint_as_float(b11 & 0xffff0000u));
+            hi[q] = (u0 >> 16) | (u1 & 0xffff0000u);
+            mid[q] = (b10 >> 16) | (b11 & 0xffff0000u);
+            lo[q] = (b20 >> 16) | (b21 & 0xffff0000u);
+        }
+        return;
+    }
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
         uint32_t h0, m0, l0, h1, m1, l1;
         split3(v[2 * q], h0, m0, l0);
         split3(v[2 * q + 1], h1, m1, l1);
         hi[q] = h0 | (h1 << 16);
         mid[q] = m0 | (m1 << 16);
         lo[q] = l0 | (l1 << 16);
+    }
+}
+
+// Eight values: two halves of four.
+__device__ __forceinline__ void split8(const float *v, u32x4 &hi, u32x4 &mid, u32x4 &lo) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        uint32_t hq[2], mq[2], lq[2];
+        split4(v + 4 * h, hq, mq, lq);
+        hi[2 * h] = hq[0], hi[2 * h + 1] = hq[1];
+        mid[2 * h] = mq[0], mid[2 * h + 1] = mq[1];
+        lo[2 * h] = lq[0], lo[2 * h + 1] = lq[1];
     }
 }
 
@@ -1857,16 +1898,11 @@ gemv_rd_mfma_rows16_kernel(const uint16_t *__restrict__ W, const float *__restri
         u32x4 h0, md0, lo0, h1, md1, lo1;
         if (MC == 4) {
             uint32_t hq[2], mq[2], lq[2];
+            const float xv[4] = {__uint_as_float(r.x0[0]), __uint_as_float(r.x0[1]), __uint_as_float(r.x0[2]),
+                                 __uint_as_float(r.x0[3])};
+            split4(xv, hq, mq, lq);
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                uint32_t ha, ma, la, hb, mb, lb;
-                split3(__uint_as_float(r.x0[2 * q]), ha, ma, la);
-                split3(__uint_as_float(r.x0[2 * q + 1]), hb, mb, lb);
-                hq[q] = ha | (hb << 16);
-                mq[q] = ma | (mb << 16);
-                lq[q] = la | (lb << 16);
-                xmx = max_mag(xmx, hq[q]);
-            }
+            for (int q = 0; q < 2; ++q) xmx = max_mag(xmx, hq[q]);
             uint8_t *const xr = xt + swz(xm, xq >> 1) + (xq & 1) * 8;
             *reinterpret_cast<uint2 *>(xr) = uint2{hq[0], hq[1]};
             *reinterpret_cast<uint2 *>(xr + kXRows * kRows16Pitch) = uint2{mq[0], mq[1]};
