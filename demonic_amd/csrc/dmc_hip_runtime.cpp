@@ -11,7 +11,9 @@
 //     deferred calls are pending each call takes its own slice of the staging
 //     buffers, and the next synchronous call or flush copies the pending
 //     outputs to their destinations (the deferred protocol of gpu.rs:439-474,
-//     with the overlap guard of gpu.rs:491-499);
+//     with the overlap guard of gpu.rs:491-499).  A deferred call's kernels
+//     write y to device memory at its slice's offset; one copy kernel moves
+//     every pending y to pinned staging when they are materialized;
 //   * no CPU arithmetic anywhere: a device failure is reported (int entries)
 //     or fatal (the void drop-in entries), never silently recomputed.
 #include "../../include/dmc_hip.h"
@@ -131,6 +133,7 @@ struct Pending {
     const void *src;  // pinned staging
     void *dst;        // caller's out
     size_t bytes;
+    bool dev;         // y is in Ctx::dyd at src's staging offset until materialized
 };
 
 // DMC_HIP_TIME=1 accounting, after the reference's DMC_GPU_TIME (gpu.rs:45-96):
@@ -161,6 +164,7 @@ struct Ctx {
     std::vector<void *> retired_ws;  // outgrown workspaces a live graph may still use
     Buf hx, hy;             // pinned staging
     size_t hx_off = 0, hy_off = 0;
+    Buf dyd;                // deferred calls' y, in device memory at their hy staging offsets
     std::vector<Pending> pending;
     void *dummy = nullptr;  // non-null device address for zero-byte weights
     void *sink = nullptr;   // probe output words
@@ -407,10 +411,35 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     return DMC_HIP_OK;
 }
 
+// Pending outputs still in device memory (deferred calls) go to their pinned
+// staging slices in one copy kernel on the stream: the slices are bump
+// allocated, so [first, last end) covers them all, at the same offsets in
+// Ctx::dyd.  Kernels that write y straight to pinned memory (synchronous
+// calls) run ~4 us longer on C2 than ones that write it to HBM: their last
+// stores cross PCIe while the workgroups hold their slots; a copy-engine
+// transfer per call cost more still (61 against 27 us per deferred call).
+int copy_pending_out() {
+    Ctx &c = ctx();
+    size_t lo = SIZE_MAX, hi = 0;
+    for (const Pending &q : c.pending) {
+        if (!q.dev) continue;
+        const size_t at = (size_t)(static_cast<const char *>(q.src) - static_cast<const char *>(c.hy.p));
+        lo = std::min(lo, at);
+        hi = std::max(hi, at + q.bytes);
+    }
+    if (hi <= lo) return DMC_HIP_OK;
+    HIP_TRY(dmc::launch_copy_words(c.hy.dev + lo, static_cast<const char *>(c.dyd.p) + lo, (int64_t)(hi - lo),
+                                   c.stream),
+            "deferred y copy");
+    return DMC_HIP_OK;
+}
+
 int flush_locked() {
     Ctx &c = ctx();
     if (!c.tried || !c.ok) return DMC_HIP_OK;
     if (!c.pending.empty()) {
+        int rc = copy_pending_out();
+        if (rc) return rc;
         HIP_TRY(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
         for (const Pending &p : c.pending) memcpy(p.dst, p.src, p.bytes);
         c.pending.clear();
@@ -533,14 +562,22 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     const bool x_direct = x_bytes <= c.x_direct_max;
     if (x_bytes) memcpy(hx, l, x_bytes);
     if (!x_direct && (rc = ensure_dev(c.dx, x_bytes ? x_bytes : 4))) return rc;
-    if (!y_direct && (rc = ensure_dev(c.dy, y_bytes))) return rc;
-    float *const ydst = static_cast<float *>(y_direct ? static_cast<void *>(hy_dev) : c.dy.p);
+    // A deferred call's y goes to device memory at its staging offset (one
+    // copy for all of them when they are materialized, copy_pending_out).
+    // The buffer keeps the staging's size; the staging only grows while
+    // nothing is pending (see above), so no pending y is ever moved.
+    if (defer && (rc = ensure_dev(c.dyd, c.hy.cap))) return rc;
+    if (!y_direct && !defer && (rc = ensure_dev(c.dy, y_bytes))) return rc;
+    float *const ydst = static_cast<float *>(
+        defer      ? static_cast<void *>(static_cast<char *>(c.dyd.p) + (hy - static_cast<char *>(c.hy.p)))
+        : y_direct ? static_cast<void *>(hy_dev)
+                   : c.dy.p);
     const float *const xsrc = static_cast<const float *>(x_direct ? static_cast<void *>(hx_dev) : c.dx.p);
     const bool timed = c.timing && !defer;
     if (timed && !x_direct) HIP_TRY(hipEventRecord(c.tev[0], c.stream), "hipEventRecord");
     if (x_bytes && !x_direct) {
         if (c.x_kernel) {
-            HIP_TRY(dmc::launch_copy_from_host(c.dx.p, hx_dev, (int64_t)x_bytes, c.stream), "x upload");
+            HIP_TRY(dmc::launch_copy_words(c.dx.p, hx_dev, (int64_t)x_bytes, c.stream), "x upload");
         } else {
             HIP_TRY(hipMemcpyAsync(c.dx.p, hx, x_bytes, hipMemcpyHostToDevice, c.stream), "x upload");
         }
@@ -570,15 +607,16 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
         e = dmc::launch_cs(p, pl, c.ws.p, c.stream);
     }
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
-    if (!y_direct)
+    if (!y_direct && !defer)
         HIP_TRY(hipMemcpyAsync(hy, c.dy.p, y_bytes, hipMemcpyDeviceToHost, c.stream), "y readback");
     if (timed) HIP_TRY(hipEventRecord(c.tev[2], c.stream), "hipEventRecord");
     c.st.enqueue_ns += ns_since(t1);
     c.st.calls++;
     if (defer) {
-        c.pending.push_back(Pending{hy, out, y_bytes});
+        c.pending.push_back(Pending{hy, out, y_bytes, true});
         return DMC_HIP_OK;
     }
+    if (!c.pending.empty() && (rc = copy_pending_out())) return rc;
     auto t2 = std::chrono::steady_clock::now();
     HIP_TRY(hipStreamSynchronize(ctx().stream), "hipStreamSynchronize");
     const uint64_t wait_ns = (uint64_t)ns_since(t2);

@@ -2490,12 +2490,14 @@ sum_slices_kernel(const float *__restrict__ P, int64_t p_slice, int slices, floa
     if (live) Y[i] = s;
 }
 
-// ---- activation upload --------------------------------------------------------
+// ---- staging copies --------------------------------------------------------------
 //
-// The drop-in entries stage x in pinned host memory; one small grid reads it
-// over PCIe (16 bytes per thread where aligned, else 4) into device memory.
+// Words between any two device-visible ranges, one small grid (16 bytes per
+// thread where aligned, else 4): x from pinned host staging into device
+// memory (DMC_HIP_X_KERNEL), and the deferred calls' outputs from device
+// memory into pinned host staging.
 __global__ void __launch_bounds__(256)
-copy_from_host_kernel(uint32_t *__restrict__ dst, const uint32_t *__restrict__ src, int64_t words, bool v4) {
+copy_words_kernel(uint32_t *__restrict__ dst, const uint32_t *__restrict__ src, int64_t words, bool v4) {
     const int64_t stride = (int64_t)gridDim.x * 256;
     if (v4) {
         const int64_t n4 = words / 4;
@@ -3978,13 +3980,13 @@ hipError_t noalloc_scratch_resolve(void **device_address) {
 }
 
 
-hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t s) {
+hipError_t launch_copy_words(void *dst, const void *src, int64_t bytes, hipStream_t s) {
     if (bytes <= 0) return hipSuccess;
     if (bytes % 4 || !aligned(dst, 4) || !aligned(src, 4)) return hipErrorInvalidValue;
     const int64_t words = bytes / 4;
     const bool v4 = aligned(dst, 16) && aligned(src, 16);
     const unsigned groups = (unsigned)std::min<int64_t>(64, std::max<int64_t>(1, (words / (v4 ? 4 : 1) + 255) / 256));
-    hipLaunchKernelGGL(copy_from_host_kernel, dim3(groups), dim3(256), 0, s, static_cast<uint32_t *>(dst),
+    hipLaunchKernelGGL(copy_words_kernel, dim3(groups), dim3(256), 0, s, static_cast<uint32_t *>(dst),
                        static_cast<const uint32_t *>(src), words, v4);
     return hipGetLastError();
 }

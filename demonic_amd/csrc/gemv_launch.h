@@ -164,10 +164,11 @@ hipError_t launch_transpose_f32(const float *src, float *dst, int64_t rows, int6
 size_t probe_sink_bytes();
 hipError_t launch_probe_read(const void *src, int64_t bytes, void *sink, hipStream_t stream);
 
-// Copy `bytes` (a multiple of 4, both ends 4-byte aligned) from pinned host
-// memory to device memory with a kernel: the drop-in path's activation
-// upload, which a copy-engine transfer delays by its own scheduling.
-hipError_t launch_copy_from_host(void *dst, const void *src, int64_t bytes, hipStream_t stream);
+// Copy `bytes` (a multiple of 4, both ends 4-byte aligned) between two
+// device-visible ranges with a kernel: the drop-in path's activation upload
+// from pinned host memory, and the deferred outputs back to pinned staging;
+// a copy-engine transfer delays either by its own scheduling.
+hipError_t launch_copy_words(void *dst, const void *src, int64_t bytes, hipStream_t stream);
 
 // The fixed scratch of the no-allocation column-stream entry: a file-scope
 // device array of noalloc_scratch_bytes() bytes in gemv_kernels.hip.  Its
