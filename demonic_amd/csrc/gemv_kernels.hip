@@ -718,7 +718,7 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
         [&](int t, float v) { Y[(int)blockIdx.x * rpw + t] = v; });
 }
 
-// ---- RD streaming, shared x over 14 waves (M = 1, long rows) ----------------
+// ---- RD streaming, shared x over 14 waves (M = 1 or 2, long rows) -----------
 //
 // The shared-x layout with one group of NS = 14 waves splitting k instead of
 // two halves of 8: lane l of wave w owns the KV windows (j*NS + w)*64 + l,
@@ -726,29 +726,43 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 // fourth window is past K for half their lanes).  The workgroup's 16 rows
 // stream 4 at a time through two register buffers with unconditional loads
 // and no barrier until the end, where wave 0 sums each row's 14 partials
-// in wave order and rd_finish settles exact zeros.
+// in wave order and rd_finish settles exact zeros.  MT activation rows
+// (1 or 2) share each weight load; each has its own LDS copy of x (56 KiB),
+// and at MT = 2 the rows stream 2 at a time.
 constexpr int kX14Waves = 14;
+constexpr int kX14MaxK = 2 * kX14Waves * 512;  // 14336: KV <= 2
+constexpr int kX14Hi = kX14MaxK / 2;            // x in LDS as two planes of each window's halves
 
-template <int KV>
+template <int KV, int MT>
 __global__ void __launch_bounds__(64 * kX14Waves)
 gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                           int K) {
-    constexpr int NS = kX14Waves, ROWS = 4, NT = 64 * NS, RPW = 16;
-    static_assert(KV * NS * 64 * 8 <= kXldsMaxK * 7 / 8, "x windows must lie inside the LDS copy");
+    // Two rows per register buffer at MT = 2 (four would take more than the
+    // 128 registers 14 waves per CU leave each lane).
+    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : 2, NT = 64 * NS, RPW = 16;
+    static_assert(KV * NS * 64 * 8 <= kX14MaxK, "x windows must lie inside the LDS copy");
+    static_assert(2 * NT * 4 == kX14Hi, "two windows a thread fill each plane");
+    static_assert(MT == 1 || MT == 2, "activation rows");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = (int)blockIdx.x * RPW;
     const int nr = max(0, min(N, rb + RPW) - rb);
 
-    __shared__ __attribute__((aligned(16))) float xs[kXldsMaxK];
-    constexpr int kHi = kXldsMaxK / 2;
-    __shared__ float red[NS][RPW];
+    __shared__ __attribute__((aligned(16))) float xs[MT][kX14MaxK];
+    __shared__ float red[NS][MT * RPW];
 
-    const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X, (uint32_t)K * 4);
-    u32x4 xp[6];
+    // x row m into LDS: windows t, t + NT (1792 = 2 * 896), each as its two
+    // halves in the two planes.  The loads go out ahead of the weights' so
+    // that the LDS stores wait on x alone.
+    u32x4 xp[MT][4];
 #pragma unroll
-    for (int i = 0; i < 6; ++i)  // windows t, t + NT, t + 2 NT (1792 < 3 * 896)
-        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + (i >> 1) * NT) * 32u + (i & 1) * 16u, 0, 0);
+    for (int m = 0; m < MT; ++m) {
+        const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m * K, (uint32_t)K * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xp[m][i] =
+                __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + (i >> 1) * NT) * 32u + (i & 1) * 16u, 0, 0);
+    }
     uint32_t eoff[KV];
     bool has[KV];
 #pragma unroll
@@ -771,28 +785,32 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 6; ++i) {
-        const uint32_t w = threadIdx.x + (i >> 1) * NT;
-        if (w < kHi / 4) *reinterpret_cast<u32x4 *>(&xs[(i & 1) * kHi + w * 4u]) = xp[i];
-    }
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            *reinterpret_cast<u32x4 *>(&xs[m][(i & 1) * kX14Hi + (threadIdx.x + (i >> 1) * NT) * 4u]) = xp[m][i];
     __syncthreads();
-    float xr[KV][8];
+    float xr[MT][KV][8];
 #pragma unroll
-    for (int j = 0; j < KV; ++j) {
-        const int w = (j * NS + wave) * 64 + lane;
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
-        const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
-        const uint32_t sgn = has[j] ? 0u : 0x80000000u;
+    for (int m = 0; m < MT; ++m)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            xr[j][q] = __uint_as_float(a[q] | sgn);
-            xr[j][q + 4] = __uint_as_float(b[q] | sgn);
+        for (int j = 0; j < KV; ++j) {
+            const int w = (j * NS + wave) * 64 + lane;
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[m][w * 4]);
+            const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[m][kX14Hi + w * 4]);
+            const uint32_t sgn = has[j] ? 0u : 0x80000000u;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                xr[m][j][q] = __uint_as_float(a[q] | sgn);
+                xr[m][j][q + 4] = __uint_as_float(b[q] | sgn);
+            }
         }
-    }
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
-        float acc[ROWS];
+        float acc[MT][ROWS];
 #pragma unroll
-        for (int q = 0; q < ROWS; ++q) acc[q] = init;
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) acc[m][q] = init;
 #pragma unroll
         for (int j = 0; j < KV; ++j)
 #pragma unroll
@@ -800,46 +818,60 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
 #pragma unroll
                 for (int q = 0; q < ROWS; ++q) {
                     const uint32_t d = wv[q][j][e >> 1];
-                    acc[q] = fmaf(xr[j][e], (e & 1) ? widen_hi(d) : widen_lo(d), acc[q]);
+                    const float wf = (e & 1) ? widen_hi(d) : widen_lo(d);
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], wf, acc[m][q]);
                 }
 #pragma unroll
-        for (int q = 0; q < ROWS; ++q) {
-            const float s = wave_sum_dpp(acc[q]);
-            if (lane == 0) red[wave][i0 + q] = s;
-        }
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int q = 0; q < ROWS; ++q) {
+                const float s = wave_sum_dpp(acc[m][q]);
+                if (lane == 0) red[wave][m * RPW + i0 + q] = s;
+            }
     };
-    sum_rows(ba, 0);
-    load(ba, 2 * ROWS);
-    sum_rows(bb, ROWS);
-    load(bb, 3 * ROWS);
-    sum_rows(ba, 2 * ROWS);
-    sum_rows(bb, 3 * ROWS);
+#pragma unroll
+    for (int i0 = 0; i0 < RPW; i0 += 2 * ROWS) {
+        sum_rows(ba, i0);
+        if (i0 + 2 * ROWS < RPW) load(ba, i0 + 2 * ROWS);
+        sum_rows(bb, i0 + ROWS);
+        if (i0 + 3 * ROWS < RPW) load(bb, i0 + 3 * ROWS);
+    }
     __syncthreads();
+    // Outputs t < MT * nr: activation row t / nr, weight row t % nr.
     __shared__ uint64_t hits[NS + 1];
     rd_finish<NS>(
-        nr, hits,
+        MT * nr, hits,
         [&](int t) {
-            float s = red[0][t];
+            const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
+            float s = red[0][m * RPW + r];
 #pragma unroll
-            for (int w = 1; w < NS; ++w) s += red[w][t];
+            for (int w = 1; w < NS; ++w) s += red[w][m * RPW + r];
             return s;
         },
         [&](int t) {
+            const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
             bool hit = false;
 #pragma unroll
             for (int j = 0; j < KV; ++j) {
                 const int w = (j * NS + wave) * 64 + lane;
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[w * 4]);
-                const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[kHi + w * 4]);
+                const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[m][w * 4]);
+                const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[m][kX14Hi + w * 4]);
                 const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
                                      __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
                                      __uint_as_float(b[2]), __uint_as_float(b[3])};
-                hit |= window_hit(xw, load_w16(rs, eoff[j], (uint32_t)t * row_bytes));
+                hit |= window_hit(xw, load_w16(rs, eoff[j], (uint32_t)r * row_bytes));
             }
             return hit;
         },
-        [&](int t) { return chain_strided(W + (int64_t)(rb + t) * K, 1, X, K); },
-        [&](int t, float v) { Y[rb + t] = v; });
+        [&](int t) {
+            const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
+            return chain_strided(W + (int64_t)(rb + r) * K, 1, X + (int64_t)m * K, K);
+        },
+        [&](int t, float v) {
+            const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
+            Y[(int64_t)m * N + rb + r] = v;
+        });
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -3489,15 +3521,22 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // (DMC_HIP_RD_X14=0 keeps the halves everywhere).
             const int64_t g16 = (p.n + 15) / 16;
             const int xl = env_int("DMC_HIP_RD_XLDS", 1);  // 0: never; 2: wherever the kernel applies
-            const bool x14 = env_int("DMC_HIP_RD_X14", 1) != 0 && p.k <= 2 * kX14Waves * 512;
-            if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
+            const bool x14 = env_int("DMC_HIP_RD_X14", 1) != 0 && p.k <= kX14MaxK;
+            // Two activation rows on the 14-wave group too (one LDS copy of x
+            // each): the streaming kernel would hold 4 windows of both rows'
+            // x in registers, one weight row per buffer.
+            const bool x14_m2 = p.m == 2 && sp.mt == 2 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 &&
+                                env_int("DMC_HIP_RD_X14_M2", 1) != 0;
+            if ((p.m == 1 ? sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 : x14_m2) &&
                 p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) && xl != 0 &&
                 x14) {
                 sp.waves = kX14Waves;
                 sp.kvec = (int)((p.k + kX14Waves * 512 - 1) / (kX14Waves * 512));
                 sp.rows = 4;
                 sp.rpw = 16;
+                sp.mt = (int)p.m;
                 sp.grid_x = (p.n + 15) / 16;
+                sp.grid_y = 1;
             } else if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
                        p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) &&
                        xl != 0) {
@@ -3744,15 +3783,20 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
     }
     if (pl.kvec > 0 && pl.any_align) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0 && pl.waves == kX14Waves && pl.rows == 4) {
-        if (pl.rpw != 16 || p.m != 1 || pl.kvec < 1 || pl.kvec > 2 || (int64_t)pl.kvec * kX14Waves * 512 < p.k ||
-            (int64_t)16 * p.k * 2 > INT32_MAX)
+        if (pl.rpw != 16 || p.m != pl.mt || (p.m != 1 && p.m != 2) || pl.kvec < 1 || pl.kvec > 2 ||
+            (int64_t)pl.kvec * kX14Waves * 512 < p.k || p.k > kX14MaxK || (int64_t)16 * p.k * 2 > INT32_MAX)
             return hipErrorInvalidValue;
-        if (pl.kvec == 1)
-            hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<1>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s,
-                               p.w, p.x, p.y, (int)p.n, (int)p.k);
-        else
-            hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<2>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s,
-                               p.w, p.x, p.y, (int)p.n, (int)p.k);
+#define DMC_X14(KV, MT)                                                                                        \
+    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<KV, MT>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s, \
+                       p.w, p.x, p.y, (int)p.n, (int)p.k)
+        switch (pl.kvec * 10 + (int)p.m) {
+        case 11: DMC_X14(1, 1); break;
+        case 21: DMC_X14(2, 1); break;
+        case 12: DMC_X14(1, 2); break;
+        case 22: DMC_X14(2, 2); break;
+        default: return hipErrorInvalidValue;
+        }
+#undef DMC_X14
         return hipGetLastError();
     }
     if (pl.kvec > 0 && pl.waves == 16) {

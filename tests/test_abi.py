@@ -180,6 +180,14 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 16, 8016), p
     p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
+    # long rows at M = 2: the 14-wave shared-x kernel with one LDS copy of x per
+    # activation row (DMC_HIP_RD_X14_M2=0: the streaming kernel)
+    p = d.plan("rd", 2, 14336, 4096, x_addr=256, w_addr=256)
+    assert (p.waves, p.slices, p.mt, p.rows_per_group, p.grid_x) == (14, 2, 2, 16, 256), p
+    monkeypatch.setenv("DMC_HIP_RD_X14_M2", "0")
+    p = d.plan("rd", 2, 14336, 4096, x_addr=256, w_addr=256)
+    assert (p.waves, p.mt) == (8, 2), p
+    monkeypatch.delenv("DMC_HIP_RD_X14_M2")
     assert d.plan("rd", 2, 28672, 32768, x_addr=256, w_addr=256).slices == -7
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "3")
     p = d.plan("rd", 2, 28672, 32768, x_addr=256, w_addr=256)
