@@ -188,6 +188,10 @@ def main(argv=None) -> int:
     ap.add_argument("--no-graph", action="store_true",
                     help="launch every batch one host call at a time, HIP graphs left out entirely "
                          "(for profiled runs; the timed C2 steps then run eagerly too)")
+    ap.add_argument("--steps-only", action="store_true",
+                    help="run the warm-up and the timed steps alone: no per-shape batches, read probe, "
+                         "dispatch floor or drop-in calls (for the kernel-trace profile, whose per-kernel "
+                         "averages are then the timed steps' own)")
     ap.add_argument("--no-c3", action="store_true",
                     help="leave C3 out of --extended (its HIP-graph replays are not traced: under rocprofv3 "
                          "one aborted the queue with a malformed-packet error)")
@@ -266,13 +270,14 @@ def main(argv=None) -> int:
     # its own, ~7-30 us on these boxes, that a short batch would charge to
     # its kernels)
     reps = max(a.steps, 200)
-    us = {}
-    for nm in order:
-        batch_us(d, lambda i, nm=nm: launch(nm, i), reps)
-        us[nm] = batch_us(d, lambda i, nm=nm: launch(nm, i), reps)
-    read_us = {nm: batch_us(d, lambda i, nm=nm: d.probe_read(shapes[nm].w[i % a.copies]), reps)
-               for nm in order}
-    floor_us = batch_us(d, lambda i: d.probe_read(None, 0), reps)
+    us, read_us, floor_us = {}, None, None
+    if not a.steps_only:
+        for nm in order:
+            batch_us(d, lambda i, nm=nm: launch(nm, i), reps)
+            us[nm] = batch_us(d, lambda i, nm=nm: launch(nm, i), reps)
+        read_us = {nm: batch_us(d, lambda i, nm=nm: d.probe_read(shapes[nm].w[i % a.copies]), reps)
+                   for nm in order}
+        floor_us = batch_us(d, lambda i: d.probe_read(None, 0), reps)
 
     # timed region: K steps, each the two GEMVs, inputs resident, replayed
     # from a HIP graph captured once (after one untimed replay); with
@@ -327,7 +332,7 @@ def main(argv=None) -> int:
     launch_us = ev_ms * 1e3 / (a.steps * len(order))
     achieved = (b_up + b_down) / 2 / (launch_us * 1e-6) / 1e9
     w_bytes = {nm: 2 * shapes[nm].shape[0] * shapes[nm].shape[1] for nm in order}
-    read_gbs = sum(w_bytes.values()) / (sum(read_us.values()) * 1e-6) / 1e9
+    read_gbs = sum(w_bytes.values()) / (sum(read_us.values()) * 1e-6) / 1e9 if read_us else None
     plans = {nm: d.plan("rd", 1, shapes[nm].shape[1], shapes[nm].shape[0],
                         x_addr=shapes[nm].x.addr, w_addr=shapes[nm].w[0].addr) for nm in order}
     roofline = {
@@ -338,7 +343,7 @@ def main(argv=None) -> int:
         "bytes_per_launch": {"up": b_up, "down": b_down},
         "avg_launch_us": round(launch_us, 3),
         "us_per_launch": {nm: round(u, 3) for nm, u in us.items()},
-        "frac_of_read_ceiling": round(achieved / read_gbs, 4),
+        "frac_of_read_ceiling": round(achieved / read_gbs, 4) if read_gbs else None,
     }
     for b in shapes.values():
         b.free()
@@ -363,10 +368,11 @@ def main(argv=None) -> int:
                                   "rows_per_step": p.rows_or_rw, "groups": p.grid_x}
                              for nm, p in plans.items()}},
         "roofline": roofline,
-        "read_ceiling": {"GB/s": round(read_gbs, 1), "us": {nm: round(u, 3) for nm, u in read_us.items()},
-                         "frac_of_peak": round(read_gbs / PEAK_GBS, 4)},
-        "dispatch_floor_us": round(floor_us, 3),
-        "dropin": dropin(d, W, 300),
+        "read_ceiling": None if read_us is None else {
+            "GB/s": round(read_gbs, 1), "us": {nm: round(u, 3) for nm, u in read_us.items()},
+            "frac_of_peak": round(read_gbs / PEAK_GBS, 4)},
+        "dispatch_floor_us": None if floor_us is None else round(floor_us, 3),
+        "dropin": None if a.steps_only else dropin(d, W, 300),
         "cpu_baseline": None if a.no_cpu else cpu_baseline(a.cpu_seconds),
     }
     if a.extended:
