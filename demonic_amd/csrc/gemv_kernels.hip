@@ -718,60 +718,59 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
         [&](int t, float v) { Y[(int)blockIdx.x * rpw + t] = v; });
 }
 
-// ---- RD streaming, shared x over 14 waves (M = 1 or 2, long rows) -----------
+// ---- RD streaming, one group of 14 waves (M = 1 to 4, long rows) -------------
 //
-// The shared-x layout with one group of NS = 14 waves splitting k instead of
-// two halves of 8: lane l of wave w owns the KV windows (j*NS + w)*64 + l,
-// so at K = 14336 (KV = 2) every load instruction carries data (the halves'
-// fourth window is past K for half their lanes).  The workgroup's 16 rows
-// stream 4 at a time through two register buffers with unconditional loads
-// and no barrier until the end, where wave 0 sums each row's 14 partials
-// in wave order and rd_finish settles exact zeros.  MT activation rows
-// (1 or 2) share each weight load; each has its own LDS copy of x (56 KiB),
-// and at MT = 2 the rows stream 2 at a time.
+// One group of NS = 14 waves splits k: lane t of the workgroup owns the KV
+// windows t + j*NT of 8 elements (NT = 896 threads), so at K = 14336 (KV = 2)
+// every load instruction carries data.  A window's x is the lane's alone, so
+// each lane loads its MT activation rows' windows straight into registers
+// (56 KiB of x per workgroup, one workgroup per CU).  The workgroup's 16 rows
+// stream ROWS at a time through two register buffers with unconditional
+// loads and no barrier until the end, where wave 0 sums each row's 14
+// partials in wave order and rd_finish settles exact zeros (its rare path
+// reads x again from memory).  Every weight load feeds all MT activation
+// rows' fma chains.
 constexpr int kX14Waves = 14;
 constexpr int kX14MaxK = 2 * kX14Waves * 512;  // 14336: KV <= 2
-constexpr int kX14Hi = kX14MaxK / 2;            // x in LDS as two planes of each window's halves
+constexpr int kX14MaxM = 4;
 
 template <int KV, int MT>
 __global__ void __launch_bounds__(64 * kX14Waves)
 gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                           int K) {
-    // Two rows per register buffer at MT = 2 (four would take more than the
-    // 128 registers 14 waves per CU leave each lane).
-    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : 2, NT = 64 * NS, RPW = 16;
-    static_assert(KV * NS * 64 * 8 <= kX14MaxK, "x windows must lie inside the LDS copy");
-    static_assert(2 * NT * 4 == kX14Hi, "two windows a thread fill each plane");
-    static_assert(MT == 1 || MT == 2, "activation rows");
+    // Rows per register buffer: 4 at MT = 1, 2 at MT = 2, 1 at MT = 3 and 4
+    // with two windows (a lane has 128 registers at 14 waves per CU; x takes
+    // 8 * KV * MT of them).
+    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : MT == 2 || KV == 1 ? 2 : 1, NT = 64 * NS, RPW = 16;
+    static_assert(KV * NS * 64 * 8 <= kX14MaxK, "windows");
+    static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = (int)blockIdx.x * RPW;
     const int nr = max(0, min(N, rb + RPW) - rb);
 
-    __shared__ __attribute__((aligned(16))) float xs[MT][kX14MaxK];
     __shared__ float red[NS][MT * RPW];
 
-    // x row m into LDS: windows t, t + NT (1792 = 2 * 896), each as its two
-    // halves in the two planes.  The loads go out ahead of the weights' so
-    // that the LDS stores wait on x alone.
-    u32x4 xp[MT][4];
+    // The lane's x windows, both 16-byte halves, issued ahead of the weights.
+    u32x4 xp[MT][KV][2];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m * K, (uint32_t)K * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            xp[m][i] =
-                __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + (i >> 1) * NT) * 32u + (i & 1) * 16u, 0, 0);
+        for (int j = 0; j < KV; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                xp[m][j][h] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + j * NT) * 32u + h * 16u, 0, 0);
     }
     uint32_t eoff[KV];
     bool has[KV];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
-        const int e = ((j * NS + wave) * 64 + lane) * 8;
+        const int e = (threadIdx.x + j * NT) * 8;
         has[j] = e < K;
         eoff[j] = has[j] ? (uint32_t)e * 2 : kOutOfRange;
     }
-    const float init = (wave * 64 + lane) * 8 < K ? 0.0f : -0.0f;
+    const float init = (int)threadIdx.x * 8 < K ? 0.0f : -0.0f;
     const uint32_t row_bytes = (uint32_t)K * 2;
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * K, (uint32_t)nr * row_bytes);
     u32x4 ba[ROWS][KV], bb[ROWS][KV];
@@ -784,25 +783,16 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
     load(ba, 0);
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<u32x4 *>(&xs[m][(i & 1) * kX14Hi + (threadIdx.x + (i >> 1) * NT) * 4u]) = xp[m][i];
-    __syncthreads();
     float xr[MT][KV][8];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int j = 0; j < KV; ++j) {
-            const int w = (j * NS + wave) * 64 + lane;
-            const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[m][w * 4]);
-            const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[m][kX14Hi + w * 4]);
             const uint32_t sgn = has[j] ? 0u : 0x80000000u;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                xr[m][j][q] = __uint_as_float(a[q] | sgn);
-                xr[m][j][q + 4] = __uint_as_float(b[q] | sgn);
+                xr[m][j][q] = __uint_as_float(xp[m][j][0][q] | sgn);
+                xr[m][j][q + 4] = __uint_as_float(xp[m][j][1][q] | sgn);
             }
         }
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
@@ -851,12 +841,13 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
         },
         [&](int t) {
             const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
+            const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m * K, (uint32_t)K * 4);
             bool hit = false;
 #pragma unroll
             for (int j = 0; j < KV; ++j) {
-                const int w = (j * NS + wave) * 64 + lane;
-                const u32x4 a = *reinterpret_cast<const u32x4 *>(&xs[m][w * 4]);
-                const u32x4 b = *reinterpret_cast<const u32x4 *>(&xs[m][kX14Hi + w * 4]);
+                const uint32_t xo = (threadIdx.x + j * NT) * 32u;
+                const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+                const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
                 const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
                                      __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
                                      __uint_as_float(b[2]), __uint_as_float(b[3])};
@@ -3306,6 +3297,35 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
+    // Three activation rows on long rows (4096 < K <= 14336, packed 128-bit
+    // rows, 16-row workgroups in whole rounds of one per CU, as at M = 1 and
+    // 2 below): the 14-wave streaming kernel with every activation row's x
+    // in registers, W read once and no x split.  Same box, C2 down, 14-wave /
+    // rows16: m = 3 21.0 / 21.7-21.8 us, m = 4 22.3-22.5 / 21.9-22.1 (one
+    // weight row per buffer at m = 4: four would spill), so M = 4 stays on
+    // rows16 (DMC_HIP_RD_X14_MAX_M: 2 turns this off, 4 takes M = 4 too).
+    // An explicit DMC_HIP_RD_MFMA_KIND keeps the MFMA layout it names;
+    // DMC_HIP_RD_XLDS=2 takes the kernel wherever it applies.
+    {
+        const int64_t g16 = (p.n + 15) / 16;
+        const int xl = env_int("DMC_HIP_RD_XLDS", 1);
+        if (p.m >= 3 && p.m <= std::min(kX14MaxM, env_int("DMC_HIP_RD_X14_MAX_M", 3)) && pl.vec == 8 &&
+            p.ldw == p.k && p.ldx == p.k && p.ldy == p.n && p.k > 0 && p.k <= kX14MaxK && xl != 0 &&
+            env_int("DMC_HIP_RD_X14", 1) != 0 && env_int("DMC_HIP_RD_MFMA_KIND", 0) == 0 &&
+            (xl == 2 || (p.k > 4096 && g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus)))) {
+            RdPlan xp{};
+            xp.vec = 8;
+            xp.waves = kX14Waves;
+            xp.kvec = (int)((p.k + kX14Waves * 512 - 1) / (kX14Waves * 512));
+            xp.rows = 4;
+            xp.rpw = 16;
+            xp.mt = (int)p.m;
+            xp.grid_x = g16;
+            xp.grid_y = 1;
+            return xp;
+        }
+    }
+
     // MFMA kernels for skinny M >= 2: packed rows, k a multiple of 64.  The
     // layout, by measurement on MI355X: rows16 with compact x for M <= 5 (C4
     // m = 2..4: 152-156 us against 158-160 for the gemm and wide layouts) and
@@ -3522,9 +3542,9 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             const int64_t g16 = (p.n + 15) / 16;
             const int xl = env_int("DMC_HIP_RD_XLDS", 1);  // 0: never; 2: wherever the kernel applies
             const bool x14 = env_int("DMC_HIP_RD_X14", 1) != 0 && p.k <= kX14MaxK;
-            // Two activation rows on the 14-wave group too (one LDS copy of x
-            // each): the streaming kernel would hold 4 windows of both rows'
-            // x in registers, one weight row per buffer.
+            // Two activation rows on the 14-wave group too: the 8-wave
+            // streaming kernel would hold 4 windows of both rows' x in
+            // registers, one weight row per buffer.
             const bool x14_m2 = p.m == 2 && sp.mt == 2 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 &&
                                 env_int("DMC_HIP_RD_X14_M2", 1) != 0;
             if ((p.m == 1 ? sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 : x14_m2) &&
@@ -3783,7 +3803,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
     }
     if (pl.kvec > 0 && pl.any_align) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0 && pl.waves == kX14Waves && pl.rows == 4) {
-        if (pl.rpw != 16 || p.m != pl.mt || (p.m != 1 && p.m != 2) || pl.kvec < 1 || pl.kvec > 2 ||
+        if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec < 1 || pl.kvec > 2 ||
             (int64_t)pl.kvec * kX14Waves * 512 < p.k || p.k > kX14MaxK || (int64_t)16 * p.k * 2 > INT32_MAX)
             return hipErrorInvalidValue;
 #define DMC_X14(KV, MT)                                                                                        \
@@ -3794,6 +3814,10 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         case 21: DMC_X14(2, 1); break;
         case 12: DMC_X14(1, 2); break;
         case 22: DMC_X14(2, 2); break;
+        case 13: DMC_X14(1, 3); break;
+        case 23: DMC_X14(2, 3); break;
+        case 14: DMC_X14(1, 4); break;
+        case 24: DMC_X14(2, 4); break;
         default: return hipErrorInvalidValue;
         }
 #undef DMC_X14

@@ -593,8 +593,9 @@ def test_rows16_split_k_on_c2(hip, shape, m, monkeypatch):
     w[5, : k // 2] = 0x3F80   # +1 then -1 against row 1's constant x: a cancellation
     w[5, k // 2:] = 0xBF80
     tiles, grid_x, ks = R16_C2_PLANS[(shape, m)]
-    if m > 16:
-        monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
+    # rows16 named: the default above 16 rows is the gemm layout, and at 3
+    # rows on down the 14-wave streaming kernel
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     with hip.DeviceBuffer.from_numpy(w) as dw, hip.DeviceBuffer.from_numpy(x) as dx, \
             hip.DeviceBuffer(4 * m * n) as dy:
         p = hip.plan("rd", m, k, n, x_addr=dx.addr, w_addr=dw.addr)
@@ -1128,19 +1129,20 @@ def _rd_dev(hip, x, w, y_init=np.nan):
         return dy.download(np.float32, (m, n))
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("n,k", X14_SHAPES)
 def test_shared_x_fourteen_waves(hip, n, k, m, monkeypatch):
-    """The shared-x layout on one group of 14 waves splitting k (the default
-    for K <= 14336; DMC_HIP_RD_XLDS=2 takes it wherever it applies), with one
-    or two activation rows (an LDS copy of x each): C2 down (two windows per
-    lane, all carrying data), a partial last workgroup (n = 4097: one row of
-    16), one window per lane (k = 4112, its last block holding 16 elements),
+    """One group of 14 waves splitting k (the default for 4096 < K <= 14336
+    at M = 1 to 4; DMC_HIP_RD_XLDS=2 takes it wherever it applies), with one
+    to four activation rows (x in registers): C2 down (two windows per lane,
+    all carrying data), a partial last workgroup (n = 4097: one row of 16),
+    one window per lane (k = 4112, its last block holding 16 elements),
     fewer rows than one workgroup (n = 6), and 1024 workgroups.  Edge data;
     the oracle's result within the parity rule and, row by row, the
     elementwise bound; two launches bit for bit alike."""
     x, w = case(m, k, n, seed=7100 + n + k + m, edge=True)
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
+    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "4")
     p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
     assert (p.waves, p.rows_per_group, p.slices, p.mt) == (14, 16, 1 if k <= 7168 else 2, m), p
     y = _rd_dev(hip, x, w)
@@ -1148,19 +1150,19 @@ def test_shared_x_fourteen_waves(hip, n, k, m, monkeypatch):
     check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"x14 m={m} n={n} k={k}")
 
 
-@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("k", [4112, 14336])
 def test_shared_x_fourteen_waves_zero_rule(hip, k, m, monkeypatch):
-    """Exact zeros on the 14-wave kernel, one or two activation rows:
+    """Exact zeros on the 14-wave kernel, one to four activation rows:
     underflowing products of one sign (zero signs from the chain) and the
     rows of zero_rows' patterns (order-dependent zeros, exact-zero products)
     -- bit for bit the reference."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
+    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "4")
     n = 4096
     assert hip.plan("rd", m, k, n, x_addr=256, w_addr=256).waves == 14
     x = np.full((m, k), np.float32(-1e-38), np.float32)
-    if m == 2:
-        x[1] = -x[1]                         # the second row: the opposite zero signs
+    x[1::2] = -x[1::2]                       # odd rows: the opposite zero signs
     w = np.full((n, k), 0x0001, np.uint16)
     w[1::2, :] = 0x8001
     y_ref = ref(x, w)
@@ -1168,7 +1170,7 @@ def test_shared_x_fourteen_waves_zero_rule(hip, k, m, monkeypatch):
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
     xm, wz = zero_rows(k, 9)
     w = np.ascontiguousarray(wz[np.arange(n) % 9])
-    xm = np.ascontiguousarray(xm[2:2 + m])
+    xm = np.ascontiguousarray(xm[(2 + np.arange(m)) % 4])
     y_ref = ref(xm, w)
     y = _rd_dev(hip, xm, w)
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
