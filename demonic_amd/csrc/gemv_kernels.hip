@@ -116,6 +116,66 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Four values of every lane summed over the wave as one reduce-scatter
+// instead of four reductions: lane pairs exchange half of what they hold
+// (xor 1: two values left, xor 2: one), so lane class c = lane mod 4 sums
+// value 2 (c & 1) + (c >> 1) over its quad; rotations by 4 and 8 within
+// each row of 16 lanes and the two lane swaps across rows (xor 16, xor 32)
+// finish it.  Lane c (c < 4) returns the total of that value; the order of
+// the additions is fixed.  15 instructions against 4 x 11.
+__device__ __forceinline__ float wave_sum4_dpp(float a0, float a1, float a2, float a3) {
+    const bool b0 = (threadIdx.x & 1) != 0, b1 = (threadIdx.x & 2) != 0;
+    const float c0 = (b0 ? a2 : a0) + dpp_mov<0xb1>(b0 ? a0 : a2);  // quad_perm [1,0,3,2]
+    const float c1 = (b0 ? a3 : a1) + dpp_mov<0xb1>(b0 ? a1 : a3);
+    float d = (b1 ? c1 : c0) + dpp_mov<0x4e>(b1 ? c0 : c1);         // quad_perm [2,3,0,1]
+    d += dpp_mov<0x124>(d);                                         // row_ror:4
+    d += dpp_mov<0x128>(d);                                         // row_ror:8
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+    d = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// Two values of every lane summed over the wave the same way: one exchange
+// (xor 1) leaves lane class c = lane mod 2 with value c; lane c (c < 2)
+// returns its total.
+__device__ __forceinline__ float wave_sum2_dpp(float a0, float a1) {
+    const bool b0 = (threadIdx.x & 1) != 0;
+    float d = (b0 ? a1 : a0) + dpp_mov<0xb1>(b0 ? a0 : a1);  // quad_perm [1,0,3,2]
+    d += dpp_mov<0x4e>(d);                                   // quad_perm [2,3,0,1]
+    d += dpp_mov<0x124>(d);                                  // row_ror:4
+    d += dpp_mov<0x128>(d);                                  // row_ror:8
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+    d = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(d), __float_as_uint(d), false, false);
+    return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
+// The V per-lane values a[0..V) summed over the wave, four (or the last two)
+// per reduce-scatter: store(v, total) runs in the one lane that holds value
+// v's total.
+template <int V, class Store>
+__device__ __forceinline__ void wave_sums(const float (&a)[V], Store store) {
+    const int lane = threadIdx.x & 63;
+    if constexpr (V == 1) {
+        const float s = wave_sum_dpp(a[0]);
+        if (lane == 0) store(0, s);
+    } else {
+#pragma unroll
+        for (int g = 0; g < V; g += 4) {
+            if (V - g == 2) {
+                const float s = wave_sum2_dpp(a[g], a[g + 1]);
+                if (lane < 2) store(g + lane, s);
+            } else {
+                const float s = wave_sum4_dpp(a[g], g + 1 < V ? a[g + 1] : 0.0f, g + 2 < V ? a[g + 2] : 0.0f,
+                                              g + 3 < V ? a[g + 3] : 0.0f);
+                const int v = g + 2 * (lane & 1) + ((lane >> 1) & 1);
+                if (lane < 4 && v < V) store(v, s);
+            }
+        }
+    }
+}
+
 // 128-bit weight loads through a buffer resource, marked nontemporal: weights
 // are streamed once per launch, so they should not displace x or y in the
 // caches.  (Measured on MI355X: ~8% more bandwidth than plain global loads.)
@@ -526,6 +586,8 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
                 }
+        // Value v of the step: activation row v / ROWS, weight row i0 + v % ROWS.
+        float a[MT * ROWS];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -535,9 +597,11 @@ gemv_rd_stream_kernel(const RdGroupArgs ga, int K, int M, int rpw) {
                 for (int j = 0; j < KV; ++j)
 #pragma unroll
                     for (int d = 0; d < 4; ++d) nz |= wv[q][j][d] & xm[m][j][d];
-                const float s = wave_sum_dpp(zero_fold(acc[m][q], nz != 0));
-                if (lane == 0 && i0 + q < nr) red[wave][m][i0 + q] = s;
+                a[m * ROWS + q] = zero_fold(acc[m][q], nz != 0);
             }
+        wave_sums(a, [&](int v, float s) {
+            if (i0 + v % ROWS < nr) red[wave][v / ROWS][i0 + v % ROWS] = s;
+        });
     };
     // Rows [i0, i0 + ROWS) sit in one buffer while the next ROWS rows load
     // into the other; the first step is peeled so that pad_x follows the
@@ -738,10 +802,10 @@ template <int KV, int MT>
 __global__ void __launch_bounds__(64 * kX14Waves)
 gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                           int K) {
-    // Rows per register buffer: 4 at MT = 1, 2 at MT = 2, 1 at MT = 3 and 4
+    // Rows per register buffer: 4 at MT = 1, 2 at MT = 2 and 3, 1 at MT = 4
     // with two windows (a lane has 128 registers at 14 waves per CU; x takes
-    // 8 * KV * MT of them).
-    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : MT == 2 || KV == 1 ? 2 : 1, NT = 64 * NS, RPW = 16;
+    // 8 * KV * MT of them, 122 in all at KV = 2, MT = 3).
+    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2, NT = 64 * NS, RPW = 16;
     static_assert(KV * NS * 64 * 8 <= kX14MaxK, "windows");
     static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
     const int lane = threadIdx.x & 63;
@@ -812,13 +876,11 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], wf, acc[m][q]);
                 }
+        // Value v of the step: activation row v / ROWS, weight row i0 + v % ROWS.
+        float a[MT * ROWS];
 #pragma unroll
-        for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int q = 0; q < ROWS; ++q) {
-                const float s = wave_sum_dpp(acc[m][q]);
-                if (lane == 0) red[wave][m * RPW + i0 + q] = s;
-            }
+        for (int v = 0; v < MT * ROWS; ++v) a[v] = acc[v / ROWS][v % ROWS];
+        wave_sums(a, [&](int v, float s) { red[wave][(v / ROWS) * RPW + i0 + v % ROWS] = s; });
     };
 #pragma unroll
     for (int i0 = 0; i0 < RPW; i0 += 2 * ROWS) {
@@ -3297,19 +3359,18 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
-    // Three activation rows on long rows (4096 < K <= 14336, packed 128-bit
-    // rows, 16-row workgroups in whole rounds of one per CU, as at M = 1 and
-    // 2 below): the 14-wave streaming kernel with every activation row's x
-    // in registers, W read once and no x split.  Same box, C2 down, 14-wave /
-    // rows16: m = 3 21.0 / 21.7-21.8 us, m = 4 22.3-22.5 / 21.9-22.1 (one
-    // weight row per buffer at m = 4: four would spill), so M = 4 stays on
-    // rows16 (DMC_HIP_RD_X14_MAX_M: 2 turns this off, 4 takes M = 4 too).
+    // Three or four activation rows on long rows (4096 < K <= 14336, packed
+    // 128-bit rows, 16-row workgroups in whole rounds of one per CU, as at
+    // M = 1 and 2 below): the 14-wave streaming kernel with every activation
+    // row's x in registers, W read once and no x split.  Same box, C2 down,
+    // 14-wave / rows16: m = 3 20.1-20.2 / 21.8 us, m = 4 21.3-21.4 / 21.9
+    // (DMC_HIP_RD_X14_MAX_M: 2 leaves both to rows16, 3 keeps M = 4 there).
     // An explicit DMC_HIP_RD_MFMA_KIND keeps the MFMA layout it names;
     // DMC_HIP_RD_XLDS=2 takes the kernel wherever it applies.
     {
         const int64_t g16 = (p.n + 15) / 16;
         const int xl = env_int("DMC_HIP_RD_XLDS", 1);
-        if (p.m >= 3 && p.m <= std::min(kX14MaxM, env_int("DMC_HIP_RD_X14_MAX_M", 3)) && pl.vec == 8 &&
+        if (p.m >= 3 && p.m <= std::min(kX14MaxM, env_int("DMC_HIP_RD_X14_MAX_M", kX14MaxM)) && pl.vec == 8 &&
             p.ldw == p.k && p.ldx == p.k && p.ldy == p.n && p.k > 0 && p.k <= kX14MaxK && xl != 0 &&
             env_int("DMC_HIP_RD_X14", 1) != 0 && env_int("DMC_HIP_RD_MFMA_KIND", 0) == 0 &&
             (xl == 2 || (p.k > 4096 && g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus)))) {

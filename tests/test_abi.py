@@ -276,27 +276,34 @@ def test_rowdot_mfma_layouts(monkeypatch):
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (8, 32, 448, 0), p
     p = d.plan("rd", 4, 4096, 4096, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
-    for m, mt in ((4, 4), (6, 8), (8, 8)):
+    for m, mt in ((6, 8), (8, 8)):
         p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
             (-7, mt, 32, 128, 2 * m * 4096 * 4), (m, p)
-    # ... except three activation rows, which take the 14-wave streaming
-    # kernel (x in registers, no workspace) unless an MFMA layout is named
-    p = d.plan("rd", 3, 14336, 4096, x_addr=256, w_addr=256)
-    assert (p.waves, p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
-        (14, 2, 3, 16, 256, 0), p
+    # ... except three and four activation rows, which take the 14-wave
+    # streaming kernel (x in registers, no workspace) unless an MFMA layout is
+    # named or DMC_HIP_RD_X14_MAX_M lowers the bound
+    for m in (3, 4):
+        p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
+        assert (p.waves, p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
+            (14, 2, m, 16, 256, 0), p
     monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
-    assert d.plan("rd", 3, 14336, 4096, x_addr=256, w_addr=256).slices == -7
+    for m in (3, 4):
+        p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
+        assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \
+            (-7, 4, 32, 128, 2 * m * 4096 * 4), (m, p)
     monkeypatch.delenv("DMC_HIP_RD_MFMA_KIND")
-    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "4")
-    assert d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256).waves == 14
+    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "3")
+    assert d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256).slices == -7
     monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "2")
     assert d.plan("rd", 3, 14336, 4096, x_addr=256, w_addr=256).slices == -7
     monkeypatch.delenv("DMC_HIP_RD_X14_MAX_M")
     monkeypatch.setenv("DMC_HIP_RD_R16_SPLIT", "0")
+    monkeypatch.setenv("DMC_HIP_RD_MFMA_KIND", "7")
     p = d.plan("rd", 4, 14336, 4096, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
     monkeypatch.delenv("DMC_HIP_RD_R16_SPLIT")
+    monkeypatch.delenv("DMC_HIP_RD_MFMA_KIND")
     # 9..16 activation rows on matrices up to 128 MiB: rows16 too, four blocks
     # per workgroup on a grid of >= 7/8 of the CUs (C2 up/gate: 224), two
     # where four would leave fewer ([8192,4096]: 256), or on C2 down four

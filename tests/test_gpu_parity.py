@@ -931,12 +931,12 @@ def test_graph_replay_after_workspace_growth(hip, monkeypatch):
 
 
 def test_graph_replay_rows16_k_split(hip):
-    """A rows16 plan that splits k (C2 down at m = 4: partial sums in the
+    """A rows16 plan that splits k (C2 down at m = 6: partial sums in the
     library workspace, then the slice-sum launch), captured after one
     uncaptured call of the same shape, replayed three times with new
     activations uploaded eagerly in between: every replay must match the
     reference (sampled rows, every activation row)."""
-    n, k, m = 4096, 14336, 4
+    n, k, m = 4096, 14336, 6
     p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
     assert p.slices == -7 and p.workspace_bytes > 0, p
     rng = np.random.default_rng(77)
@@ -1142,7 +1142,6 @@ def test_shared_x_fourteen_waves(hip, n, k, m, monkeypatch):
     elementwise bound; two launches bit for bit alike."""
     x, w = case(m, k, n, seed=7100 + n + k + m, edge=True)
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
-    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "4")
     p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
     assert (p.waves, p.rows_per_group, p.slices, p.mt) == (14, 16, 1 if k <= 7168 else 2, m), p
     y = _rd_dev(hip, x, w)
@@ -1158,7 +1157,6 @@ def test_shared_x_fourteen_waves_zero_rule(hip, k, m, monkeypatch):
     rows of zero_rows' patterns (order-dependent zeros, exact-zero products)
     -- bit for bit the reference."""
     monkeypatch.setenv("DMC_HIP_RD_XLDS", "2")
-    monkeypatch.setenv("DMC_HIP_RD_X14_MAX_M", "4")
     n = 4096
     assert hip.plan("rd", m, k, n, x_addr=256, w_addr=256).waves == 14
     x = np.full((m, k), np.float32(-1e-38), np.float32)
