@@ -736,11 +736,9 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
                     const uint32_t d = wv[q][j][e >> 1];
                     acc[q] = fmaf(xr[j][e], (e & 1) ? widen_hi(d) : widen_lo(d), acc[q]);
                 }
-#pragma unroll
-        for (int q = 0; q < ROWS; ++q) {
-            const float s = wave_sum_dpp(acc[q]);
-            if (lane == 0 && i0 + q < nr) red[half][wave][i0 + q] = s;
-        }
+        wave_sums(acc, [&](int q, float s) {
+            if (i0 + q < nr) red[half][wave][i0 + q] = s;
+        });
     };
     sum_rows(ba, 0);
     for (int i0 = 0; i0 + ROWS < nr; i0 += 2 * ROWS) {
@@ -1091,6 +1089,7 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
     // loads, out of range, stay unconditional).
     const bool last_block = 8 * (((KV - 1) * NW + wave) * 64) - h < kmh;
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
+        float a[ROWS];
 #pragma unroll
         for (int q = 0; q < ROWS; ++q) {
             float acc = init;
@@ -1106,9 +1105,11 @@ gemv_rd_unaligned_kernel(const uint16_t *__restrict__ W, const float *__restrict
                     nz |= wv[q][j][d] & hm[j][d];
                 }
             }
-            const float s = wave_sum_dpp(zero_fold(acc, nz != 0));
-            if (lane == 0 && i0 + q < nr) red[wave][i0 + q] = s;
+            a[q] = zero_fold(acc, nz != 0);
         }
+        wave_sums(a, [&](int q, float s) {
+            if (i0 + q < nr) red[wave][i0 + q] = s;
+        });
     };
     for (int i0 = 0; i0 < nr; i0 += 2 * ROWS) {
         load(bb, i0 + ROWS);
@@ -2816,6 +2817,8 @@ gemv_rd_f32_stream_kernel(const float *__restrict__ W, const float *__restrict__
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], w, acc[m][q]);
                 }
+        // Value v of the step: activation row v / ROWS, weight row i0 + v % ROWS.
+        float a[MT * ROWS];
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
@@ -2825,9 +2828,11 @@ gemv_rd_f32_stream_kernel(const float *__restrict__ W, const float *__restrict__
                 for (int j = 0; j < KV; ++j)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) nz |= wv[q][j][e] & xm[m][j][e];
-                const float s = wave_sum_dpp(zero_fold(acc[m][q], nz != 0));
-                if (lane == 0 && i0 + q < nr) red[wave][m][i0 + q] = s;
+                a[m * ROWS + q] = zero_fold(acc[m][q], nz != 0);
             }
+        wave_sums(a, [&](int v, float s) {
+            if (i0 + v % ROWS < nr) red[wave][v / ROWS][i0 + v % ROWS] = s;
+        });
     };
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);  // x's wait below comes after every load above
