@@ -491,7 +491,7 @@ def extended(d, W, reps: int) -> dict:
             s = Rotating(d, w, x, 5, n_out=n)
             f = lambda i: d.gemv_rd(s.x, s.w[i % 5], s.y, m, k, n)  # noqa: E731
             f(0)
-            record(f"C2 rd {name} m={m}", batch_us(d, f, 50), n, k, m)
+            record(f"C2 rd {name} m={m}", batch_us(d, f, reps), n, k, m)
             s.free()
     # prefill-sized M on C2's shapes (the gemm layout): TFLOP/s of x.W products
     for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
