@@ -351,17 +351,19 @@ int residency_rc(int rc, int64_t bytes) {
 }
 
 // Device copy of the host weight [host, host+bytes), uploading on a miss.
-// With t_rows > 0 the host bytes hold W [t_rows, t_cols] and the device copy
-// is W^T [t_cols, t_rows]: the drop-in x @ W keeps its weight in the row-dot
-// layout, whose kernel needs one launch where the column-stream layout needs
-// two.  `elem` is the element size (2: bf16, 4: f32) the transpose moves.
-// The layout, the column count and the element size are part of the key, so
-// the same bytes used through another entry or shape get their own copy.  `pin`:
+// With t_rows > 0 the host bytes hold t_batch matrices W [t_rows, t_cols],
+// one after another, and the device copy holds each one's W^T [t_cols,
+// t_rows] in the same order: the drop-in x @ W keeps its weight in the
+// row-dot layout, whose kernel needs one launch where the column-stream
+// layout needs two.  `elem` is the element size (2: bf16, 4: f32) the
+// transpose moves.  The layout, the column and matrix counts and the element
+// size are part of the key, so the same bytes used through another entry or
+// shape get their own copy.  `pin`:
 // the caller keeps the device address (dmc_hip_register_weight), so no
 // eviction may free this entry (residency.h).  DMC_HIP_RESIDENT_CAP (bytes)
 // caps what may stay resident.
 int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, int64_t t_cols = 0,
-             bool pin = false, int elem = 2) {
+             bool pin = false, int elem = 2, int64_t t_batch = 1) {
     Ctx &c = ctx();
     if (bytes <= 0) {
         *dev = c.dummy;
@@ -371,7 +373,7 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
     Key key = content_key(host, bytes);
     if (t_rows > 0)
         key.b = mix64(key.b ^ 0x7472616e73706f73ULL ^ ((uint64_t)t_cols * 0x9E3779B97F4A7C15ULL) ^
-                      (elem == 4 ? 0x6633320000000000ULL : 0));
+                      (elem == 4 ? 0x6633320000000000ULL : 0) ^ ((uint64_t)(t_batch - 1) << 40));
     auto t1 = std::chrono::steady_clock::now();
     c.st.key_ns += (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count();
     if (void *hit = c.weights->find(key, pin, pin ? host : nullptr)) {
@@ -388,11 +390,15 @@ int resident(const void *host, int64_t bytes, void **dev, int64_t t_rows = 0, in
         return rc;
     }
     hipError_t e = hipMemcpyAsync(raw ? raw : d, host, (size_t)bytes, hipMemcpyHostToDevice, c.stream);
-    if (e == hipSuccess && raw)
-        e = elem == 4 ? dmc::launch_transpose_f32(static_cast<const float *>(raw), static_cast<float *>(d), t_rows,
-                                                  t_cols, c.stream)
-                      : dmc::launch_transpose_bf16(static_cast<const uint16_t *>(raw), static_cast<uint16_t *>(d),
-                                                   t_rows, t_cols, c.stream);
+    const size_t t_bytes = (size_t)(t_rows * t_cols) * (size_t)elem;  // one matrix
+    for (int64_t z = 0; e == hipSuccess && raw && z < t_batch; ++z) {
+        const char *src = static_cast<const char *>(raw) + z * t_bytes;
+        char *dst = static_cast<char *>(d) + z * t_bytes;
+        e = elem == 4 ? dmc::launch_transpose_f32(reinterpret_cast<const float *>(src), reinterpret_cast<float *>(dst),
+                                                  t_rows, t_cols, c.stream)
+                      : dmc::launch_transpose_bf16(reinterpret_cast<const uint16_t *>(src),
+                                                   reinterpret_cast<uint16_t *>(dst), t_rows, t_cols, c.stream);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(c.stream);
     if (raw) (void)hipFree(raw);
     if (e != hipSuccess) {
@@ -585,18 +591,25 @@ int run_host(bool rd, const float *l, const uint16_t *r, float *out, int64_t m, 
     c.st.stage_ns += ns_since(t0);
 
     // x @ W with one slice runs on the row-dot kernel over a transposed
-    // resident copy (DMC_HIP_CS_LAYOUT=1 keeps the column-stream kernels);
-    // batched calls keep the column-stream kernels, whose one launch covers
-    // every slice.
-    const bool cs_as_rd = !rd && batch == 1 && !env_flag("DMC_HIP_CS_LAYOUT");
+    // resident copy (DMC_HIP_CS_LAYOUT=1 keeps the column-stream kernels).
+    // So does a batch of slices that share one activation row (ls = 0, m =
+    // 1) over weights one after another (rs = k n), per-head projections of
+    // one token: the slices' transposes, stacked, are one weight [batch n,
+    // k] whose row-dot GEMV writes y [batch, n] in one launch.  Other batched
+    // calls keep the column-stream kernels, whose one launch covers every
+    // slice.
+    const bool stacked = batch > 1 && ls == 0 && m == 1 && rs == k * n && k > 0 && batch * n <= INT32_MAX;
+    const bool cs_as_rd = !rd && (batch == 1 || stacked) && !env_flag("DMC_HIP_CS_LAYOUT");
+    const int64_t nrd = cs_as_rd ? batch * n : n;  // row-dot output rows
     void *dw = nullptr;
-    if ((rc = cs_as_rd ? resident(r, (int64_t)w_bytes, &dw, k, n) : resident(r, (int64_t)w_bytes, &dw))) return rc;
+    if ((rc = cs_as_rd ? resident(r, (int64_t)w_bytes, &dw, k, n, false, 2, batch) : resident(r, (int64_t)w_bytes, &dw)))
+        return rc;
 
     auto t1 = std::chrono::steady_clock::now();
     if (timed) HIP_TRY(hipEventRecord(c.tev[1], c.stream), "hipEventRecord");
     hipError_t e;
     if (rd || cs_as_rd) {
-        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, n, m, k, n};
+        dmc::RdProblem p{static_cast<const uint16_t *>(dw), k, xsrc, k, ydst, nrd, m, k, nrd};
         const dmc::RdPlan pl = dmc::plan_rd(p, c.cus);
         if ((rc = ensure_dev(c.ws, pl.workspace_bytes))) return rc;
         e = dmc::launch_rd(p, pl, pl.workspace_bytes ? c.ws.p : nullptr, c.stream);

@@ -649,6 +649,32 @@ def test_batched_broadcast_activation(hip):
     check(y, oracle.matmul_bf16_batched(x, w, k, n, batch, 0, k * n), what="broadcast")
 
 
+@pytest.mark.parametrize("batch,k,n", [(8, 4096, 128), (32, 4096, 128), (3, 1001, 77), (5, 64, 1)])
+def test_batched_broadcast_stacked_rowdot(hip, batch, k, n, monkeypatch):
+    """Slices that share one activation row over weights one after another
+    (per-head projections of one token: ls = 0, m = 1, rs = k n) run as one
+    row-dot GEMV over the slices' stacked transposes, resident after the
+    first call; the same calls on the column-stream kernels
+    (DMC_HIP_CS_LAYOUT=1) and the oracle agree.  Special weights included;
+    the deferred protocol too."""
+    rng = np.random.default_rng(batch * 7 + k + n)
+    x = rng.standard_normal(k).astype(np.float32)
+    x[::17] = 0.0
+    w = W.bf16_rne(np.float32(0.02) * rng.standard_normal(batch * k * n).astype(np.float32))
+    pos = rng.integers(0, w.size, size=max(1, w.size // 500))
+    w[pos] = rng.choice(np.array([0x0001, 0x8001, 0x0000, 0x8000, 0x7F80, 0xFF80], np.uint16), size=pos.size)
+    y_ref = oracle.matmul_bf16_batched(x, w, k, n, batch, 0, k * n)
+    for _ in range(2):  # upload and transpose, then the resident copy
+        y = hip.matmul_bf16_gpu_batched(x, w, 1, k, n, batch, 0, k * n)
+        check(y, y_ref, what=f"stacked row-dot batch={batch} k={k} n={n}")
+    out = np.full(batch * n, np.nan, np.float32)
+    hip.matmul_bf16_gpu_batched_deferred(x, w, out, 1, k, n, batch, 0, k * n)
+    hip.flush()
+    check(out, y_ref, what="stacked row-dot, deferred")
+    monkeypatch.setenv("DMC_HIP_CS_LAYOUT", "1")
+    check(hip.matmul_bf16_gpu_batched(x, w, 1, k, n, batch, 0, k * n), y_ref, what="column-stream layout")
+
+
 def test_deferred_then_flush(hip):
     k, n = 512, 256
     rng = np.random.default_rng(6)
