@@ -424,7 +424,7 @@ def extended(d, W, reps: int) -> dict:
         dy = d.DeviceBuffer(4 * n * m)
         f = lambda i: d.gemv_rd(dx, dw, dy, m, k, n)  # noqa: E731
         f(0)
-        record(f"C4 rd m={m}", batch_us(d, f, 20), n, k, m)
+        record(f"C4 rd m={m}", batch_us(d, f, 60), n, k, m)
         dx.free()
         dy.free()
     dw.free()
@@ -439,7 +439,7 @@ def extended(d, W, reps: int) -> dict:
             else:
                 f = lambda i: d.gemv_cs(s.x, s.w[i % 3], s.y, 1, k, n)  # noqa: E731
             f(0)
-            record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, 10), n, k)
+            record(f"C5 {layout} W[{n},{k}]", batch_us(d, f, reps), n, k)
             s.free()
     # Batched per-head projections, one launch over every head: the
     # reference's [B,1,S,K] @ [H,K,N] collapse (jit.rs:19914-19933) on device
@@ -456,11 +456,36 @@ def extended(d, W, reps: int) -> dict:
         s = Rotating(d, wb, xb, copies, n_out=heads * n)
         f = lambda i: d.gemv_cs(s.x, s.w[i % copies], s.y, 1, k, n, heads, ls, k * n)  # noqa: E731
         f(0)
-        us = batch_us(d, f, 20)
+        us = batch_us(d, f, reps)
         gbs = (wb.nbytes + xb.nbytes + 4 * heads * n) / (us * 1e-6) / 1e9
         out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
         s.free()
+        if ls == 0:
+            # The same projections through the drop-in's batched entry with
+            # host x and y, in the deferred protocol (eight calls, one
+            # flush): one broadcast x over consecutive heads runs as one
+            # row-dot GEMV over the heads' stacked resident transposes.
+            # Distinct weights rotate so that every call reads cold bytes.
+            lib = d._lib.load()
+            nw = copies
+            hw = [W_bf16(rng, heads * k, n) for _ in range(nw)]
+            ys = [np.empty(heads * n, np.float32) for _ in range(8)]
+            dfr, flush = lib.dmc_matmul_bf16_gpu_batched_deferred, lib.dmc_matmul_bf16_gpu_flush
+            groups = max(1, reps // 8)
+            for g in range(-(-nw // 8) + groups):  # every weight's upload untimed
+                if g == -(-nw // 8):
+                    t0 = time.perf_counter()
+                for j in range(8):
+                    dfr(xb.ctypes.data, hw[(8 * g + j) % nw].ctypes.data, ys[j].ctypes.data, 1, k, n, heads, 0,
+                        k * n)
+                flush()
+            us = (time.perf_counter() - t0) / (8 * groups) * 1e6
+            gbs = (wb.nbytes + xb.nbytes + 4 * heads * n) / (us * 1e-6) / 1e9
+            dl = f"drop-in {label} deferred x8 + flush"
+            out[dl] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+            log(f"{dl}: {us:.2f} us/call  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%} (PCIe-inclusive)")
+            del hw
     # One GPU's share of C2 under 8-way tensor parallelism (rows of gate/up,
     # k of down split eight ways): W[1792,4096] and W[4096,1792], 14.7 MB
     # each, 20 rotating copies (294 MB between reuses, above the 256 MB
@@ -620,7 +645,7 @@ def helpers(d, w) -> dict:
     for label, nbytes, f in cases:
         for i in range(3):
             f(i)
-        us = batch_us(d, f, 20)
+        us = batch_us(d, f, 60)
         gbs = nbytes / (us * 1e-6) / 1e9
         out[label] = {"us": round(us, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
         log(f"{label}: {us:.2f} us  {gbs:.0f} GB/s  {gbs / PEAK_GBS:.1%}")
