@@ -3260,18 +3260,26 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
     const int kv = (int)((k + nw * 512 - 1) / (nw * 512));
     const int mt_cap = kv == 1 ? 8 : kv == 2 ? 4 : kv <= 4 ? 2 : 1;
     const int mt = std::min(mt_for(m), mt_cap);
-    // Rows per register buffer: 2, or 1 for long rows (more than 4 vectors
-    // per lane) and for long rows at two or more activation rows (C2 down at
-    // m = 2: 21.4-21.5 us against 22.0-22.2 with 2).
-    const int rows_default = kv > 4 || (kv >= 2 && mt >= 2) ? 1 : 2;
-    int rows = env_int("DMC_HIP_RD_ROWS", rows_default);
-    if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = rows_default;
     const int64_t gy = (m + mt - 1) / mt;
     auto blocks = [&](int64_t r) {
         int64_t b = 0;
         for (int i = 0; i < count; ++i) b += (n[i] + r - 1) / r;
         return b;
     };
+    // Rows per register buffer: 2, or 1 for long rows (more than 4 vectors
+    // per lane) and for long rows at two or more activation rows (C2 down at
+    // m = 2: 21.4-21.5 us against 22.0-22.2 with 2).  At one activation row
+    // and one window per lane, 4 rows in one step while 4-row workgroups
+    // number at most 8 per CU: every load of a short-lived workgroup in
+    // flight at once (same box, 4 / 2 rows per step, us: [1024,4096] 3.56 /
+    // 3.62, [1792,4096] 4.54 / 4.84, [2048,4096] 4.66 / 5.06, C1 6.98 /
+    // 7.12, [8192,4096] 11.54 / 11.68, [4096,2048] 4.89 / 4.99); on larger
+    // grids 2 rows stay ahead (C2 up 18.3 against 18.5, C4 141.9 against
+    // 143.4).
+    const int rows_default =
+        kv > 4 || (kv >= 2 && mt >= 2) ? 1 : mt == 1 && kv == 1 && blocks(4) * gy <= 8 * cus ? 4 : 2;
+    int rows = env_int("DMC_HIP_RD_ROWS", rows_default);
+    if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = rows_default;
     // Rows per workgroup, measured on MI355X: 4 for short rows (k <= 4096
     // per 8 waves: up/gate 18.1 us, 8 rows 18.5), fewer when that would leave
     // under 4 workgroups per CU; 8 for long ones (down, k = 14336: 19.0 us,

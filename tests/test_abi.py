@@ -168,8 +168,17 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     assert d.plan("rd", 1, 11008, 4097, x_addr=256, w_addr=256).waves == 8
     assert d.plan("rd", 1, 8192, 8192, x_addr=256, w_addr=256).waves == 14      # two whole rounds
     assert d.plan("rd", 1, 8192, 28672, x_addr=256, w_addr=256).waves == 14     # seven
-    small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)  # k/v projections
-    assert small.grid_x >= 512
+    # small grids at one window per lane: 4 rows in one step, 4 per workgroup
+    # (k/v projections: 256 workgroups; C1: 1024); up to 8 such workgroups
+    # per CU, then 2 rows per step (C2 up/gate above)
+    small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)
+    assert (small.rows_or_rw, small.rows_per_group, small.grid_x) == (4, 4, 256), small
+    p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)  # one GPU's gate/up share under TP = 8
+    assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 448), p
+    p = d.plan("rd", 1, 4096, 8192, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 2048), p
+    p = d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.rows_per_group) == (2, 4), p
     # M = 1: the streaming kernel
     p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
     assert p.mt == 1 and p.slices >= 1, p
