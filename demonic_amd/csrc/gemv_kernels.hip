@@ -3266,9 +3266,12 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
         for (int i = 0; i < count; ++i) b += (n[i] + r - 1) / r;
         return b;
     };
-    // Rows per register buffer: 2, or 1 for long rows (more than 4 vectors
-    // per lane) and for long rows at two or more activation rows (C2 down at
-    // m = 2: 21.4-21.5 us against 22.0-22.2 with 2).  At one activation row
+    // Rows per register buffer: 2, or 1 for rows of 3 or more vectors per
+    // lane (same box, 1 / 2 rows per step, us: W[4097,11008] 15.6 / 15.85,
+    // W[4097,14336] 19.2 / 20.95; at 2 vectors even or behind: [4097,8192]
+    // 11.82 / 11.77, [6000,6144] 13.15 / 12.98) and for 2 vectors at two or
+    // more activation rows (C2 down at m = 2: 21.4-21.5 us against
+    // 22.0-22.2 with 2).  At one activation row
     // and one window per lane, 4 rows in one step while 4-row workgroups
     // number at most 8 per CU: every load of a short-lived workgroup in
     // flight at once (same box, 4 / 2 rows per step, us: [1024,4096] 3.56 /
@@ -3277,7 +3280,7 @@ bool plan_stream(int64_t m, int64_t k, const int64_t *n, int count, int64_t cus,
     // grids 2 rows stay ahead (C2 up 18.3 against 18.5, C4 141.9 against
     // 143.4).
     const int rows_default =
-        kv > 4 || (kv >= 2 && mt >= 2) ? 1 : mt == 1 && kv == 1 && blocks(4) * gy <= 8 * cus ? 4 : 2;
+        kv >= 3 || (kv == 2 && mt >= 2) ? 1 : mt == 1 && kv == 1 && blocks(4) * gy <= 8 * cus ? 4 : 2;
     int rows = env_int("DMC_HIP_RD_ROWS", rows_default);
     if (!(rows == 1 || rows == 2 || (rows == 4 && kv <= 2))) rows = rows_default;
     // Rows per workgroup, measured on MI355X: 4 for short rows (k <= 4096
@@ -3621,7 +3624,10 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
             // registers, one weight row per buffer.
             const bool x14_m2 = p.m == 2 && sp.mt == 2 && sp.waves == 8 && sp.kvec >= 2 && sp.kvec <= 4 &&
                                 env_int("DMC_HIP_RD_X14_M2", 1) != 0;
-            if ((p.m == 1 ? sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 : x14_m2) &&
+            // (DMC_HIP_RD_ROWS names the 8-wave kernel's rows per step: set, it
+            // keeps that kernel at M = 1.)
+            const bool rows_auto = env_int("DMC_HIP_RD_ROWS", 0) == 0;
+            if ((p.m == 1 ? sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && rows_auto : x14_m2) &&
                 p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) && xl != 0 &&
                 x14) {
                 sp.waves = kX14Waves;
@@ -3631,12 +3637,13 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
                 sp.mt = (int)p.m;
                 sp.grid_x = (p.n + 15) / 16;
                 sp.grid_y = 1;
-            } else if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && sp.rows == 2 &&
+            } else if (p.m == 1 && sp.waves == 8 && sp.kvec >= (xl == 2 ? 1 : 2) && sp.kvec <= 4 && rows_auto &&
                        p.k <= kXldsMaxK && (xl == 2 || (g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus))) &&
                        xl != 0) {
                 int rpw = env_int("DMC_HIP_RD_XLDS_RPW", 16);
                 if (rpw != 8 && rpw != 16 && rpw != 32) rpw = 16;
                 sp.waves = 16;
+                sp.rows = 2;  // the halves walk their rows 2 at a time
                 sp.rpw = rpw;
                 sp.grid_x = (p.n + rpw - 1) / rpw;
             }
