@@ -783,28 +783,35 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 // ---- RD streaming, one group of 14 waves (M = 1 to 4, long rows) -------------
 //
 // One group of NS = 14 waves splits k: lane t of the workgroup owns the KV
-// windows t + j*NT of 8 elements (NT = 896 threads), so at K = 14336 (KV = 2)
-// every load instruction carries data.  A window's x is the lane's alone, so
-// each lane loads its MT activation rows' windows straight into registers
-// (56 KiB of x per workgroup, one workgroup per CU).  The workgroup's 16 rows
-// stream ROWS at a time through two register buffers with unconditional
-// loads and no barrier until the end, where wave 0 sums each row's 14
-// partials in wave order and rd_finish settles exact zeros (its rare path
-// reads x again from memory).  Every weight load feeds all MT activation
-// rows' fma chains.
+// 16-byte windows t + j*NT of a row (NT = 896 threads; 8 bf16 or 4 f32
+// weights each), so at K = 14336 every load instruction carries data.  A
+// window's x is the lane's alone, so each lane loads its MT activation rows'
+// windows straight into registers (56 KiB of x per activation row and
+// workgroup, one workgroup per CU).  The workgroup's 16 rows stream ROWS at a
+// time through two register buffers with unconditional loads and no barrier
+// until the end, where wave 0 sums each row's 14 partials in wave order and
+// rd_finish settles exact zeros (its rare path reads x again from memory).
+// Every weight load feeds all MT activation rows' fma chains.  Output
+// (activation row m, weight row n) goes to Y[m * ys_act + n * ys_row].
 constexpr int kX14Waves = 14;
-constexpr int kX14MaxK = 2 * kX14Waves * 512;  // 14336: KV <= 2
+constexpr int kX14MaxK = 2 * kX14Waves * 512;  // 14336: KV <= 2 (bf16), 4 (f32)
 constexpr int kX14MaxM = 4;
 
-template <int KV, int MT>
+__device__ float chain_f32(const float *__restrict__ w, const float *__restrict__ x, int K);
+
+template <typename WT, int KV, int MT>
 __global__ void __launch_bounds__(64 * kX14Waves)
-gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
-                          int K) {
-    // Rows per register buffer: 4 at MT = 1, 2 at MT = 2 and 3, 1 at MT = 4
-    // with two windows (a lane has 128 registers at 14 waves per CU; x takes
-    // 8 * KV * MT of them, 122 in all at KV = 2, MT = 3).
-    constexpr int NS = kX14Waves, ROWS = MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2, NT = 64 * NS, RPW = 16;
-    static_assert(KV * NS * 64 * 8 <= kX14MaxK, "windows");
+gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N, int K,
+                          int64_t ys_act, int64_t ys_row) {
+    constexpr bool F32 = sizeof(WT) == 4;
+    constexpr int EW = 16 / sizeof(WT);  // weights per window
+    // Rows per register buffer (a lane has 128 registers at 14 waves per CU;
+    // x takes EW * KV * MT of them): bf16 4 at MT = 1, 2 at MT = 2 and 3, 1
+    // at MT = 4 with two windows (122 registers in all at KV = 2, MT = 3);
+    // f32 2 up to MT = 2, then 1.
+    constexpr int ROWS = F32 ? (MT <= 2 ? 2 : 1) : MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2;
+    constexpr int NS = kX14Waves, NT = 64 * NS, RPW = 16;
+    static_assert(KV * NS * 64 * EW <= kX14MaxK, "windows");
     static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -813,27 +820,30 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
 
     __shared__ float red[NS][MT * RPW];
 
-    // The lane's x windows, both 16-byte halves, issued ahead of the weights.
-    u32x4 xp[MT][KV][2];
+    // The lane's x windows (EW floats: one or two 16-byte halves), issued
+    // ahead of the weights.
+    constexpr int XH = EW / 4;
+    u32x4 xp[MT][KV][XH];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         const __amdgpu_buffer_rsrc_t xrs = weight_rsrc(X + (int64_t)m * K, (uint32_t)K * 4);
 #pragma unroll
         for (int j = 0; j < KV; ++j)
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
-                xp[m][j][h] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + j * NT) * 32u + h * 16u, 0, 0);
+            for (int h = 0; h < XH; ++h)
+                xp[m][j][h] =
+                    __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + j * NT) * (4u * EW) + h * 16u, 0, 0);
     }
     uint32_t eoff[KV];
     bool has[KV];
 #pragma unroll
     for (int j = 0; j < KV; ++j) {
-        const int e = (threadIdx.x + j * NT) * 8;
+        const int e = (threadIdx.x + j * NT) * EW;
         has[j] = e < K;
-        eoff[j] = has[j] ? (uint32_t)e * 2 : kOutOfRange;
+        eoff[j] = has[j] ? (uint32_t)e * (uint32_t)sizeof(WT) : kOutOfRange;
     }
-    const float init = (int)threadIdx.x * 8 < K ? 0.0f : -0.0f;
-    const uint32_t row_bytes = (uint32_t)K * 2;
+    const float init = (int)threadIdx.x * EW < K ? 0.0f : -0.0f;
+    const uint32_t row_bytes = (uint32_t)K * (uint32_t)sizeof(WT);
     const __amdgpu_buffer_rsrc_t rs = weight_rsrc(W + (int64_t)rb * K, (uint32_t)nr * row_bytes);
     u32x4 ba[ROWS][KV], bb[ROWS][KV];
     auto load = [&](u32x4 (&wv)[ROWS][KV], int i0) {
@@ -845,17 +855,14 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
     load(ba, 0);
     load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);
-    float xr[MT][KV][8];
+    float xr[MT][KV][EW];
 #pragma unroll
     for (int m = 0; m < MT; ++m)
 #pragma unroll
         for (int j = 0; j < KV; ++j) {
             const uint32_t sgn = has[j] ? 0u : 0x80000000u;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                xr[m][j][q] = __uint_as_float(xp[m][j][0][q] | sgn);
-                xr[m][j][q + 4] = __uint_as_float(xp[m][j][1][q] | sgn);
-            }
+            for (int e = 0; e < EW; ++e) xr[m][j][e] = __uint_as_float(xp[m][j][e >> 2][e & 3] | sgn);
         }
     auto sum_rows = [&](const u32x4 (&wv)[ROWS][KV], int i0) {
         float acc[MT][ROWS];
@@ -866,11 +873,16 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
 #pragma unroll
         for (int j = 0; j < KV; ++j)
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
+            for (int e = 0; e < EW; ++e)
 #pragma unroll
                 for (int q = 0; q < ROWS; ++q) {
-                    const uint32_t d = wv[q][j][e >> 1];
-                    const float wf = (e & 1) ? widen_hi(d) : widen_lo(d);
+                    float wf;
+                    if constexpr (F32) {
+                        wf = __uint_as_float(wv[q][j][e]);
+                    } else {
+                        const uint32_t d = wv[q][j][e >> 1];
+                        wf = (e & 1) ? widen_hi(d) : widen_lo(d);
+                    }
 #pragma unroll
                     for (int m = 0; m < MT; ++m) acc[m][q] = fmaf(xr[m][j][e], wf, acc[m][q]);
                 }
@@ -905,23 +917,33 @@ gemv_rd_stream_x14_kernel(const uint16_t *__restrict__ W, const float *__restric
             bool hit = false;
 #pragma unroll
             for (int j = 0; j < KV; ++j) {
-                const uint32_t xo = (threadIdx.x + j * NT) * 32u;
-                const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
-                const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
-                const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
-                                     __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
-                                     __uint_as_float(b[2]), __uint_as_float(b[3])};
-                hit |= window_hit(xw, load_w16(rs, eoff[j], (uint32_t)r * row_bytes));
+                const uint32_t xo = (threadIdx.x + j * NT) * (4u * EW);
+                const u32x4 wv = load_w16(rs, eoff[j], (uint32_t)r * row_bytes);
+                if constexpr (F32) {
+                    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) hit |= (a[e] & 0x7fffffffu) != 0 && (wv[e] & 0x7fffffffu) != 0;
+                } else {
+                    const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo, 0, 0);
+                    const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(xrs, xo + 16u, 0, 0);
+                    const float xw[8] = {__uint_as_float(a[0]), __uint_as_float(a[1]), __uint_as_float(a[2]),
+                                         __uint_as_float(a[3]), __uint_as_float(b[0]), __uint_as_float(b[1]),
+                                         __uint_as_float(b[2]), __uint_as_float(b[3])};
+                    hit |= window_hit(xw, wv);
+                }
             }
             return hit;
         },
         [&](int t) {
             const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
-            return chain_strided(W + (int64_t)(rb + r) * K, 1, X + (int64_t)m * K, K);
+            if constexpr (F32)
+                return chain_f32(W + (int64_t)(rb + r) * K, X + (int64_t)m * K, K);
+            else
+                return chain_strided(W + (int64_t)(rb + r) * K, 1, X + (int64_t)m * K, K);
         },
         [&](int t, float v) {
             const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
-            Y[(int64_t)m * N + rb + r] = v;
+            Y[(int64_t)m * ys_act + (int64_t)(rb + r) * ys_row] = v;
         });
 }
 
@@ -3887,9 +3909,9 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec < 1 || pl.kvec > 2 ||
             (int64_t)pl.kvec * kX14Waves * 512 < p.k || p.k > kX14MaxK || (int64_t)16 * p.k * 2 > INT32_MAX)
             return hipErrorInvalidValue;
-#define DMC_X14(KV, MT)                                                                                        \
-    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<KV, MT>), dim3((unsigned)pl.grid_x), dim3(64 * kX14Waves), 0, s, \
-                       p.w, p.x, p.y, (int)p.n, (int)p.k)
+#define DMC_X14(KV, MT)                                                                                      \
+    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<uint16_t, KV, MT>), dim3((unsigned)pl.grid_x),               \
+                       dim3(64 * kX14Waves), 0, s, p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
         switch (pl.kvec * 10 + (int)p.m) {
         case 11: DMC_X14(1, 1); break;
         case 21: DMC_X14(2, 1); break;
@@ -3990,6 +4012,35 @@ hipError_t launch_cs(const CsProblem &p, const CsPlan &pl, void *workspace, hipS
 F32Plan plan_f32(const F32Problem &p, int num_cus) {
     F32Plan pl{};
     const int64_t cus = num_cus > 0 ? num_cus : 256;
+    // Two to four activation rows on long rows (4096 < K <= 14336, 16-byte
+    // rows, 16-row workgroups in whole rounds of one per CU) that the 8-wave
+    // streaming kernel below would take in more than one pass over W: the
+    // 14-wave kernel of the bf16 path with 4 f32 weights per window, every
+    // activation row's x in registers, W read once.  Same box, 8-wave /
+    // 14-wave, us: W[4096,14336] m = 2 / 3 / 4 68.0 / 100.2 / 132.2 against
+    // 35.5 / 36.3 / 36.5; [4096,11008] m = 2 53.1 against 29.1; [4096,8192]
+    // m = 3 42.0 against 24.7; where one pass suffices the 8-wave kernel is as
+    // fast or faster ([4096,8192] m = 1 / 2 23.0 / 23.4 against 25.8 / 26.1;
+    // [4096,11008] m = 1 28.3 against 29.1).  DMC_HIP_F32_X14: 0 never, 2
+    // wherever the kernel applies.
+    {
+        const int xf = env_int("DMC_HIP_F32_X14", 1);
+        const int64_t g16 = (p.n + 15) / 16;
+        const int kv8 = (int)((p.k + 8 * 256 - 1) / (8 * 256));  // the 8-wave kernel's vectors per lane
+        const int64_t cap8 = kv8 <= 2 ? 4 : kv8 <= 4 ? 2 : 1;    // ... and its activation rows per pass
+        if (xf != 0 && p.m >= 1 && p.m <= kX14MaxM && p.k > (xf == 2 ? 3584 : 4096) && p.k <= kX14MaxK &&
+            p.k % 4 == 0 && p.ldw == p.k && p.ldx == p.k && aligned(p.w, 16) && aligned(p.x, 16) &&
+            (xf == 2 || (p.m > cap8 && g16 >= cus && (g16 % cus == 0 || g16 >= 4 * cus)))) {
+            pl.waves = kX14Waves;
+            pl.kvec = (int)((p.k + kX14Waves * 256 - 1) / (kX14Waves * 256));
+            pl.rows = p.m <= 2 ? 2 : 1;
+            pl.mt = (int)p.m;
+            pl.rpw = 16;
+            pl.grid_x = g16;
+            pl.grid_y = 1;
+            return pl;
+        }
+    }
     // Streaming: 16-byte rows, x rows alike, K within 8 vectors of 4 per lane
     // over 8 waves.  Waves as for bf16 by bytes per row (1 KiB per wave per
     // vector); activation rows per workgroup within the register budget; rows
@@ -4067,6 +4118,33 @@ hipError_t launch_f32(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
     if (p.k < 0 || p.m > INT32_MAX || p.n > INT32_MAX || p.k > INT32_MAX || pl.grid_x < 1 || pl.grid_y < 1 ||
         pl.grid_y > 65535 || pl.grid_x > INT32_MAX || pl.grid_x * pl.rpw < p.n || pl.grid_y * pl.mt < p.m)
         return hipErrorInvalidValue;
+    if (pl.kvec > 0 && pl.waves == kX14Waves) {
+        // The 14-wave kernel: 16 rows per workgroup, x straight into registers.
+        if (pl.rpw != 16 || pl.mt != p.m || p.m < 1 || p.m > kX14MaxM || pl.kvec < 2 || pl.kvec > 4 ||
+            (int64_t)pl.kvec * kX14Waves * 256 < p.k || p.k > kX14MaxK || p.k % 4 != 0 || p.ldw != p.k ||
+            p.ldx != p.k || !aligned(p.w, 16) || !aligned(p.x, 16) || pl.grid_x != (p.n + 15) / 16 || pl.grid_y != 1)
+            return hipErrorInvalidValue;
+#define DMC_F32X14(KV, MT)                                                                                  \
+    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<float, KV, MT>), dim3((unsigned)pl.grid_x),              \
+                       dim3(64 * kX14Waves), 0, s, p.w, p.x, p.y, (int)p.n, (int)p.k, p.ys_act, p.ys_row)
+        switch (pl.kvec * 10 + (int)p.m) {
+        case 21: DMC_F32X14(2, 1); break;
+        case 22: DMC_F32X14(2, 2); break;
+        case 23: DMC_F32X14(2, 3); break;
+        case 24: DMC_F32X14(2, 4); break;
+        case 31: DMC_F32X14(3, 1); break;
+        case 32: DMC_F32X14(3, 2); break;
+        case 33: DMC_F32X14(3, 3); break;
+        case 34: DMC_F32X14(3, 4); break;
+        case 41: DMC_F32X14(4, 1); break;
+        case 42: DMC_F32X14(4, 2); break;
+        case 43: DMC_F32X14(4, 3); break;
+        case 44: DMC_F32X14(4, 4); break;
+        default: return hipErrorInvalidValue;
+        }
+#undef DMC_F32X14
+        return hipGetLastError();
+    }
     if (pl.kvec > 0) {
         // The shapes the streaming kernel assumes (plan_f32's conditions).
         if (p.k % 4 != 0 || p.ldw != p.k || p.ldx != p.k || !aligned(p.w, 16) || !aligned(p.x, 16) ||

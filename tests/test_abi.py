@@ -603,10 +603,25 @@ def test_f32_general_kernel_for_odd_k_misaligned_or_long_rows(k, x_addr, w_addr)
     assert p.kvec == 0 and p.waves == 4 and p.rows_per_group == 4 and p.grid_x == 14336 // 4, p
 
 
-def test_f32_activation_rows_per_workgroup():
+def test_f32_activation_rows_per_workgroup(monkeypatch):
     assert d.plan_f32(4, 4096, 4096, x_addr=256, w_addr=256).mt == 4      # kvec 2: up to 4
     assert d.plan_f32(16, 4096, 4096, x_addr=256, w_addr=256).grid_y == 4
+    # long rows that the 8-wave kernel would take one activation row per pass
+    # (kvec 7 at K = 14336): the 14-wave kernel, every activation row in one
+    # pass; a lone row, and a grid short of one 16-row workgroup per CU, keep
+    # the 8-wave kernel (DMC_HIP_F32_X14=2 takes the 14-wave one there too)
+    for m in (2, 3, 4):
+        p = d.plan_f32(m, 14336, 4096, x_addr=256, w_addr=256)
+        assert (p.waves, p.kvec, p.mt, p.rows_per_group, p.grid_x, p.grid_y) == (14, 4, m, 16, 256, 1), p
+    assert d.plan_f32(1, 14336, 4096, x_addr=256, w_addr=256).waves == 8
+    assert d.plan_f32(2, 8192, 4096, x_addr=256, w_addr=256).waves == 8   # kvec 4: two per pass
+    assert d.plan_f32(3, 8192, 4096, x_addr=256, w_addr=256).waves == 14
+    assert d.plan_f32(2, 14336, 1000, x_addr=256, w_addr=256).waves == 8
+    monkeypatch.setenv("DMC_HIP_F32_X14", "0")
     assert d.plan_f32(4, 14336, 4096, x_addr=256, w_addr=256).mt == 1     # kvec 7: one
+    monkeypatch.setenv("DMC_HIP_F32_X14", "2")
+    assert d.plan_f32(1, 14336, 1000, x_addr=256, w_addr=256).waves == 14
+    monkeypatch.delenv("DMC_HIP_F32_X14")
     assert d.plan_f32(16, 4097, 64, x_addr=256, w_addr=256).mt == 16      # general
 
 

@@ -195,3 +195,69 @@ def test_full_decode_shapes_on_sampled_rows(hip, n, k):
     y_ref = oracle.gemv_points_f32(x, w, np.zeros(rows.size, np.int64), rows)
     check(y[rows], y_ref, what=f"f32 full W[{n},{k}] sampled")
     assert np.all(np.isfinite(y))
+
+
+X14_F32 = [(4096, 14336), (4097, 14336), (1030, 12288), (6, 9000), (300, 4100)]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", X14_F32)
+def test_fourteen_waves_f32(hip, n, k, m, monkeypatch):
+    """The 14-wave kernel with f32 weights (the default where the 8-wave
+    kernel would take the activation rows in several passes;
+    DMC_HIP_F32_X14=2 takes it wherever it applies): 2 to 4 windows of 4
+    weights per lane, a partial last workgroup (n = 4097), fewer rows than one
+    workgroup (n = 6), edge values; through the device-pointer entry (y [m,n])
+    and the drop-in's W @ x (out [n,m]: the other output orientation); two
+    launches bit for bit alike."""
+    monkeypatch.setenv("DMC_HIP_F32_X14", "2")
+    rng = np.random.default_rng(n + k + m)
+    x = edge(rng.standard_normal((m, k)).astype(np.float32), rng)
+    w = edge(rng.standard_normal((n, k)).astype(np.float32), rng)
+    y_ref = oracle.matmul_f32(x, np.ascontiguousarray(w.T))
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        pl = hip.plan_f32(m, k, n, x_addr=dx.addr, w_addr=dw.addr)
+        assert (pl.waves, pl.mt, pl.rows_per_group) == (14, m, 16), pl
+        ys = []
+        for _ in range(2):
+            hip.gemv_f32_rd(dx, dw, dy, m, k, n)
+            hip.synchronize()
+            ys.append(dy.download(np.float32, (m, n)))
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+    check(ys[0], y_ref, what=f"f32 x14 device m={m} n={n} k={k}")
+    check(hip.matmul_f32_gpu(w, np.ascontiguousarray(x.T)), np.ascontiguousarray(y_ref.T),
+          what=f"f32 x14 W@x m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [2, 4])
+def test_fourteen_waves_f32_zero_rule(hip, m, monkeypatch):
+    """Exact zeros on the f32 14-wave kernel (the default at K = 14336 and
+    2 or more activation rows over 4096 rows): products that all underflow
+    (-0 / +0 by their sign in the chain), a sign flip at the last product,
+    exact-zero rows, an exact cancellation -- bit for bit the reference."""
+    k, n = 14336, 4096
+    rng = np.random.default_rng(m)
+    x = np.full((m, k), np.float32(1e-30), np.float32)
+    x[1::2] = np.float32(0.5)
+    w = np.full((n, k), np.float32(1e-30), np.float32)
+    w[1::6] = -w[1::6]
+    w[2::6, k - 1] = -w[2::6, k - 1]
+    w[3::6] = 0
+    h = k // 2
+    w[4::6, :h] = 1.0
+    w[4::6, h:] = -1.0
+    w[5::6, ::2] = -w[5::6, ::2]
+    assert hip.plan_f32(m, k, n, x_addr=256, w_addr=256).waves == 14
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        hip.gemv_f32_rd(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (m, n))
+    rows = np.r_[0:12, n - 12:n]
+    y_ref = oracle.matmul_f32(x, np.ascontiguousarray(w[rows].T))
+    z = y_ref == 0
+    assert np.any(z)
+    assert np.array_equal(y[:, rows][z].view(np.uint32), y_ref[z].view(np.uint32)), (y[:, rows], y_ref)
+    for r in range(m):
+        check_bound(y[r, rows], y_ref[r], x[r], w[rows], what=f"f32 x14 zero rule m={m} row {r}")
