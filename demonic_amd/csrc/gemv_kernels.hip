@@ -88,14 +88,6 @@ __device__ __forceinline__ void load_x(const float *p, float (&v)[VEC]) {
     }
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the same bits (the
-// xor butterfly is symmetric and IEEE addition is commutative).
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
 // Sum over the 64 lanes of a wave with DPP moves inside each row of 16 lanes
 // (xor 1, xor 2, half-row mirror, row mirror), then the four row sums read
 // out in a fixed order.  Every lane gets the same bits.
@@ -813,7 +805,6 @@ gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X,
     constexpr int NS = kX14Waves, NT = 64 * NS, RPW = 16;
     static_assert(KV * NS * 64 * EW <= kX14MaxK, "windows");
     static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
-    const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rb = (int)blockIdx.x * RPW;
     const int nr = max(0, min(N, rb + RPW) - rb);
@@ -2210,13 +2201,12 @@ gemv_rd_kernel(const uint16_t *__restrict__ W, int64_t ldw, const float *__restr
     }
 
     __shared__ float red[kWaves][MT * ROWS];
+    {
+        float a[MT * ROWS];
 #pragma unroll
-    for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            const float s = wave_sum(acc[m][r]);
-            if (lane == 0) red[wave][m * ROWS + r] = s;
-        }
+        for (int v = 0; v < MT * ROWS; ++v) a[v] = acc[v / ROWS][v % ROWS];
+        wave_sums(a, [&](int v, float s) { red[wave][v] = s; });
+    }
     __syncthreads();
     for (int i0 = wave * 64; i0 < MT * ROWS; i0 += kThreads) {  // wave-uniform: settle_zero needs whole waves
         const int i = i0 + lane < MT * ROWS ? i0 + lane : 0;
@@ -2939,16 +2929,15 @@ gemv_rd_f32_kernel(const float *__restrict__ W, int64_t ldw, const float *__rest
             }
         }
     }
+    float a[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
+    for (int m = 0; m < MT; ++m) a[m] = m < mrows ? zero_fold(acc[m], nz[m] != 0) : 0.0f;
+    wave_sums(a, [&](int m, float s) {
         if (m < mrows) {
-            float s = wave_sum_dpp(zero_fold(acc[m], nz[m] != 0));
-            if (lane == 0) {
-                s = zero_unfold_f32(s, true, x + (int64_t)m * ldx, w, K);
-                Y[(int64_t)(m0 + m) * ys_act + (int64_t)n * ys_row] = s;
-            }
+            s = zero_unfold_f32(s, true, x + (int64_t)m * ldx, w, K);
+            Y[(int64_t)(m0 + m) * ys_act + (int64_t)n * ys_row] = s;
         }
-    }
+    });
 }
 
 // dst [cols, rows] = src [rows, cols]^T for 4-byte elements (the resident
