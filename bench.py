@@ -13,7 +13,9 @@ value         whole-job throughput: algorithmic bytes (2NK + 4K + 4N per GEMV)
               of the K timed steps over their host wall time, synchronized on
               both sides.  The K steps (2K launches on resident inputs) are
               captured once into a HIP graph on the library stream and the
-              timed region is one replay of it.  The per-shape batches below
+              timed region is one replay of it, timed --repeats times (3),
+              each bracketed by a synchronize: `value` takes the median
+              (`timing` lists every repeat).  The per-shape batches below
               run first, so the timed region starts on a device that has been
               streaming, as a decode loop's steps do.  `eager` times the same
               K steps launched one Python call at a time.
@@ -179,6 +181,9 @@ def main(argv=None) -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--repeats", type=int, default=3,
+                    help="time the K steps this many times (each bracketed by a synchronize) and report "
+                         "the median")
     ap.add_argument("--copies", type=int, default=6, help="distinct device copies per weight")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -261,6 +266,15 @@ def main(argv=None) -> int:
         d.synchronize()
         return time.perf_counter() - t0
 
+    repeats = max(1, a.repeats)
+
+    def timed_median(run):
+        """The median of `repeats` timings of run() (each bracketed by a
+        synchronize), and all of them: a single timing of a short region
+        varies by a few per cent from one to the next."""
+        walls = [timed(run) for _ in range(repeats)]
+        return sorted(walls)[len(walls) // 2], walls
+
     # per-shape launch durations, the read ceiling and the dispatch floor
     # (measured first: the timed region below then starts on a device that
     # has been streaming for a while, as a decode loop's steps do; each
@@ -290,7 +304,7 @@ def main(argv=None) -> int:
             steps()
         graph.launch()
         d.synchronize()
-        wall = timed(graph.launch)
+        wall, walls = timed_median(graph.launch)
         # device time of the same K steps (HIP events; see batch_us), repeated
         # in one graph until it holds >= 400 launches: each graph replay
         # carries a fixed cost of its own (~20-30 us on these boxes), which
@@ -310,7 +324,7 @@ def main(argv=None) -> int:
     else:
         steps()
         d.synchronize()
-        wall = timed(steps)
+        wall, walls = timed_median(steps)
         e0.record()
         for _ in range(replays):
             steps()
@@ -321,7 +335,7 @@ def main(argv=None) -> int:
     # the same K steps launched one call at a time (garbage collector paused)
     gc.disable()
     try:
-        eager_wall = timed(steps)
+        eager_wall, _ = timed_median(steps)
     finally:
         gc.enable()
     for nm in order:
@@ -339,7 +353,7 @@ def main(argv=None) -> int:
         "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic_from_profile(),
         "kernel": "row-dot streaming GEMVs: gemv_rd_stream_kernel (up/gate), "
-                  "gemv_rd_stream_x14_kernel (down, 14 waves sharing x through LDS)",
+                  "gemv_rd_stream_x14_kernel (down, 14 waves splitting k, one workgroup per CU)",
         "bytes_per_launch": {"up": b_up, "down": b_down},
         "avg_launch_us": round(launch_us, 3),
         "us_per_launch": {nm: round(u, 3) for nm, u in us.items()},
@@ -354,6 +368,8 @@ def main(argv=None) -> int:
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16w-f32acc",
         "submission": ("one HIP graph replay of the K timed steps (2K kernel launches)" if GRAPHS
                        else "the K timed steps launched one call at a time (--no-graph)"),
+        "timing": {"repeats": repeats, "statistic": "median of the repeats, each bracketed by a synchronize",
+                   "ms_per_repeat": [round(w * 1e3, 4) for w in walls]},
         "eager": {"value": round(bytes_step * a.steps / eager_wall / 1e9, 1),
                   "note": "the same K steps launched one Python call at a time, host wall time"},
         "data": "synthetic: seeded N(0,0.02) bf16 weights, N(0,1) f32 activations (PCG64 seed 0)",
