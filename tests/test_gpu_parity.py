@@ -1141,6 +1141,25 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
 
 
+@pytest.mark.parametrize("n,k", [(1030, 4096), (1, 4096), (4097, 4000), (2049, 2048), (7, 1024), (8190, 4096)])
+def test_four_rows_per_step_on_small_grids(hip, n, k):
+    """One activation row, one window per lane and at most 8 four-row
+    workgroups per CU: 4 rows in one step, 4 per workgroup (partial last
+    workgroups: n = 1030, 4097, 2049, 7; a lone row; fewer waves at k = 2048
+    and 1024).  Edge data; the parity rule and, row by row, the bound; the
+    zero rule's rare path on rows of underflowing products."""
+    p = hip.plan("rd", 1, k, n, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.rows_per_group) == (4, 4), p
+    x, w = case(1, k, n, seed=7300 + n + k, edge=True)
+    check_or_bound(run_rd(hip, x, w), ref(x, w), x, W.bf16_to_f32(w), what=f"4 rows per step n={n} k={k}")
+    xz = np.full((1, k), np.float32(-1e-38), np.float32)
+    wz = np.full((n, k), 0x0001, np.uint16)
+    wz[1::2] = 0x8001
+    y_ref = ref(xz, wz)
+    y = run_rd(hip, xz, wz)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+
+
 X14_SHAPES = [(4096, 14336), (4097, 14336), (8190, 12288), (4096, 4112), (1030, 14336), (6, 9000), (16384, 12288)]
 
 
