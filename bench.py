@@ -722,14 +722,15 @@ def dropin(d, W, reps: int) -> dict:
 
 
 def skinny(d, W, reps: int) -> dict:
-    """C2's shapes at m = 2 .. 16 (the skinny-M MFMA kernels) and 64 / 512
-    (prefill, the gemm layout), `reps` launches each, one host call per
-    launch: no HIP graph, so counter collection sees ordinary dispatches."""
+    """C2's shapes at m = 2 .. 16 (the streaming, 14-wave and skinny-M MFMA
+    kernels) and 64 / 512 (prefill, the gemm layout), `reps` launches each,
+    one host call per launch: no HIP graph, so counter collection sees
+    ordinary dispatches."""
     out = {}
     c2 = W.c2()
     for name, (w, _) in (("up", c2["up"]), ("down", c2["down"])):
         n, k = w.shape
-        for m in (2, 4, 8, 12, 16, 64, 512):
+        for m in (2, 3, 4, 8, 12, 16, 64, 512):
             x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
             s = Rotating(d, w, x, 3, n_out=n)
             f = lambda i: d.gemv_rd(s.x, s.w[i % 3], s.y, m, k, n)  # noqa: E731
@@ -738,7 +739,8 @@ def skinny(d, W, reps: int) -> dict:
             p = d.plan("rd", m, k, n, x_addr=s.x.addr, w_addr=s.w[0].addr)
             out[f"C2 rd {name} m={m}"] = {"us": round(us, 3), "GB/s": round(b_alg(n, k, m) / (us * 1e-6) / 1e9, 1),
                                           "TFLOP/s": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
-                                          "layout": {-6: "wide", -7: "rows16", -8: "gemm"}.get(p.slices, "stream")}
+                                          "layout": {-6: "wide", -7: "rows16", -8: "gemm"}.get(
+                                              p.slices, "x14" if p.waves == 14 else "stream")}
             log(f"C2 rd {name} m={m}: {us:.2f} us ({out[f'C2 rd {name} m={m}']['layout']})")
             s.free()
     return out
