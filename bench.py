@@ -740,7 +740,8 @@ def skinny(d, W, reps: int) -> dict:
             out[f"C2 rd {name} m={m}"] = {"us": round(us, 3), "GB/s": round(b_alg(n, k, m) / (us * 1e-6) / 1e9, 1),
                                           "TFLOP/s": round(2.0 * m * n * k / (us * 1e-6) / 1e12, 1),
                                           "layout": {-6: "wide", -7: "rows16", -8: "gemm"}.get(
-                                              p.slices, "x14" if p.waves == 14 else "stream")}
+                                              p.slices, "x14" if p.waves == 14 else
+                                              "x8" if (p.waves, p.rows_or_rw, p.rows_per_group) == (8, 4, 16) else "stream")}
             log(f"C2 rd {name} m={m}: {us:.2f} us ({out[f'C2 rd {name} m={m}']['layout']})")
             s.free()
     return out

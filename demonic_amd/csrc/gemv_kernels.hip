@@ -776,7 +776,9 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 //
 // One group of NS = 14 waves splits k: lane t of the workgroup owns the KV
 // 16-byte windows t + j*NT of a row (NT = 896 threads; 8 bf16 or 4 f32
-// weights each), so at K = 14336 every load instruction carries data.  A
+// weights each), so at K = 14336 every load instruction carries data.  The
+// same layout on NS = 8 waves (NT = 512, one window per lane) serves bf16
+// rows of K <= 4096, three or four workgroups to a CU.  A
 // window's x is the lane's alone, so each lane loads its MT activation rows'
 // windows straight into registers (56 KiB of x per activation row and
 // workgroup, one workgroup per CU).  The workgroup's 16 rows stream ROWS at a
@@ -791,8 +793,8 @@ constexpr int kX14MaxM = 4;
 
 __device__ float chain_f32(const float *__restrict__ w, const float *__restrict__ x, int K);
 
-template <typename WT, int KV, int MT>
-__global__ void __launch_bounds__(64 * kX14Waves)
+template <typename WT, int KV, int MT, int NS = kX14Waves>
+__global__ void __launch_bounds__(64 * NS)
 gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N, int K,
                           int64_t ys_act, int64_t ys_row) {
     constexpr bool F32 = sizeof(WT) == 4;
@@ -800,9 +802,10 @@ gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X,
     // Rows per register buffer (a lane has 128 registers at 14 waves per CU;
     // x takes EW * KV * MT of them): bf16 4 at MT = 1, 2 at MT = 2 and 3, 1
     // at MT = 4 with two windows (122 registers in all at KV = 2, MT = 3);
-    // f32 2 up to MT = 2, then 1.
+    // f32 2 up to MT = 2, then 1.  On 8 waves (KV = 1) the same rows take 54
+    // to 76 registers.
     constexpr int ROWS = F32 ? (MT <= 2 ? 2 : 1) : MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2;
-    constexpr int NS = kX14Waves, NT = 64 * NS, RPW = 16;
+    constexpr int NT = 64 * NS, RPW = 16;
     static_assert(KV * NS * 64 * EW <= kX14MaxK, "windows");
     static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -3386,6 +3389,52 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
+    // One to four activation rows on rows of 2048 < K <= 4096: the 14-wave
+    // kernel's layout on one group of 8 waves (a window per lane, x in
+    // registers, 16 rows per workgroup, zeros settled after the stream; 3 or
+    // 4 workgroups share a CU).  Same boxes, 8-wave group / default, us, K =
+    // 4096 unless named:
+    // - M = 1, where the groups spread evenly over at most two rounds: C1
+    //   6.66 / 6.88, [8192,4096] 11.36 / 11.61, [4096,3072] 5.47 / 6.34;
+    //   elsewhere the 4-row streaming workgroups win ([5120,4096] 9.09 /
+    //   8.03, [28672,4096] 34.65 / 33.77, [1024,4096] 4.62 / 3.32);
+    // - M = 2 from 3/4 of a round: C2 up 19.41-19.46 / 20.03-20.08, C1 7.11 /
+    //   7.97, [12288,4096] 16.38 / 17.50 ([5120,4096] the loss, 9.85 / 9.41);
+    // - M = 3 everywhere: C2 up 20.10-20.29 / 20.82-20.91 (rows16), [1024,4096]
+    //   5.95 / 6.99, [12288,4096] 16.96 / 19.85;
+    // - M = 4 except between one and two rounds of resident groups (three
+    //   per CU): [12288,4096] 17.90 / 19.88, TP = 8 gate/up [1792,4096] 6.56
+    //   / 7.25, C4 150.6 / 153.1, [28672,4096] 37.2-37.7 / 38.0-38.2; C2 up's
+    //   896 groups leave a short second round (21.14-21.47 / 20.83-20.86).
+    // C4 at M = 2 / 3: 145.4 / 146.4 against 146.5 / 154.2.
+    // At K = 2048 half the lanes would hold no window ([4096,2048] lost at
+    // every M).  DMC_HIP_RD_X8: 0 never, 2 wherever it applies (K <= 4096);
+    // explicit MFMA, rows16 or rows-per-step settings keep their kernels.
+    const int x8 = env_int("DMC_HIP_RD_X8", 1);
+    const int64_t g16x = (p.n + 15) / 16;
+    const bool x8_auto = x8 == 1 && p.k > 2048 && env_int("DMC_HIP_RD_XLDS", 1) != 2 &&
+                         env_int("DMC_HIP_RD_MFMA_KIND", 0) == 0 && env_int("DMC_HIP_RD_MFMA_MIN_M", -1) < 0 &&
+                         env_int("DMC_HIP_RD_ROWS", 0) == 0 && env_int("DMC_HIP_RD_R16_TILES", 0) == 0 &&
+                         env_int("DMC_HIP_RD_R16_SPLIT", -1) < 0 &&
+                         (p.m == 1   ? g16x % cus == 0 && g16x <= 2 * cus
+                          : p.m == 2 ? 4 * g16x >= 3 * cus
+                          : p.m == 3 ? true
+                                     : g16x <= 3 * cus || g16x >= 6 * cus);
+    if ((x8 == 2 || x8_auto) && p.m >= 1 && p.m <= kX14MaxM && pl.vec == 8 && p.ldw == p.k && p.ldx == p.k &&
+        p.ldy == p.n && p.k > 0 && p.k <= 8 * 512) {
+        RdPlan xp{};
+        xp.vec = 8;
+        xp.waves = 8;
+        xp.xreg8 = true;
+        xp.kvec = 1;
+        xp.rows = 4;
+        xp.rpw = 16;
+        xp.mt = (int)p.m;
+        xp.grid_x = g16x;
+        xp.grid_y = 1;
+        return xp;
+    }
+
     // Three or four activation rows on long rows (4096 < K <= 14336, packed
     // 128-bit rows, 16-row workgroups in whole rounds of one per CU, as at
     // M = 1 and 2 below): the 14-wave streaming kernel with every activation
@@ -3892,6 +3941,23 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
+    }
+    if (pl.kvec > 0 && pl.xreg8) {
+        if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec != 1 || pl.waves != 8 ||
+            p.k > 8 * 512 || p.k < 1)
+            return hipErrorInvalidValue;
+#define DMC_X8(MT)                                                                                           \
+    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<uint16_t, 1, MT, 8>), dim3((unsigned)pl.grid_x), dim3(512), \
+                       0, s, p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
+        switch ((int)p.m) {
+        case 1: DMC_X8(1); break;
+        case 2: DMC_X8(2); break;
+        case 3: DMC_X8(3); break;
+        case 4: DMC_X8(4); break;
+        default: return hipErrorInvalidValue;
+        }
+#undef DMC_X8
+        return hipGetLastError();
     }
     if (pl.kvec > 0 && pl.any_align) return rd_unaligned_dispatch(p, pl, s);
     if (pl.kvec > 0 && pl.waves == kX14Waves && pl.rows == 4) {

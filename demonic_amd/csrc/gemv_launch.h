@@ -80,6 +80,7 @@ struct RdPlan {
     // rows
     bool any_align = false;
     int rstep = 1;
+    bool xreg8 = false;  // the 14-wave kernel's layout on 8 waves (K <= 4096)
     size_t workspace_bytes = 0;
 };
 

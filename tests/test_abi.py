@@ -175,20 +175,39 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     assert (small.rows_or_rw, small.rows_per_group, small.grid_x) == (4, 4, 256), small
     p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)  # one GPU's gate/up share under TP = 8
     assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 448), p
+    # ... except where one group of 8 waves per 16 rows (x in registers, a
+    # window per lane) spreads evenly over at most two rounds (C1: 256 groups;
+    # [8192,4096]: 512)
+    for n in (4096, 8192):
+        p = d.plan("rd", 1, 4096, n, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.grid_x) == (8, 4, 16, 1, n // 16), p
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     p = d.plan("rd", 1, 4096, 8192, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 2048), p
+    monkeypatch.delenv("DMC_HIP_RD_X8")
+    assert d.plan("rd", 1, 4096, 5120, x_addr=256, w_addr=256).rows_per_group == 4  # 320 groups: uneven
+    assert d.plan("rd", 1, 2048, 4096, x_addr=256, w_addr=256).rows_per_group == 4  # K = 2048: half the lanes idle
     p = d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group) == (2, 4), p
     # M = 1: the streaming kernel
     p = d.plan("rd", 1, 4096, 128256, x_addr=256, w_addr=256)
     assert p.mt == 1 and p.slices >= 1, p
-    # M = 2: the streaming kernel, 16 weight rows per workgroup where the grid
-    # keeps 4 workgroups per CU (8 on C2 up/gate); rows16 where rows too long
-    # for the streaming kernel's registers would take one activation row per pass
+    # M = 2 on rows of 2048 < K <= 4096: the 8-wave group (16 rows, x in
+    # registers) from 3/4 of a round of groups; otherwise the streaming
+    # kernel, 16 weight rows per workgroup where the grid keeps 4 workgroups
+    # per CU (8 on C2 up/gate); rows16 where rows too long for the streaming
+    # kernel's registers would take one activation row per pass
+    for n in (128256, 14336, 4096, 3072):
+        p = d.plan("rd", 2, 4096, n, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.slices, p.mt, p.rows_per_group, p.grid_x) == \
+            (8, 4, 1, 2, 16, n // 16), p
+    assert d.plan("rd", 2, 4096, 1792, x_addr=256, w_addr=256).rows_or_rw == 2  # 112 groups
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 16, 8016), p
     p = d.plan("rd", 2, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 8, 1792), p
+    monkeypatch.delenv("DMC_HIP_RD_X8")
     # long rows at M = 2: the 14-wave shared-x kernel with one LDS copy of x per
     # activation row (DMC_HIP_RD_X14_M2=0: the streaming kernel)
     p = d.plan("rd", 2, 14336, 4096, x_addr=256, w_addr=256)
@@ -205,10 +224,17 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # M >= 3 with k % 64 == 0: an MFMA kernel (slices == -kind).  M <= 4: rows16
     # (two 16-row blocks per workgroup, 4 activation rows); 6..16 rows on the LM
     # head: the gemm layout with 16-row tiles, x split in the kernel, k in one
-    # slice (no workspace)
+    # slice (no workspace).  At K <= 4096 the 8-wave group takes 3 rows
+    # everywhere and 4 outside one to two rounds of groups (C4: 8016).
+    for m in (3, 4):
+        p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.slices, p.mt, p.rows_per_group, p.grid_x) == (8, 4, 1, m, 16, 8016), p
+    assert d.plan("rd", 4, 4096, 14336, x_addr=256, w_addr=256).slices == -7  # C2 up: 896 groups
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     for m in (3, 4):
         p = d.plan("rd", m, 4096, 128256, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
+    monkeypatch.delenv("DMC_HIP_RD_X8")
     monkeypatch.setenv("DMC_HIP_RD_MFMA_MIN_M", "2")
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == (-7, 4, 32, 8, 4008), p
@@ -255,11 +281,17 @@ def test_rowdot_aligned_rows_with_a_short_last_block_take_the_short_tail():
 
 
 def test_rowdot_mfma_layouts(monkeypatch):
-    # N too small for the wide layout: rows16, activation rows per workgroup 4, 8 or 16
+    # N too small for the wide layout: rows16, activation rows per workgroup 4,
+    # 8 or 16 (DMC_HIP_RD_X8=0: at m = 3 the 8-wave group would take it)
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     for m, mt, rpw in [(3, 4, 32), (4, 4, 32), (5, 8, 32), (8, 8, 32)]:
         p = d.plan("rd", m, 4096, 16387, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.waves, p.grid_x) == \
             (-7, mt, rpw, 8, (16387 + rpw - 1) // rpw), (m, p)
+    monkeypatch.delenv("DMC_HIP_RD_X8")
+    p = d.plan("rd", 3, 4096, 16387, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, 4, 16, 1025), p
+    assert d.plan("rd", 4, 4096, 16387, x_addr=256, w_addr=256).slices == -7  # 1025 groups: one to two rounds
     # from 9 activation rows on a matrix above 128 MiB, and above 16 (past the
     # small-matrix rule) whatever N, the gemm layout (16 activation rows per
     # workgroup up to 16, 32 up to 32); at 32-row tiles on 4-wave workgroups
@@ -283,8 +315,12 @@ def test_rowdot_mfma_layouts(monkeypatch):
     # (256 workgroups, the slices' partials in the workspace)
     p = d.plan("rd", 8, 4096, 14336, x_addr=256, w_addr=256)
     assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (8, 32, 448, 0), p
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")  # C1 at m = 4 otherwise takes the 8-wave group
     p = d.plan("rd", 4, 4096, 4096, x_addr=256, w_addr=256)
-    assert (p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (4, 16, 256, 0), p
+    assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == (-7, 4, 16, 256, 0), p
+    monkeypatch.delenv("DMC_HIP_RD_X8")
+    p = d.plan("rd", 4, 4096, 4096, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.mt, p.rows_per_group, p.grid_x) == (8, 4, 4, 16, 256), p
     for m, mt in ((6, 8), (8, 8)):
         p = d.plan("rd", m, 14336, 4096, x_addr=256, w_addr=256)
         assert (p.slices, p.mt, p.rows_per_group, p.grid_x, p.workspace_bytes) == \

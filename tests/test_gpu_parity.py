@@ -1142,12 +1142,14 @@ def test_shared_x_zero_signs(hip, k, monkeypatch):
 
 
 @pytest.mark.parametrize("n,k", [(1030, 4096), (1, 4096), (4097, 4000), (2049, 2048), (7, 1024), (8190, 4096)])
-def test_four_rows_per_step_on_small_grids(hip, n, k):
+def test_four_rows_per_step_on_small_grids(hip, n, k, monkeypatch):
     """One activation row, one window per lane and at most 8 four-row
     workgroups per CU: 4 rows in one step, 4 per workgroup (partial last
     workgroups: n = 1030, 4097, 2049, 7; a lone row; fewer waves at k = 2048
-    and 1024).  Edge data; the parity rule and, row by row, the bound; the
-    zero rule's rare path on rows of underflowing products."""
+    and 1024; n = 8190 with the 8-wave group switched off).  Edge data; the
+    parity rule and, row by row, the bound; the zero rule's rare path on rows
+    of underflowing products."""
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     p = hip.plan("rd", 1, k, n, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group) == (4, 4), p
     x, w = case(1, k, n, seed=7300 + n + k, edge=True)
@@ -1206,6 +1208,53 @@ def test_shared_x_fourteen_waves_zero_rule(hip, k, m, monkeypatch):
     assert hip.plan("rd", m, k, n, x_addr=256, w_addr=256).waves == 14
     x = np.full((m, k), np.float32(-1e-38), np.float32)
     x[1::2] = -x[1::2]                       # odd rows: the opposite zero signs
+    w = np.full((n, k), 0x0001, np.uint16)
+    w[1::2, :] = 0x8001
+    y_ref = ref(x, w)
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+    xm, wz = zero_rows(k, 9)
+    w = np.ascontiguousarray(wz[np.arange(n) % 9])
+    xm = np.ascontiguousarray(xm[(2 + np.arange(m)) % 4])
+    y_ref = ref(xm, w)
+    y = _rd_dev(hip, xm, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
+        np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
+
+
+X8_SHAPES = [(14336, 4096), (4097, 4096), (1030, 4000), (6, 3000), (1, 4096), (1792, 4096), (16384, 2056)]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", X8_SHAPES)
+def test_eight_wave_group(hip, n, k, m, monkeypatch):
+    """The 14-wave kernel's layout on one group of 8 waves (K <= 4096: one
+    window per lane, x in registers), forced with DMC_HIP_RD_X8=2: C2
+    up/gate, a partial last workgroup (n = 4097), lanes past K (k = 4000,
+    3000, 2056), fewer rows than one workgroup (n = 6, a lone row), a TP = 8
+    share, 1024 workgroups.  Edge data; the oracle's result within the
+    parity rule and, row by row, the elementwise bound; two launches bit for
+    bit alike."""
+    x, w = case(m, k, n, seed=7700 + n + k + m, edge=True)
+    monkeypatch.setenv("DMC_HIP_RD_X8", "2")
+    p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.mt, p.grid_x) == (8, 4, 16, 1, m, -(-n // 16)), p
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
+    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"x8 m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [4096, 2056])
+def test_eight_wave_group_zero_rule(hip, k, m, monkeypatch):
+    """Exact zeros on the 8-wave group, one to four activation rows: the
+    patterns of test_shared_x_fourteen_waves_zero_rule, bit for bit the
+    reference."""
+    monkeypatch.setenv("DMC_HIP_RD_X8", "2")
+    n = 4096
+    assert hip.plan("rd", m, k, n, x_addr=256, w_addr=256).waves == 8
+    x = np.full((m, k), np.float32(-1e-38), np.float32)
+    x[1::2] = -x[1::2]
     w = np.full((n, k), 0x0001, np.uint16)
     w[1::2, :] = 0x8001
     y_ref = ref(x, w)
