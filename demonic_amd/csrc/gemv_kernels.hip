@@ -793,10 +793,9 @@ constexpr int kX14MaxM = 4;
 
 __device__ float chain_f32(const float *__restrict__ w, const float *__restrict__ x, int K);
 
-template <typename WT, int KV, int MT, int NS = kX14Waves>
-__global__ void __launch_bounds__(64 * NS)
-gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N, int K,
-                          int64_t ys_act, int64_t ys_row) {
+template <typename WT, int KV, int MT, int NS>
+__device__ __forceinline__ void rd_group_body(const WT *__restrict__ W, const float *__restrict__ X,
+                                              float *__restrict__ Y, int N, int K, int64_t ys_act, int64_t ys_row) {
     constexpr bool F32 = sizeof(WT) == 4;
     constexpr int EW = 16 / sizeof(WT);  // weights per window
     // Rows per register buffer (a lane has 128 registers at 14 waves per CU;
@@ -939,6 +938,22 @@ gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X,
             const int m = MT == 1 ? 0 : t / nr, r = MT == 1 ? t : t - m * nr;
             Y[(int64_t)m * ys_act + (int64_t)(rb + r) * ys_row] = v;
         });
+}
+
+template <typename WT, int KV, int MT>
+__global__ void __launch_bounds__(64 * kX14Waves)
+gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N, int K,
+                          int64_t ys_act, int64_t ys_row) {
+    rd_group_body<WT, KV, MT, kX14Waves>(W, X, Y, N, K, ys_act, ys_row);
+}
+
+// The same on one group of 8 waves: bf16 rows of K <= 4096, one window per
+// lane.
+template <int MT>
+__global__ void __launch_bounds__(512)
+gemv_rd_stream_x8_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                         int K, int64_t ys_act, int64_t ys_row) {
+    rd_group_body<uint16_t, 1, MT, 8>(W, X, Y, N, K, ys_act, ys_row);
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -3947,7 +3962,7 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             p.k > 8 * 512 || p.k < 1)
             return hipErrorInvalidValue;
 #define DMC_X8(MT)                                                                                           \
-    hipLaunchKernelGGL((gemv_rd_stream_x14_kernel<uint16_t, 1, MT, 8>), dim3((unsigned)pl.grid_x), dim3(512), \
+    hipLaunchKernelGGL((gemv_rd_stream_x8_kernel<MT>), dim3((unsigned)pl.grid_x), dim3(512),                 \
                        0, s, p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
         switch ((int)p.m) {
         case 1: DMC_X8(1); break;
