@@ -778,7 +778,8 @@ gemv_rd_stream_xlds_kernel(const uint16_t *__restrict__ W, const float *__restri
 // 16-byte windows t + j*NT of a row (NT = 896 threads; 8 bf16 or 4 f32
 // weights each), so at K = 14336 every load instruction carries data.  The
 // same layout on NS = 8 waves (NT = 512, one window per lane) serves bf16
-// rows of K <= 4096, three or four workgroups to a CU.  A
+// rows of K <= 4096, three or four workgroups to a CU, and on NS = 4 rows of
+// K <= 2048.  A
 // window's x is the lane's alone, so each lane loads its MT activation rows'
 // windows straight into registers (56 KiB of x per activation row and
 // workgroup, one workgroup per CU).  The workgroup's 16 rows stream ROWS at a
@@ -947,13 +948,20 @@ gemv_rd_stream_x14_kernel(const WT *__restrict__ W, const float *__restrict__ X,
     rd_group_body<WT, KV, MT, kX14Waves>(W, X, Y, N, K, ys_act, ys_row);
 }
 
-// The same on one group of 8 waves: bf16 rows of K <= 4096, one window per
-// lane.
+// The same on one group of 8 waves (bf16 rows of K <= 4096) or of 4 (K <=
+// 2048), one window per lane.
 template <int MT>
 __global__ void __launch_bounds__(512)
 gemv_rd_stream_x8_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                          int K, int64_t ys_act, int64_t ys_row) {
     rd_group_body<uint16_t, 1, MT, 8>(W, X, Y, N, K, ys_act, ys_row);
+}
+
+template <int MT>
+__global__ void __launch_bounds__(256)
+gemv_rd_stream_x4_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                         int K, int64_t ys_act, int64_t ys_row) {
+    rd_group_body<uint16_t, 1, MT, 4>(W, X, Y, N, K, ys_act, ys_row);
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -3404,42 +3412,54 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
     }
     const int64_t cus = num_cus > 0 ? num_cus : 256;
 
-    // One to four activation rows on rows of 2048 < K <= 4096: the 14-wave
-    // kernel's layout on one group of 8 waves (a window per lane, x in
-    // registers, 16 rows per workgroup, zeros settled after the stream; 3 or
-    // 4 workgroups share a CU).  Same boxes, 8-wave group / default, us, K =
-    // 4096 unless named:
+    // One to four activation rows on rows of 1024 < K <= 4096: the 14-wave
+    // kernel's layout on one group of 8 waves, or of 4 for K <= 2048 (a
+    // window per lane, x in registers, 16 rows per workgroup, zeros settled
+    // after the stream; 3 or 4 workgroups share a CU at 8 waves).  Same
+    // boxes, group / default, us:
     // - M = 1, where the groups spread evenly over at most two rounds: C1
-    //   6.66 / 6.88, [8192,4096] 11.36 / 11.61, [4096,3072] 5.47 / 6.34;
-    //   elsewhere the 4-row streaming workgroups win ([5120,4096] 9.09 /
-    //   8.03, [28672,4096] 34.65 / 33.77, [1024,4096] 4.62 / 3.32);
-    // - M = 2 from 3/4 of a round: C2 up 19.41-19.46 / 20.03-20.08, C1 7.11 /
-    //   7.97, [12288,4096] 16.38 / 17.50 ([5120,4096] the loss, 9.85 / 9.41);
-    // - M = 3 everywhere: C2 up 20.10-20.29 / 20.82-20.91 (rows16), [1024,4096]
-    //   5.95 / 6.99, [12288,4096] 16.96 / 19.85;
-    // - M = 4 except between one and two rounds of resident groups (three
-    //   per CU): [12288,4096] 17.90 / 19.88, TP = 8 gate/up [1792,4096] 6.56
-    //   / 7.25, C4 150.6 / 153.1, [28672,4096] 37.2-37.7 / 38.0-38.2; C2 up's
-    //   896 groups leave a short second round (21.14-21.47 / 20.83-20.86).
-    // C4 at M = 2 / 3: 145.4 / 146.4 against 146.5 / 154.2.
-    // At K = 2048 half the lanes would hold no window ([4096,2048] lost at
-    // every M).  DMC_HIP_RD_X8: 0 never, 2 wherever it applies (K <= 4096);
+    //   6.66 / 6.88, [8192,4096] 11.36 / 11.61, [4096,3072] 5.47 / 6.34; on 4
+    //   waves TP = 8 down [4096,1792] 4.07 / 4.51, [8192,2048] 6.69 / 7.17,
+    //   [4096,1536] 3.86 / 4.30; elsewhere the 4-row streaming workgroups win
+    //   ([5120,4096] 9.09 / 8.03, [28672,4096] 34.65 / 33.77, [1024,4096] 4.62
+    //   / 3.32, [2048,2048] 3.73 / 3.55);
+    // - 8 waves, M = 2 from 3/4 of a round: C2 up 19.41-19.46 / 20.03-20.08,
+    //   C1 7.11 / 7.97, [12288,4096] 16.38 / 17.50 ([5120,4096] the loss, 9.85
+    //   / 9.41);
+    // - 8 waves, M = 3 everywhere: C2 up 20.10-20.29 / 20.82-20.91 (rows16),
+    //   [1024,4096] 5.95 / 6.99, [12288,4096] 16.96 / 19.85;
+    // - 8 waves, M = 4 except between one and two rounds of resident groups
+    //   (three per CU): [12288,4096] 17.90 / 19.88, TP = 8 gate/up
+    //   [1792,4096] 6.56 / 7.25, C4 150.6 / 153.1, [28672,4096] 37.2-37.7 /
+    //   38.0-38.2; C2 up's 896 groups leave a short second round (21.14-21.47
+    //   / 20.83-20.86).  C4 at M = 2 / 3: 145.4 / 146.4 against 146.5 / 154.2;
+    // - 4 waves, M = 2 to 4 on full windows (K > 1792) from two rounds:
+    //   [8192,2048] 6.95 / 7.63 / 7.30 against 7.88 / 9.06 / 9.10, [14336,2048]
+    //   11.30 / 11.94 / 12.46 against 11.37 / 12.57 / 12.61 (TP = 8 down at
+    //   one round: 5.12 / 5.47 / 5.67 against 5.04 / 5.42 / 5.44).
+    // At K = 2048 on 8 waves, or 1024 on 4, half the lanes would hold no
+    // window ([4096,2048] and [16384,1024] lost at every M).  DMC_HIP_RD_X8:
+    // 0 never, 2 wherever it applies (K <= 4096, 4 waves for K <= 2048);
     // explicit MFMA, rows16 or rows-per-step settings keep their kernels.
     const int x8 = env_int("DMC_HIP_RD_X8", 1);
     const int64_t g16x = (p.n + 15) / 16;
-    const bool x8_auto = x8 == 1 && p.k > 2048 && env_int("DMC_HIP_RD_XLDS", 1) != 2 &&
-                         env_int("DMC_HIP_RD_MFMA_KIND", 0) == 0 && env_int("DMC_HIP_RD_MFMA_MIN_M", -1) < 0 &&
-                         env_int("DMC_HIP_RD_ROWS", 0) == 0 && env_int("DMC_HIP_RD_R16_TILES", 0) == 0 &&
-                         env_int("DMC_HIP_RD_R16_SPLIT", -1) < 0 &&
-                         (p.m == 1   ? g16x % cus == 0 && g16x <= 2 * cus
-                          : p.m == 2 ? 4 * g16x >= 3 * cus
-                          : p.m == 3 ? true
-                                     : g16x <= 3 * cus || g16x >= 6 * cus);
+    const int gw = p.k <= 4 * 512 ? 4 : 8;  // waves per group
+    const bool x8_env_ok = env_int("DMC_HIP_RD_XLDS", 1) != 2 && env_int("DMC_HIP_RD_MFMA_KIND", 0) == 0 &&
+                           env_int("DMC_HIP_RD_MFMA_MIN_M", -1) < 0 && env_int("DMC_HIP_RD_ROWS", 0) == 0 &&
+                           env_int("DMC_HIP_RD_R16_TILES", 0) == 0 && env_int("DMC_HIP_RD_R16_SPLIT", -1) < 0;
+    const bool even = g16x % cus == 0 && g16x <= 2 * cus;
+    const bool x8_auto =
+        x8 == 1 && x8_env_ok &&
+        (gw == 8 ? (p.m == 1   ? even
+                    : p.m == 2 ? 4 * g16x >= 3 * cus
+                    : p.m == 3 ? true
+                               : g16x <= 3 * cus || g16x >= 6 * cus)
+                 : p.k > 1024 && (p.m == 1 ? even : p.k > 1792 && g16x >= 2 * cus));
     if ((x8 == 2 || x8_auto) && p.m >= 1 && p.m <= kX14MaxM && pl.vec == 8 && p.ldw == p.k && p.ldx == p.k &&
         p.ldy == p.n && p.k > 0 && p.k <= 8 * 512) {
         RdPlan xp{};
         xp.vec = 8;
-        xp.waves = 8;
+        xp.waves = gw;
         xp.xreg8 = true;
         xp.kvec = 1;
         xp.rows = 4;
@@ -3956,6 +3976,22 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
+    }
+    if (pl.kvec > 0 && pl.xreg8 && pl.waves == 4) {
+        if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec != 1 || p.k > 4 * 512 || p.k < 1)
+            return hipErrorInvalidValue;
+#define DMC_X4(MT)                                                                                           \
+    hipLaunchKernelGGL((gemv_rd_stream_x4_kernel<MT>), dim3((unsigned)pl.grid_x), dim3(256), 0, s, p.w, p.x,  \
+                       p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
+        switch ((int)p.m) {
+        case 1: DMC_X4(1); break;
+        case 2: DMC_X4(2); break;
+        case 3: DMC_X4(3); break;
+        case 4: DMC_X4(4); break;
+        default: return hipErrorInvalidValue;
+        }
+#undef DMC_X4
+        return hipGetLastError();
     }
     if (pl.kvec > 0 && pl.xreg8) {
         if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec != 1 || pl.waves != 8 ||

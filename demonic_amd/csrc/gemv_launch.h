@@ -80,7 +80,7 @@ struct RdPlan {
     // rows
     bool any_align = false;
     int rstep = 1;
-    bool xreg8 = false;  // the 14-wave kernel's layout on 8 waves (K <= 4096)
+    bool xreg8 = false;  // the 14-wave kernel's layout on `waves` = 8 (K <= 4096) or 4 (K <= 2048)
     size_t workspace_bytes = 0;
 };
 

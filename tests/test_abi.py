@@ -186,7 +186,16 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 2048), p
     monkeypatch.delenv("DMC_HIP_RD_X8")
     assert d.plan("rd", 1, 4096, 5120, x_addr=256, w_addr=256).rows_per_group == 4  # 320 groups: uneven
-    assert d.plan("rd", 1, 2048, 4096, x_addr=256, w_addr=256).rows_per_group == 4  # K = 2048: half the lanes idle
+    # 1024 < K <= 2048: the same group on 4 waves (TP = 8 down share, [4096,2048]); at K = 1024 half
+    # its lanes would idle; at 2 to 4 rows only on full windows from two rounds
+    for k in (1792, 2048):
+        p = d.plan("rd", 1, k, 4096, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 16, 256), p
+    assert d.plan("rd", 1, 1024, 4096, x_addr=256, w_addr=256).rows_per_group == 4
+    p = d.plan("rd", 3, 2048, 8192, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.mt, p.grid_x) == (4, 4, 16, 3, 512), p
+    assert d.plan("rd", 2, 2048, 4096, x_addr=256, w_addr=256).rows_per_group != 16   # one round
+    assert d.plan("rd", 2, 1792, 8192, x_addr=256, w_addr=256).rows_per_group != 16   # windows not full
     p = d.plan("rd", 1, 4096, 11008, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group) == (2, 4), p
     # M = 1: the streaming kernel

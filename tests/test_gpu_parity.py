@@ -1269,6 +1269,50 @@ def test_eight_wave_group_zero_rule(hip, k, m, monkeypatch):
         np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
 
 
+X4_SHAPES = [(4096, 1792), (4097, 2048), (1030, 1000), (6, 1504), (1, 2048), (8192, 2048), (300, 64)]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", X4_SHAPES)
+def test_four_wave_group(hip, n, k, m, monkeypatch):
+    """The same group on 4 waves (K <= 2048), forced with DMC_HIP_RD_X8=2:
+    TP = 8's down share, a partial last workgroup (n = 4097), lanes past K
+    (k = 1792, 1000, 1504, 64), fewer rows than one workgroup, two rounds
+    (n = 8192).  Edge data; the parity rule and, row by row, the bound; two
+    launches bit for bit alike."""
+    x, w = case(m, k, n, seed=7900 + n + k + m, edge=True)
+    monkeypatch.setenv("DMC_HIP_RD_X8", "2")
+    p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.mt, p.grid_x) == (4, 4, 16, 1, m, -(-n // 16)), p
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
+    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"x4 m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("k", [2048, 1032])
+def test_four_wave_group_zero_rule(hip, k, m, monkeypatch):
+    """Exact zeros on the 4-wave group: the patterns of
+    test_shared_x_fourteen_waves_zero_rule, bit for bit the reference."""
+    monkeypatch.setenv("DMC_HIP_RD_X8", "2")
+    n = 4096
+    assert hip.plan("rd", m, k, n, x_addr=256, w_addr=256).waves == 4
+    x = np.full((m, k), np.float32(-1e-38), np.float32)
+    x[1::2] = -x[1::2]
+    w = np.full((n, k), 0x0001, np.uint16)
+    w[1::2, :] = 0x8001
+    y_ref = ref(x, w)
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32))
+    xm, wz = zero_rows(k, 9)
+    w = np.ascontiguousarray(wz[np.arange(n) % 9])
+    xm = np.ascontiguousarray(xm[(2 + np.arange(m)) % 4])
+    y_ref = ref(xm, w)
+    y = _rd_dev(hip, xm, w)
+    assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
+        np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
+
+
 # ---- prefill-sized M on the gemm layout (16 * MB activation rows per workgroup) --------
 
 @pytest.mark.parametrize("fuse", [0, 2])
