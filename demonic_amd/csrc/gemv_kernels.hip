@@ -794,7 +794,7 @@ constexpr int kX14MaxM = 4;
 
 __device__ float chain_f32(const float *__restrict__ w, const float *__restrict__ x, int K);
 
-template <typename WT, int KV, int MT, int NS>
+template <typename WT, int KV, int MT, int NS, int RPW_ = 16, int ROWS_ = 0>
 __device__ __forceinline__ void rd_group_body(const WT *__restrict__ W, const float *__restrict__ X,
                                               float *__restrict__ Y, int N, int K, int64_t ys_act, int64_t ys_row) {
     constexpr bool F32 = sizeof(WT) == 4;
@@ -804,8 +804,9 @@ __device__ __forceinline__ void rd_group_body(const WT *__restrict__ W, const fl
     // at MT = 4 with two windows (122 registers in all at KV = 2, MT = 3);
     // f32 2 up to MT = 2, then 1.  On 8 waves (KV = 1) the same rows take 54
     // to 76 registers.
-    constexpr int ROWS = F32 ? (MT <= 2 ? 2 : 1) : MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2;
-    constexpr int NT = 64 * NS, RPW = 16;
+    constexpr int ROWS = ROWS_ ? ROWS_ : F32 ? (MT <= 2 ? 2 : 1) : MT == 1 ? 4 : MT == 4 && KV == 2 ? 1 : 2;
+    constexpr int NT = 64 * NS, RPW = RPW_;
+    static_assert(RPW % ROWS == 0, "rows per workgroup");
     static_assert(KV * NS * 64 * EW <= kX14MaxK, "windows");
     static_assert(MT >= 1 && MT <= kX14MaxM, "activation rows");
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -847,7 +848,7 @@ __device__ __forceinline__ void rd_group_body(const WT *__restrict__ W, const fl
             for (int j = 0; j < KV; ++j) wv[q][j] = load_w16(rs, eoff[j], (uint32_t)(i0 + q) * row_bytes);
     };
     load(ba, 0);
-    load(bb, ROWS);
+    if constexpr (ROWS < RPW) load(bb, ROWS);
     __builtin_amdgcn_sched_barrier(0);
     float xr[MT][KV][EW];
 #pragma unroll
@@ -890,8 +891,10 @@ __device__ __forceinline__ void rd_group_body(const WT *__restrict__ W, const fl
     for (int i0 = 0; i0 < RPW; i0 += 2 * ROWS) {
         sum_rows(ba, i0);
         if (i0 + 2 * ROWS < RPW) load(ba, i0 + 2 * ROWS);
-        sum_rows(bb, i0 + ROWS);
-        if (i0 + 3 * ROWS < RPW) load(bb, i0 + 3 * ROWS);
+        if (i0 + ROWS < RPW) {
+            sum_rows(bb, i0 + ROWS);
+            if (i0 + 3 * ROWS < RPW) load(bb, i0 + 3 * ROWS);
+        }
     }
     __syncthreads();
     // Outputs t < MT * nr: activation row t / nr, weight row t % nr.
@@ -962,6 +965,15 @@ __global__ void __launch_bounds__(256)
 gemv_rd_stream_x4_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                          int K, int64_t ys_act, int64_t ys_row) {
     rd_group_body<uint16_t, 1, MT, 4>(W, X, Y, N, K, ys_act, ys_row);
+}
+
+// One 8-wave group per CU at one activation row: RPW rows per workgroup
+// (N = RPW * CUs), ROWS per register buffer.
+template <int RPW, int ROWS>
+__global__ void __launch_bounds__(512)
+gemv_rd_stream_x8r_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                          int K, int64_t ys_act, int64_t ys_row) {
+    rd_group_body<uint16_t, 1, 1, 8, RPW, ROWS>(W, X, Y, N, K, ys_act, ys_row);
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -3448,9 +3460,18 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
                            env_int("DMC_HIP_RD_MFMA_MIN_M", -1) < 0 && env_int("DMC_HIP_RD_ROWS", 0) == 0 &&
                            env_int("DMC_HIP_RD_R16_TILES", 0) == 0 && env_int("DMC_HIP_RD_R16_SPLIT", -1) < 0;
     const bool even = g16x % cus == 0 && g16x <= 2 * cus;
+    // One activation row on N = r * CUs rows, r = 4, 6, 7, 8, 10, 12 or 14
+    // (8 waves): one group of r rows per CU.  Same box, group / default, us:
+    // [1024,4096] 3.30 / 3.46 (the drop-in's stacked k/v heads), [1536,4096]
+    // 3.93 / 4.39, TP = 8 gate/up [1792,4096] 4.20 / 4.54, [2048,4096] 4.40 /
+    // 4.70, [2560,4096] 5.07 / 5.60, [3072,4096] 5.52 / 5.80, [3584,4096] 6.09
+    // / 6.71, [1792,3072] 3.78 / 4.33 (16-row groups there: 4.38-5.13).
+    const int64_t rpc = p.n % cus == 0 ? p.n / cus : 0;
+    const bool per_cu = p.m == 1 && gw == 8 &&
+                        (rpc == 4 || rpc == 6 || rpc == 7 || rpc == 8 || rpc == 10 || rpc == 12 || rpc == 14);
     const bool x8_auto =
         x8 == 1 && x8_env_ok &&
-        (gw == 8 ? (p.m == 1   ? even
+        (gw == 8 ? (p.m == 1   ? even || per_cu
                     : p.m == 2 ? 4 * g16x >= 3 * cus
                     : p.m == 3 ? true
                                : g16x <= 3 * cus || g16x >= 6 * cus)
@@ -3467,6 +3488,11 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
         xp.mt = (int)p.m;
         xp.grid_x = g16x;
         xp.grid_y = 1;
+        if (per_cu) {
+            xp.rpw = (int)rpc;
+            xp.rows = rpc <= 8 ? (int)rpc : (int)rpc / 2;
+            xp.grid_x = cus;
+        }
         return xp;
     }
 
@@ -3976,6 +4002,22 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
             return hipGetLastError();
         }
         return hipErrorInvalidValue;
+    }
+    if (pl.kvec > 0 && pl.xreg8 && pl.waves == 8 && pl.rpw != 16) {
+        if (p.m != 1 || pl.kvec != 1 || p.k > 8 * 512 || p.k < 1) return hipErrorInvalidValue;
+#define DMC_X8R(R, Q)                                                                                         \
+    hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, p.w, p.x, \
+                       p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
+        if (pl.rpw == 4 && pl.rows == 4) DMC_X8R(4, 4);
+        else if (pl.rpw == 6 && pl.rows == 6) DMC_X8R(6, 6);
+        else if (pl.rpw == 7 && pl.rows == 7) DMC_X8R(7, 7);
+        else if (pl.rpw == 8 && pl.rows == 8) DMC_X8R(8, 8);
+        else if (pl.rpw == 10 && pl.rows == 5) DMC_X8R(10, 5);
+        else if (pl.rpw == 12 && pl.rows == 6) DMC_X8R(12, 6);
+        else if (pl.rpw == 14 && pl.rows == 7) DMC_X8R(14, 7);
+        else return hipErrorInvalidValue;
+#undef DMC_X8R
+        return hipGetLastError();
     }
     if (pl.kvec > 0 && pl.xreg8 && pl.waves == 4) {
         if (pl.rpw != 16 || p.m != pl.mt || p.m < 1 || p.m > kX14MaxM || pl.kvec != 1 || p.k > 4 * 512 || p.k < 1)

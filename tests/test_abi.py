@@ -173,8 +173,18 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # per CU, then 2 rows per step (C2 up/gate above)
     small = d.plan("rd", 1, 4096, 1024, x_addr=256, w_addr=256)
     assert (small.rows_or_rw, small.rows_per_group, small.grid_x) == (4, 4, 256), small
-    p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)  # one GPU's gate/up share under TP = 8
+    # one GPU's gate/up share under TP = 8, 1792 = 7 * 256 rows: one 8-wave group of 7 rows per CU
+    # (the streaming kernel's 4-row workgroups with DMC_HIP_RD_X8=0)
+    p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)
+    assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (7, 7, 256), p
+    for n, r in ((1024, 4), (1536, 6), (2560, 10), (3584, 14)):
+        p = d.plan("rd", 1, 4096, n, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, r if r <= 8 else r // 2, r, 256), p
+    assert d.plan("rd", 1, 4096, 1280, x_addr=256, w_addr=256).rows_per_group == 4  # 5 rows per CU: not taken
+    monkeypatch.setenv("DMC_HIP_RD_X8", "0")
+    p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 448), p
+    monkeypatch.delenv("DMC_HIP_RD_X8")
     # ... except where one group of 8 waves per 16 rows (x in registers, a
     # window per lane) spreads evenly over at most two rounds (C1: 256 groups;
     # [8192,4096]: 512)

@@ -1223,6 +1223,7 @@ def test_shared_x_fourteen_waves_zero_rule(hip, k, m, monkeypatch):
 
 
 X8_SHAPES = [(14336, 4096), (4097, 4096), (1030, 4000), (6, 3000), (1, 4096), (1792, 4096), (16384, 2056)]
+PER_CU_ROWS = (4, 6, 7, 8, 10, 12, 14)
 
 
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
@@ -1238,7 +1239,9 @@ def test_eight_wave_group(hip, n, k, m, monkeypatch):
     x, w = case(m, k, n, seed=7700 + n + k + m, edge=True)
     monkeypatch.setenv("DMC_HIP_RD_X8", "2")
     p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
-    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.mt, p.grid_x) == (8, 4, 16, 1, m, -(-n // 16)), p
+    rpc = n // 256 if m == 1 and n % 256 == 0 and n // 256 in PER_CU_ROWS else 0  # one group per CU
+    want = (8, rpc if rpc <= 8 else rpc // 2, rpc, 1, m, 256) if rpc else (8, 4, 16, 1, m, -(-n // 16))
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.mt, p.grid_x) == want, p
     y = _rd_dev(hip, x, w)
     assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
     check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"x8 m={m} n={n} k={k}")
@@ -1267,6 +1270,31 @@ def test_eight_wave_group_zero_rule(hip, k, m, monkeypatch):
     y = _rd_dev(hip, xm, w)
     assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
         np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
+
+
+@pytest.mark.parametrize("n,k", [(1024, 4096), (1536, 4096), (1792, 4096), (2048, 4000), (2560, 4096),
+                                 (3072, 3000), (3584, 4096), (1792, 2056)])
+def test_one_group_per_cu(hip, n, k):
+    """One activation row on N = r * 256 rows (r = 4 .. 14): one 8-wave
+    group of r rows per CU, the planner's own choice (the drop-in's stacked
+    k/v heads, TP = 8's gate/up share), with lanes past K (k = 4000, 3000,
+    2056).  Edge data within the parity rule and, row by row, the bound; the
+    zero rule's patterns bit for bit the reference."""
+    p = hip.plan("rd", 1, k, n, x_addr=256, w_addr=256)
+    r = n // 256
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, r if r <= 8 else r // 2, r, 256), p
+    x, w = case(1, k, n, seed=7800 + n + k, edge=True)
+    y = _rd_dev(hip, x, w)
+    assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
+    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"group per CU n={n} k={k}")
+    xm, wz = zero_rows(k, 9)
+    wz = np.ascontiguousarray(wz[np.arange(n) % 9])
+    for row in range(4):
+        xr = np.ascontiguousarray(xm[row:row + 1])
+        y_ref = ref(xr, wz)
+        y = _rd_dev(hip, xr, wz)
+        assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
+            (row, np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8])
 
 
 X4_SHAPES = [(4096, 1792), (4097, 2048), (1030, 1000), (6, 1504), (1, 2048), (8192, 2048), (300, 64)]
