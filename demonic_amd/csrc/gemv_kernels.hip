@@ -967,13 +967,13 @@ gemv_rd_stream_x4_kernel(const uint16_t *__restrict__ W, const float *__restrict
     rd_group_body<uint16_t, 1, MT, 4>(W, X, Y, N, K, ys_act, ys_row);
 }
 
-// One 8-wave group per CU at one activation row: RPW rows per workgroup
-// (N = RPW * CUs), ROWS per register buffer.
-template <int RPW, int ROWS>
+// One 8-wave group per CU: RPW rows per workgroup (N = RPW * CUs), ROWS per
+// register buffer, MT activation rows.
+template <int RPW, int ROWS, int MT = 1>
 __global__ void __launch_bounds__(512)
 gemv_rd_stream_x8r_kernel(const uint16_t *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
                           int K, int64_t ys_act, int64_t ys_row) {
-    rd_group_body<uint16_t, 1, 1, 8, RPW, ROWS>(W, X, Y, N, K, ys_act, ys_row);
+    rd_group_body<uint16_t, 1, MT, 8, RPW, ROWS>(W, X, Y, N, K, ys_act, ys_row);
 }
 
 // ---- RD streaming, rows at any 2-byte alignment (odd K, offset views) ----------
@@ -3460,18 +3460,24 @@ RdPlan plan_rd(const RdProblem &p, int num_cus) {
                            env_int("DMC_HIP_RD_MFMA_MIN_M", -1) < 0 && env_int("DMC_HIP_RD_ROWS", 0) == 0 &&
                            env_int("DMC_HIP_RD_R16_TILES", 0) == 0 && env_int("DMC_HIP_RD_R16_SPLIT", -1) < 0;
     const bool even = g16x % cus == 0 && g16x <= 2 * cus;
-    // One activation row on N = r * CUs rows, r = 4, 6, 7, 8, 10, 12 or 14
-    // (8 waves): one group of r rows per CU.  Same box, group / default, us:
+    // N = r * CUs rows, r = 4, 6, 7, 8, 10, 12 or 14 (8 waves): one group of
+    // r rows per CU.  Same box, group / default, us: one activation row,
     // [1024,4096] 3.30 / 3.46 (the drop-in's stacked k/v heads), [1536,4096]
     // 3.93 / 4.39, TP = 8 gate/up [1792,4096] 4.20 / 4.54, [2048,4096] 4.40 /
     // 4.70, [2560,4096] 5.07 / 5.60, [3072,4096] 5.52 / 5.80, [3584,4096] 6.09
-    // / 6.71, [1792,3072] 3.78 / 4.33 (16-row groups there: 4.38-5.13).
+    // / 6.71, [1792,3072] 3.78 / 4.33 (16-row groups there: 4.38-5.13); two to
+    // four rows up to r = 12, m = 2 / 3 / 4: [1024,4096] 3.67 / 3.93 / 4.24
+    // against 4.09 / 6.03 / 6.42, TP = 8 gate/up 4.51 / 5.01 / 5.39 against
+    // 5.80 / 6.29 / 6.64, [3072,4096] 5.86 / 6.51 / 7.00 against 6.03 / 6.83 /
+    // 7.15 (r = 14 lost: [3584,4096] 6.58 / 7.32 / 7.83 against 6.39 / 7.05 /
+    // 7.37).
     const int64_t rpc = p.n % cus == 0 ? p.n / cus : 0;
-    const bool per_cu = p.m == 1 && gw == 8 &&
-                        (rpc == 4 || rpc == 6 || rpc == 7 || rpc == 8 || rpc == 10 || rpc == 12 || rpc == 14);
+    const bool per_cu = gw == 8 && (rpc == 4 || rpc == 6 || rpc == 7 || rpc == 8 || rpc == 10 || rpc == 12 || rpc == 14) &&
+                        (p.m == 1 || (p.m <= 4 && rpc <= 12));
     const bool x8_auto =
         x8 == 1 && x8_env_ok &&
         (gw == 8 ? (p.m == 1   ? even || per_cu
+                    : per_cu   ? true
                     : p.m == 2 ? 4 * g16x >= 3 * cus
                     : p.m == 3 ? true
                                : g16x <= 3 * cus || g16x >= 6 * cus)
@@ -4004,10 +4010,19 @@ hipError_t launch_rd(const RdProblem &p, const RdPlan &pl, void *workspace, hipS
         return hipErrorInvalidValue;
     }
     if (pl.kvec > 0 && pl.xreg8 && pl.waves == 8 && pl.rpw != 16) {
-        if (p.m != 1 || pl.kvec != 1 || p.k > 8 * 512 || p.k < 1) return hipErrorInvalidValue;
+        if (p.m < 1 || p.m > 4 || p.m != pl.mt || pl.kvec != 1 || p.k > 8 * 512 || p.k < 1)
+            return hipErrorInvalidValue;
 #define DMC_X8R(R, Q)                                                                                         \
-    hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, p.w, p.x, \
-                       p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1)
+    do switch ((int)p.m) {                                                                                    \
+    case 1: hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q, 1>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, \
+                               p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1); break;          \
+    case 2: hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q, 2>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, \
+                               p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1); break;          \
+    case 3: hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q, 3>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, \
+                               p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1); break;          \
+    default: hipLaunchKernelGGL((gemv_rd_stream_x8r_kernel<R, Q, 4>), dim3((unsigned)pl.grid_x), dim3(512), 0, \
+                               s, p.w, p.x, p.y, (int)p.n, (int)p.k, (int64_t)p.ldy, (int64_t)1); break;       \
+    } while (0)
         if (pl.rpw == 4 && pl.rows == 4) DMC_X8R(4, 4);
         else if (pl.rpw == 6 && pl.rows == 6) DMC_X8R(6, 6);
         else if (pl.rpw == 7 && pl.rows == 7) DMC_X8R(7, 7);

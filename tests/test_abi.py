@@ -181,6 +181,10 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
         p = d.plan("rd", 1, 4096, n, x_addr=256, w_addr=256)
         assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, r if r <= 8 else r // 2, r, 256), p
     assert d.plan("rd", 1, 4096, 1280, x_addr=256, w_addr=256).rows_per_group == 4  # 5 rows per CU: not taken
+    for m in (2, 3, 4):  # two to four activation rows up to 12 rows per CU
+        p = d.plan("rd", m, 4096, 1792, x_addr=256, w_addr=256)
+        assert (p.waves, p.rows_or_rw, p.rows_per_group, p.mt, p.grid_x) == (8, 7, 7, m, 256), p
+        assert d.plan("rd", m, 4096, 3584, x_addr=256, w_addr=256).rows_per_group != 14
     monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     p = d.plan("rd", 1, 4096, 1792, x_addr=256, w_addr=256)
     assert (p.rows_or_rw, p.rows_per_group, p.grid_x) == (4, 4, 448), p
@@ -216,11 +220,13 @@ def test_rowdot_plans_at_decode_shapes(monkeypatch):
     # kernel, 16 weight rows per workgroup where the grid keeps 4 workgroups
     # per CU (8 on C2 up/gate); rows16 where rows too long for the streaming
     # kernel's registers would take one activation row per pass
-    for n in (128256, 14336, 4096, 3072):
+    for n in (128256, 14336, 4096):
         p = d.plan("rd", 2, 4096, n, x_addr=256, w_addr=256)
         assert (p.waves, p.rows_or_rw, p.slices, p.mt, p.rows_per_group, p.grid_x) == \
             (8, 4, 1, 2, 16, n // 16), p
-    assert d.plan("rd", 2, 4096, 1792, x_addr=256, w_addr=256).rows_or_rw == 2  # 112 groups
+    p = d.plan("rd", 2, 4096, 3072, x_addr=256, w_addr=256)  # 12 rows per CU: one group each
+    assert (p.waves, p.rows_or_rw, p.slices, p.mt, p.rows_per_group, p.grid_x) == (8, 6, 1, 2, 12, 256), p
+    assert d.plan("rd", 2, 4096, 1280, x_addr=256, w_addr=256).rows_or_rw == 2  # 80 groups of 16: streaming
     monkeypatch.setenv("DMC_HIP_RD_X8", "0")
     p = d.plan("rd", 2, 4096, 128256, x_addr=256, w_addr=256)
     assert (p.slices, p.mt, p.rows_per_group, p.grid_x) == (1, 2, 16, 8016), p

@@ -1239,7 +1239,7 @@ def test_eight_wave_group(hip, n, k, m, monkeypatch):
     x, w = case(m, k, n, seed=7700 + n + k + m, edge=True)
     monkeypatch.setenv("DMC_HIP_RD_X8", "2")
     p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
-    rpc = n // 256 if m == 1 and n % 256 == 0 and n // 256 in PER_CU_ROWS else 0  # one group per CU
+    rpc = n // 256 if n % 256 == 0 and n // 256 in PER_CU_ROWS and (m == 1 or n // 256 <= 12) else 0  # per CU
     want = (8, rpc if rpc <= 8 else rpc // 2, rpc, 1, m, 256) if rpc else (8, 4, 16, 1, m, -(-n // 16))
     assert (p.waves, p.rows_or_rw, p.rows_per_group, p.slices, p.mt, p.grid_x) == want, p
     y = _rd_dev(hip, x, w)
@@ -1272,25 +1272,31 @@ def test_eight_wave_group_zero_rule(hip, k, m, monkeypatch):
         np.flatnonzero(y.view(np.uint32) != y_ref.view(np.uint32))[:8]
 
 
-@pytest.mark.parametrize("n,k", [(1024, 4096), (1536, 4096), (1792, 4096), (2048, 4000), (2560, 4096),
-                                 (3072, 3000), (3584, 4096), (1792, 2056)])
-def test_one_group_per_cu(hip, n, k):
-    """One activation row on N = r * 256 rows (r = 4 .. 14): one 8-wave
-    group of r rows per CU, the planner's own choice (the drop-in's stacked
-    k/v heads, TP = 8's gate/up share), with lanes past K (k = 4000, 3000,
-    2056).  Edge data within the parity rule and, row by row, the bound; the
-    zero rule's patterns bit for bit the reference."""
-    p = hip.plan("rd", 1, k, n, x_addr=256, w_addr=256)
+PER_CU_CASES = [(n, k, m) for (n, k) in [(1024, 4096), (1536, 4096), (1792, 4096), (2048, 4000), (2560, 4096),
+                                         (3072, 3000), (3584, 4096), (1792, 2056)]
+                for m in (1, 2, 3, 4) if m == 1 or n // 256 <= 12]
+
+
+@pytest.mark.parametrize("n,k,m", PER_CU_CASES)
+def test_one_group_per_cu(hip, n, k, m):
+    """N = r * 256 rows (r = 4 .. 14): one 8-wave group of r rows per CU, the
+    planner's own choice at one activation row (the drop-in's stacked k/v
+    heads, TP = 8's gate/up share) and at two to four up to r = 12, with
+    lanes past K (k = 4000, 3000, 2056).  Edge data within the parity rule
+    and, row by row, the bound; the zero rule's patterns bit for bit the
+    reference."""
     r = n // 256
-    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.grid_x) == (8, r if r <= 8 else r // 2, r, 256), p
-    x, w = case(1, k, n, seed=7800 + n + k, edge=True)
+    p = hip.plan("rd", m, k, n, x_addr=256, w_addr=256)
+    assert (p.waves, p.rows_or_rw, p.rows_per_group, p.mt, p.grid_x) == (8, r if r <= 8 else r // 2, r, m, 256), p
+    x, w = case(m, k, n, seed=7800 + n + k + m, edge=True)
     y = _rd_dev(hip, x, w)
     assert np.array_equal(y.view(np.uint32), _rd_dev(hip, x, w).view(np.uint32))
-    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"group per CU n={n} k={k}")
+    check_or_bound(y, ref(x, w), x, W.bf16_to_f32(w), what=f"group per CU m={m} n={n} k={k}")
     xm, wz = zero_rows(k, 9)
     wz = np.ascontiguousarray(wz[np.arange(n) % 9])
-    for row in range(4):
-        xr = np.ascontiguousarray(xm[row:row + 1])
+    xm = np.ascontiguousarray(xm[(np.arange(m) + (m - 1)) % 4]) if m > 1 else None
+    for row in range(4) if m == 1 else [None]:
+        xr = np.ascontiguousarray(xm if m > 1 else zero_rows(k, 9)[0][row:row + 1])
         y_ref = ref(xr, wz)
         y = _rd_dev(hip, xr, wz)
         assert np.array_equal(y.view(np.uint32), y_ref.view(np.uint32)), \
