@@ -967,6 +967,13 @@ gemv_rd_stream_x4_kernel(const uint16_t *__restrict__ W, const float *__restrict
     rd_group_body<uint16_t, 1, MT, 4>(W, X, Y, N, K, ys_act, ys_row);
 }
 
+template <int MT>
+__global__ void __launch_bounds__(512)
+gemv_rd_stream_x8f_kernel(const float *__restrict__ W, const float *__restrict__ X, float *__restrict__ Y, int N,
+                          int K, int64_t ys_act, int64_t ys_row) {
+    rd_group_body<float, 2, MT, 8>(W, X, Y, N, K, ys_act, ys_row);
+}
+
 // One 8-wave group per CU: RPW rows per workgroup (N = RPW * CUs), ROWS per
 // register buffer, MT activation rows.
 template <int RPW, int ROWS, int MT = 1>
@@ -4204,6 +4211,29 @@ F32Plan plan_f32(const F32Problem &p, int num_cus) {
             return pl;
         }
     }
+    // One group of 8 waves for 2048 < K <= 4096 (two windows of 4 weights per
+    // lane, x in registers, zeros settled after the stream): at 3 or 4
+    // activation rows, and where the 8-wave streaming kernel's last window
+    // would be partly empty (K not a multiple of 2048).  Same box, group /
+    // streaming, us: W[14336,4096] m = 3 / 4 38.4 / 38.5 against 42.2 / 43.0,
+    // [4096,4096] 12.0 / 12.2 against 14.5 / 14.9, [1792,4096] 8.8 / 9.0
+    // against 9.7 / 10.0; [8192,3072] m = 1 / 2 / 3 / 4 16.1 / 16.3 / 17.2 /
+    // 17.4 against 17.0 / 19.2 / 23.1 / 23.3; at K = 4096 and one or two rows
+    // the streaming kernel wins ([14336,4096] 35.9 / 37.3 against 38.8 /
+    // 40.3).  DMC_HIP_F32_X8: 0 never, 2 wherever it applies.
+    const int xf8 = env_int("DMC_HIP_F32_X8", 1);
+    if (xf8 != 0 && p.m >= 1 && p.m <= kX14MaxM && p.k > 2048 && p.k <= 4096 && p.k % 4 == 0 && p.ldw == p.k &&
+        p.ldx == p.k && aligned(p.w, 16) && aligned(p.x, 16) &&
+        (xf8 == 2 || p.m >= 3 || p.k % 2048 != 0) && env_int("DMC_HIP_F32_STREAM", 1) != 0) {
+        pl.waves = 8;
+        pl.kvec = 2;
+        pl.rows = p.m <= 2 ? 2 : 1;
+        pl.mt = (int)p.m;
+        pl.rpw = 16;
+        pl.grid_x = (p.n + 15) / 16;
+        pl.grid_y = 1;
+        return pl;
+    }
     // Streaming: 16-byte rows, x rows alike, K within 8 vectors of 4 per lane
     // over 8 waves.  Waves as for bf16 by bytes per row (1 KiB per wave per
     // vector); activation rows per workgroup within the register budget; rows
@@ -4281,6 +4311,22 @@ hipError_t launch_f32(const F32Problem &p, const F32Plan &pl, hipStream_t s) {
     if (p.k < 0 || p.m > INT32_MAX || p.n > INT32_MAX || p.k > INT32_MAX || pl.grid_x < 1 || pl.grid_y < 1 ||
         pl.grid_y > 65535 || pl.grid_x > INT32_MAX || pl.grid_x * pl.rpw < p.n || pl.grid_y * pl.mt < p.m)
         return hipErrorInvalidValue;
+    if (pl.kvec == 2 && pl.waves == 8 && pl.rpw == 16) {
+        if (pl.mt != p.m || p.m < 1 || p.m > kX14MaxM || p.k > 4096 || p.k < 1 || p.k % 4 != 0 || p.ldw != p.k ||
+            p.ldx != p.k || !aligned(p.w, 16) || !aligned(p.x, 16) || pl.grid_x != (p.n + 15) / 16 || pl.grid_y != 1)
+            return hipErrorInvalidValue;
+#define DMC_F32X8(MT)                                                                                        \
+    hipLaunchKernelGGL((gemv_rd_stream_x8f_kernel<MT>), dim3((unsigned)pl.grid_x), dim3(512), 0, s, p.w, p.x, \
+                       p.y, (int)p.n, (int)p.k, p.ys_act, p.ys_row)
+        switch ((int)p.m) {
+        case 1: DMC_F32X8(1); break;
+        case 2: DMC_F32X8(2); break;
+        case 3: DMC_F32X8(3); break;
+        default: DMC_F32X8(4); break;
+        }
+#undef DMC_F32X8
+        return hipGetLastError();
+    }
     if (pl.kvec > 0 && pl.waves == kX14Waves) {
         // The 14-wave kernel: 16 rows per workgroup, x straight into registers.
         if (pl.rpw != 16 || pl.mt != p.m || p.m < 1 || p.m > kX14MaxM || pl.kvec < 2 || pl.kvec > 4 ||

@@ -666,6 +666,17 @@ def test_f32_general_kernel_for_odd_k_misaligned_or_long_rows(k, x_addr, w_addr)
 
 def test_f32_activation_rows_per_workgroup(monkeypatch):
     assert d.plan_f32(4, 4096, 4096, x_addr=256, w_addr=256).mt == 4      # kvec 2: up to 4
+    # 2048 < K <= 4096: the 8-wave group (16 rows, two windows per lane) at 3 and 4 rows, and
+    # where K is not a multiple of 2048; the streaming kernel (4 rows per workgroup) otherwise
+    for m, k, group in ((3, 4096, True), (4, 4096, True), (1, 4096, False), (2, 4096, False), (1, 3072, True),
+                        (2, 2560, True), (4, 2048, False)):
+        p = d.plan_f32(m, k, 4096, x_addr=256, w_addr=256)
+        assert (p.waves == 8 and p.rows_per_group == 16) == group, (m, k, p)
+        if group:
+            assert (p.kvec, p.mt, p.grid_x, p.grid_y) == (2, m, 256, 1), p
+    monkeypatch.setenv("DMC_HIP_F32_X8", "0")
+    assert d.plan_f32(4, 4096, 4096, x_addr=256, w_addr=256).rows_per_group == 4
+    monkeypatch.delenv("DMC_HIP_F32_X8")
     assert d.plan_f32(16, 4096, 4096, x_addr=256, w_addr=256).grid_y == 4
     # long rows that the 8-wave kernel would take one activation row per pass
     # (kvec 7 at K = 14336): the 14-wave kernel, every activation row in one

@@ -230,6 +230,70 @@ def test_fourteen_waves_f32(hip, n, k, m, monkeypatch):
           what=f"f32 x14 W@x m={m} n={n} k={k}")
 
 
+X8_F32 = [(14336, 4096), (4097, 4096), (1030, 3000), (6, 2052), (300, 4096), (1792, 3072)]
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", X8_F32)
+def test_eight_wave_group_f32(hip, n, k, m, monkeypatch):
+    """The f32 weights' 8-wave group (2048 < K <= 4096, two windows of 4
+    weights per lane; the default at 3 and 4 activation rows and where K is
+    not a multiple of 2048, DMC_HIP_F32_X8=2 here): a partial last workgroup
+    (n = 4097), lanes past K (k = 3000, 2052), fewer rows than one workgroup
+    (n = 6), edge values; through the device-pointer entry and the drop-in's
+    W @ x; two launches bit for bit alike."""
+    monkeypatch.setenv("DMC_HIP_F32_X8", "2")
+    rng = np.random.default_rng(3 * n + k + m)
+    x = edge(rng.standard_normal((m, k)).astype(np.float32), rng)
+    w = edge(rng.standard_normal((n, k)).astype(np.float32), rng)
+    y_ref = oracle.matmul_f32(x, np.ascontiguousarray(w.T))
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        pl = hip.plan_f32(m, k, n, x_addr=dx.addr, w_addr=dw.addr)
+        assert (pl.waves, pl.kvec, pl.mt, pl.rows_per_group, pl.grid_x) == (8, 2, m, 16, -(-n // 16)), pl
+        ys = []
+        for _ in range(2):
+            hip.gemv_f32_rd(dx, dw, dy, m, k, n)
+            hip.synchronize()
+            ys.append(dy.download(np.float32, (m, n)))
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+    check(ys[0], y_ref, what=f"f32 x8 device m={m} n={n} k={k}")
+    check(hip.matmul_f32_gpu(w, np.ascontiguousarray(x.T)), np.ascontiguousarray(y_ref.T),
+          what=f"f32 x8 W@x m={m} n={n} k={k}")
+
+
+@pytest.mark.parametrize("m", [3, 4])
+def test_eight_wave_group_f32_zero_rule(hip, m):
+    """Exact zeros on the f32 8-wave group at its default shapes (K = 4096,
+    3 or 4 activation rows): the patterns of the 14-wave test, bit for bit
+    the reference."""
+    k, n = 4096, 4096
+    x = np.full((m, k), np.float32(1e-30), np.float32)
+    x[1::2] = np.float32(0.5)
+    w = np.full((n, k), np.float32(1e-30), np.float32)
+    w[1::6] = -w[1::6]
+    w[2::6, k - 1] = -w[2::6, k - 1]
+    w[3::6] = 0
+    h = k // 2
+    w[4::6, :h] = 1.0
+    w[4::6, h:] = -1.0
+    w[5::6, ::2] = -w[5::6, ::2]
+    pl = hip.plan_f32(m, k, n, x_addr=256, w_addr=256)
+    assert (pl.waves, pl.rows_per_group) == (8, 16), pl
+    with hip.DeviceBuffer.from_numpy(x) as dx, hip.DeviceBuffer.from_numpy(w) as dw, \
+            hip.DeviceBuffer(4 * m * n) as dy:
+        hip.gemv_f32_rd(dx, dw, dy, m, k, n)
+        hip.synchronize()
+        y = dy.download(np.float32, (m, n))
+    rows = np.r_[0:12, n - 12:n]
+    y_ref = oracle.matmul_f32(x, np.ascontiguousarray(w[rows].T))
+    z = y_ref == 0
+    assert np.any(z)
+    assert np.array_equal(y[:, rows][z].view(np.uint32), y_ref[z].view(np.uint32)), (y[:, rows], y_ref)
+    for r in range(m):
+        check_bound(y[r, rows], y_ref[r], x[r], w[rows], what=f"f32 x8 zero rule m={m} row {r}")
+
+
 @pytest.mark.parametrize("m", [2, 4])
 def test_fourteen_waves_f32_zero_rule(hip, m, monkeypatch):
     """Exact zeros on the f32 14-wave kernel (the default at K = 14336 and
